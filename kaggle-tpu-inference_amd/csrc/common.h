@@ -1,0 +1,170 @@
+// Shared device helpers for the gfx950 kernels of libg4mi.
+//
+// bf16 values travel as raw uint16_t (the upper half of an IEEE f32).  All
+// arithmetic happens in f32 (or f64 where a result must be independent of the
+// reduction order) and is rounded back to bf16 round-to-nearest-even at the
+// points where the JAX reference materialises a bf16 tensor.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace g4mi {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// ------------------------------------------------------------------ bf16 <-> f32
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
+
+// f32 -> bf16, round to nearest even (NaN stays NaN).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+// Round an f32 to the nearest bf16 and return it as f32.
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+// 8 bf16 in a 16-byte vector -> 8 f32.
+__device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
+  f[0] = bf_lo(v.x); f[1] = bf_hi(v.x);
+  f[2] = bf_lo(v.y); f[3] = bf_hi(v.y);
+  f[4] = bf_lo(v.z); f[5] = bf_hi(v.z);
+  f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
+}
+
+// f32 dot of 8 bf16 pairs, accumulated into acc in element order.
+__device__ __forceinline__ float dot8(const u32x4 a, const u32x4 b, float acc) {
+  acc = fmaf(bf_lo(a.x), bf_lo(b.x), acc); acc = fmaf(bf_hi(a.x), bf_hi(b.x), acc);
+  acc = fmaf(bf_lo(a.y), bf_lo(b.y), acc); acc = fmaf(bf_hi(a.y), bf_hi(b.y), acc);
+  acc = fmaf(bf_lo(a.z), bf_lo(b.z), acc); acc = fmaf(bf_hi(a.z), bf_hi(b.z), acc);
+  acc = fmaf(bf_lo(a.w), bf_lo(b.w), acc); acc = fmaf(bf_hi(a.w), bf_hi(b.w), acc);
+  return acc;
+}
+
+// f64 dot of 8 bf16 pairs.  Every bf16*bf16 product is exact in f64 and, for
+// operands within ~2^37 of each other in magnitude, so is every partial sum:
+// the result does not depend on the order in which lanes are combined.
+__device__ __forceinline__ double dot8_f64(const u32x4 a, const u32x4 b, double acc) {
+  acc = fma((double)bf_lo(a.x), (double)bf_lo(b.x), acc); acc = fma((double)bf_hi(a.x), (double)bf_hi(b.x), acc);
+  acc = fma((double)bf_lo(a.y), (double)bf_lo(b.y), acc); acc = fma((double)bf_hi(a.y), (double)bf_hi(b.y), acc);
+  acc = fma((double)bf_lo(a.z), (double)bf_lo(b.z), acc); acc = fma((double)bf_hi(a.z), (double)bf_hi(b.z), acc);
+  acc = fma((double)bf_lo(a.w), (double)bf_lo(b.w), acc); acc = fma((double)bf_hi(a.w), (double)bf_hi(b.w), acc);
+  return acc;
+}
+
+__device__ __forceinline__ double sumsq8_f64(const u32x4 a, double acc) {
+  float f[8];
+  unpack8(a, f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc = fma((double)f[i], (double)f[i], acc);
+  return acc;
+}
+
+// ------------------------------------------------------------------ loads
+// Weights are streamed once per token: mark them non-temporal so they do not
+// evict the activations and KV pages that are re-read.
+__device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
+
+// ------------------------------------------------------------------ reductions
+// Butterfly sum over groups of W consecutive lanes (W a power of two <= 64).
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ double group_sum_f64(double v) {
+#pragma unroll
+  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  return v;
+}
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int m = W / 2; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m, kWave));
+  return v;
+}
+
+// Block-wide f64 sum (exact inputs => order-independent result).  `red` must
+// hold blockDim.x/64 doubles of LDS.  All threads receive the total.
+__device__ __forceinline__ double block_sum_f64(double v, double* red) {
+  v = group_sum_f64<kWave>(v);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  double t = 0.0;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// ------------------------------------------------------------------ RMSNorm
+// The RMSNorm scale of the reference (model.py rms_norm): x * rsqrt(mean(x^2)+eps)
+// with mean/eps in f32.  The sum of squares is exact (f64) and the reciprocal
+// square root is taken in f64 and rounded once, so the CPU oracle and every
+// wave that recomputes it agree bit for bit.
+__device__ __forceinline__ float rms_scale(double sumsq, int n, float eps) {
+  float mean = (float)sumsq / (float)n;
+  float a = mean + eps;
+  return (float)(1.0 / sqrt((double)a));
+}
+
+// out = bf16(x * r * w) elementwise on 8 packed bf16 (w may be null: weight 1).
+__device__ __forceinline__ u32x4 scale8(const u32x4 x, float r, const u32x4* w) {
+  float f[8];
+  unpack8(x, f);
+  if (w != nullptr) {
+    float g[8];
+    unpack8(*w, g);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = f[i] * r * g[i];
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) f[i] = f[i] * r;
+  }
+  u32x4 o;
+  o.x = pack2(f[0], f[1]); o.y = pack2(f[2], f[3]); o.z = pack2(f[4], f[5]); o.w = pack2(f[6], f[7]);
+  return o;
+}
+
+// ------------------------------------------------------------------ activations
+__device__ __forceinline__ float gelu_tanh(float x) {
+  const float k0 = 0.7978845608028654f;  // sqrt(2/pi)
+  const float x3 = x * x * x;
+  const float cdf = 0.5f * (1.0f + tanhf(k0 * (x + 0.044715f * x3)));
+  return x * cdf;
+}
+
+// ------------------------------------------------------------------ last-block
+// Returns true in every thread of the block that arrives last at `counter`
+// (device-scope), after making the block's prior global writes visible.  The
+// last block resets the counter so the next launch (or graph replay) starts
+// from zero.
+__device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int total, int* flag_lds) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned int prev = atomicAdd(counter, 1u);
+    int last = (prev == total - 1);
+    if (last) atomicExch(counter, 0u);
+    *flag_lds = last;
+  }
+  __syncthreads();
+  const bool last = *flag_lds != 0;
+  if (last) __threadfence();
+  return last;
+}
+
+}  // namespace g4mi

@@ -1,0 +1,188 @@
+"""GPU parity of the MoE decode block (router/top-k, expert GEMVs, combine)
+against the CPU oracle, on the isolated-block workload (hidden 2816, 128
+experts top-8, width 704, seed 1, batches 1/4/8) and on the tiny model's
+shapes.  Also checks the device weight generator bit for bit against its
+numpy restatement.
+
+Tolerances: top-k indices bit-exact; top-k weights within 2 f32 ulps (the
+recipes are identical, so they are expected bit-exact); expert outputs (bf16)
+corr >= 0.9999 with every element within 2^-7 of the output's max magnitude
+and >= 98% of elements bit-identical (the GPU accumulates the GEMVs in f32,
+the oracle in f64: rare one-ulp flips of bf16 roundings are expected).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gemma4_mi import ops
+from gemma4_mi.config import tiny_parity_config
+from oracle import philox, twin
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+class _C2Cfg:
+    hidden_size = 2816
+    num_experts = 128
+    top_k_experts = 8
+    moe_intermediate_size = 704
+    rms_norm_eps = 1e-6
+
+
+def _gen(shape, seed, name, std, device=DEV):
+    t = torch.empty(shape, dtype=torch.bfloat16, device=device)
+    ops.fill_normal_(t, philox.tensor_key(seed, name), std)
+    return t
+
+
+@pytest.fixture(scope="module")
+def c2():
+    cfg = _C2Cfg()
+    h, e, f = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
+    g = {
+        "router.proj": _gen((e, h), 1, "router.proj", 0.02),
+        "router.scale": torch.ones(h, dtype=torch.bfloat16, device=DEV),
+        "router.per_expert_scale": torch.ones(e, dtype=torch.bfloat16, device=DEV),
+        "experts.gate_up_proj": _gen((e, 2, f, h), 1, "experts.gate_up_proj", 0.02),
+        "experts.down_proj": _gen((e, h, f), 1, "experts.down_proj", 0.02),
+    }
+    torch.cuda.synchronize()
+    cpu = {k: v.cpu() for k, v in g.items()}
+    return cfg, g, cpu
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu().numpy()
+
+
+def test_fill_normal_matches_numpy_generator():
+    n = 3_000_001
+    key = philox.tensor_key(7, "probe.tensor")
+    t = torch.empty(n + 1, dtype=torch.bfloat16, device=DEV)
+    ops.fill_normal_(t[:n], key, 0.02)
+    got = _bits(t[:n]).view(np.uint16)
+    exp = philox.normal_bf16_bits(n, key, 0.02)
+    assert np.array_equal(got, exp), f"{np.sum(got != exp)} of {n} elements differ"
+
+
+def test_philox_known_answers():
+    # Random123 kat_vectors, philox4x32 with 10 rounds
+    cases = [
+        ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+        ((0xFFFFFFFF,) * 4, (0xFFFFFFFF, 0xFFFFFFFF), (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+        ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+         (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+    ]
+    for ctr, key, want in cases:
+        c = torch.tensor(np.array(ctr, np.uint32).view(np.int32), device=DEV)
+        out = ops.philox4x32_10(c, key[0] | (key[1] << 32)).cpu().numpy().view(np.uint32)
+        assert tuple(int(v) for v in out) == want
+
+
+def _check_out(got, exp, what):
+    g = got.float().cpu().numpy().ravel()
+    e = exp.float().numpy().ravel()
+    scale = float(np.abs(e).max())
+    err = np.abs(g - e)
+    corr = np.corrcoef(g, e)[0, 1]
+    same = np.mean(_bits(got).ravel() == exp.contiguous().view(torch.int16).numpy().ravel())
+    print(f"{what}: max|d|={err.max():.3e} (scale {scale:.3e}) corr={corr:.7f} bit-identical={same:.4f}")
+    assert corr >= 0.9999, what
+    assert err.max() <= scale * 2.0**-7, what
+    assert same >= 0.98, what
+
+
+@pytest.mark.parametrize("n", [1, 4, 8])
+def test_router_topk_bit_exact_c2(c2, n):
+    cfg, g, cpu = c2
+    x = _gen((n, cfg.hidden_size), 1, f"x.n{n}", 1.0)
+    tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                 cfg.top_k_experts, cfg.rms_norm_eps)
+    torch.cuda.synchronize()
+    ew, ei = twin.router(cfg, cpu, x.cpu())
+    assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32))
+    np.testing.assert_allclose(tw.cpu().numpy(), ew.numpy(), rtol=2.5e-7, atol=0)
+
+
+@pytest.mark.parametrize("n", [1, 4, 8])
+def test_experts_decode_c2(c2, n):
+    cfg, g, cpu = c2
+    x = _gen((n, cfg.hidden_size), 1, f"x.n{n}", 1.0)
+    tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                 cfg.top_k_experts, cfg.rms_norm_eps)
+    out = ops.moe_experts(x, g["experts.gate_up_proj"], g["experts.down_proj"], tw, ti)
+    torch.cuda.synchronize()
+    exp = twin.moe(cfg, cpu, x.cpu(), dense=False)
+    _check_out(out, exp, f"experts decode n={n}")
+
+
+def _dense_selected(cfg, lp, x):
+    """Dense-MoE semantics (model.py:241-250) restricted to the selected experts
+    (the others carry an exact zero weight)."""
+    tw, ti = twin.router(cfg, lp, x)
+    outs = []
+    for n in range(x.shape[0]):
+        acc = torch.zeros(cfg.hidden_size, dtype=torch.float64)
+        for kk in range(cfg.top_k_experts):
+            e = int(ti[n, kk])
+            gu = twin.ein("h,cfh->cf", x[n], lp["experts.gate_up_proj"][e])
+            a = twin.rb(twin.f32(twin.gelu(gu[0])) * twin.f32(gu[1]))
+            a = twin.rb(twin.f32(a) * twin.f32(twin.rb(tw[n, kk])))
+            acc += torch.einsum("f,hf->h", a.double(), lp["experts.down_proj"][e].double())
+        outs.append(twin.rb(acc))
+    return torch.stack(outs, 0)
+
+
+def test_experts_f32_combine_c2(c2):
+    cfg, g, cpu = c2
+    x = _gen((4, cfg.hidden_size), 1, "x.dense", 1.0)
+    tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                 cfg.top_k_experts, cfg.rms_norm_eps)
+    out = ops.moe_experts(x, g["experts.gate_up_proj"], g["experts.down_proj"], tw, ti, combine="f32")
+    torch.cuda.synchronize()
+    _check_out(out, _dense_selected(cfg, cpu, x.cpu()), "experts f32 combine")
+
+
+def test_moe_tiny_model_layers():
+    """Tiny-model shapes (hidden 256, 16 experts top-4, width 128) with random
+    router scales, routed from the residual with the fused pre-norm."""
+    cfg = tiny_parity_config()
+    params = twin.random_params(cfg, 0)
+    for i in range(cfg.num_hidden_layers):
+        lp = twin.layer_params(params, i)
+        gl = {k: v.to(DEV) for k, v in lp.items()}
+        resid = _gen((16, cfg.hidden_size), 5, f"resid.{i}", 1.0)
+        tw, ti = ops.moe_router_topk(resid, gl["router.scale"], gl["router.proj"], gl["router.per_expert_scale"],
+                                     cfg.top_k_experts, cfg.rms_norm_eps,
+                                     pre_norm_w=gl["pre_feedforward_layernorm_2"])
+        flat = twin.rms_norm(resid.cpu(), lp["pre_feedforward_layernorm_2"], cfg.rms_norm_eps)
+        ew, ei = twin.router(cfg, lp, flat)
+        assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32)), f"layer {i}"
+        np.testing.assert_allclose(tw.cpu().numpy(), ew.numpy(), rtol=2.5e-7, atol=0)
+        out = ops.moe_experts(flat.to(DEV), gl["experts.gate_up_proj"], gl["experts.down_proj"], tw, ti)
+        _check_out(out, twin.moe(cfg, lp, flat, dense=False), f"tiny layer {i}")
+
+
+def test_router_rejects_bad_arguments(c2):
+    cfg, g, _ = c2
+    x = torch.zeros((1, cfg.hidden_size), dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(Exception):
+        ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"], 0, 1e-6)
+    with pytest.raises(Exception):
+        ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"], 200, 1e-6)
+
+
+def test_router_workspace_reuse_across_batch_sizes(c2):
+    """A workspace grown for a large batch stays valid for a smaller one (the
+    completion counter sits at a fixed offset, not after the score array)."""
+    cfg, g, cpu = c2
+    for n in (8, 1, 4, 1):
+        x = _gen((n, cfg.hidden_size), 1, f"x.reuse{n}", 1.0)
+        tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                     cfg.top_k_experts, cfg.rms_norm_eps)
+        torch.cuda.synchronize()
+        _, ei = twin.router(cfg, cpu, x.cpu())
+        assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32)), n
