@@ -12,8 +12,11 @@ Prints ONE JSON line (rank 0, N=1):
 Workloads (--workload):
   moe_block  the isolated MoE decode block: hidden 2816, router 2816x128,
              128 experts top-8 of width 704, bf16, seed 1, batch --batch
-             (1, 4 or 8); the hidden state of each step is drawn from a bank of
-             1024 N(0,1) vectors so the routed experts change every step.
+             (1, 4 or 8).  One HIP graph holds up to 64 consecutive steps, each
+             on its own N(0,1) hidden state, so the routed experts change every
+             step (the 1.5 GB expert table is 6x the 256 MB Infinity Cache).
+  copy       a 1 GiB device-to-device copy of known size: the calibration run
+             for the HBM byte counters (FETCH_SIZE / WRITE_SIZE).
 """
 
 from __future__ import annotations
@@ -48,13 +51,52 @@ def _cpu_name() -> str:
     return platform.processor() or "unknown"
 
 
+# ------------------------------------------------------------------ helpers
+def _chunk(steps: int, cap: int = 64) -> int:
+    """Largest divisor of `steps` that is <= cap (steps per captured graph)."""
+    for g in range(min(cap, steps), 0, -1):
+        if steps % g == 0:
+            return g
+    return 1
+
+
+def _capture(fn):
+    """Captures fn() (a sequence of launches on the current stream) in a HIP graph."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()  # warm: first-call allocations happen outside the capture
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def _time_graph(g, replays: int) -> float:
+    """ms for `replays` replays, bracketed by HIP events on the replay stream."""
+    import torch
+
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b)
+
+
 # ------------------------------------------------------------------ moe block
 class MoeBlock:
     H, E, K, F = 2816, 128, 8, 704
     SEED = 1
-    BANK = 1024
 
-    def __init__(self, batch: int):
+    def __init__(self, batch: int, bank: int):
         import torch
 
         from gemma4_mi import ops
@@ -62,8 +104,9 @@ class MoeBlock:
 
         self.torch, self.ops = torch, ops
         self.n = batch
+        self.nbank = bank
         dev = "cuda:0"
-        H, E, F = self.H, self.E, self.F
+        H, E, F, K = self.H, self.E, self.F, self.K
 
         def gen(shape, name, std):
             t = torch.empty(shape, dtype=torch.bfloat16, device=dev)
@@ -75,42 +118,33 @@ class MoeBlock:
         self.pes = torch.ones(E, dtype=torch.bfloat16, device=dev)
         self.gate_up = gen((E, 2, F, H), "experts.gate_up_proj", 0.02)
         self.down = gen((E, H, F), "experts.down_proj", 0.02)
-        self.bank = gen((self.BANK, batch, H), f"x.bank.n{batch}", 1.0)
-        self.top_w = torch.empty((batch, self.K), dtype=torch.float32, device=dev)
-        self.top_i = torch.empty((batch, self.K), dtype=torch.int32, device=dev)
-        self.act = torch.empty((batch, self.K, F), dtype=torch.bfloat16, device=dev)
-        self.out = torch.empty((batch, H), dtype=torch.bfloat16, device=dev)
-        self.experts_seen = 0
+        self.bank = gen((bank, batch, H), f"x.bank.n{batch}", 1.0)
+        self.out = torch.empty((bank, batch, H), dtype=torch.bfloat16, device=dev)
+        self.tw = torch.empty((bank, batch, K), dtype=torch.float32, device=dev)
+        self.ti = torch.empty((bank, batch, K), dtype=torch.int32, device=dev)
+        self.scores = torch.empty((bank, batch, E), dtype=torch.float32, device=dev)
+        self.act = torch.empty((bank, batch, K, F), dtype=torch.bfloat16, device=dev)
         torch.cuda.synchronize()
 
-    def step(self, i: int, ev=None):
-        ops = self.ops
-        x = self.bank[i % self.BANK]
-        ops.moe_router_topk(x, self.scale, self.proj, self.pes, self.K, 1e-6, out=(self.top_w, self.top_i))
-        if ev is not None:
-            ev[0].record()
-        ops.moe_gateup(x, self.gate_up, self.top_w, self.top_i, act=self.act)
-        if ev is not None:
-            ev[1].record()
-        ops.moe_down(self.act, self.down, self.top_i, out=self.out)
+    def block(self, i: int):
+        self.ops.moe_block(self.bank[i], self.scale, self.proj, self.pes, self.gate_up, self.down, self.K, 1e-6,
+                           out=self.out[i], route=(self.tw[i], self.ti[i]))
 
-    def unique_experts(self, steps: int) -> float:
-        """Mean |union of routed experts| per step over the bank (for bytes)."""
+    def gateup(self, i: int):
+        self.ops.moe_gateup_routed(self.bank[i], self.scores[i], self.pes, self.gate_up, self.K, act=self.act[i],
+                                   route=(self.tw[i], self.ti[i]))
+
+    def bytes_per_step(self, steps: int) -> tuple[float, float]:
+        """(mean algorithmic bytes per step, mean |union of experts|) over the bank."""
         torch = self.torch
-        tot = 0
-        m = min(steps, self.BANK)
-        for i in range(m):
-            self.ops.moe_router_topk(self.bank[i], self.scale, self.proj, self.pes, self.K, 1e-6,
-                                     out=(self.top_w, self.top_i))
-            tot += int(torch.unique(self.top_i).numel())
-        return tot / m
-
-    def bytes_per_step(self, uniq: float) -> float:
-        return self.E * self.H * 2 + uniq * 3 * self.F * self.H * 2
+        uniq = [int(torch.unique(self.ti[i]).numel()) for i in range(min(steps, self.nbank))]
+        u = sum(uniq) / len(uniq)
+        return self.E * self.H * 2 + u * 3 * self.F * self.H * 2 + 2 * self.n * self.H * 2, u
 
     def gateup_bytes(self) -> float:
-        # weights of the selected (token, slot) rows + x + act written
-        return self.n * self.K * 2 * self.F * self.H * 2 + self.n * self.H * 2 + self.n * self.K * self.F * 2
+        # selected rows of gate_up + x + scores read + act written
+        n, K, F, H, E = self.n, self.K, self.F, self.H, self.E
+        return n * K * 2 * F * H * 2 + n * H * 2 + n * E * 4 + n * K * F * 2
 
     def cpu_baseline(self, budget_s: float) -> dict:
         torch = self.torch
@@ -131,7 +165,7 @@ class MoeBlock:
         twin.moe(C, lp, bank[0], dense=False, precise=False)  # warm-up
         done, t0 = 0, time.perf_counter()
         while True:
-            twin.moe(C, lp, bank[done % self.BANK], dense=False, precise=False)
+            twin.moe(C, lp, bank[done % self.nbank], dense=False, precise=False)
             done += 1
             el = time.perf_counter() - t0
             if el >= budget_s and done >= 3:
@@ -144,27 +178,21 @@ class MoeBlock:
 
 
 def run_moe_block(args) -> dict:
-    import torch
-
-    wl = MoeBlock(args.batch)
-    _log(f"moe_block batch={args.batch}: weights ready")
-    for i in range(args.warmup):
-        wl.step(i)
-    torch.cuda.synchronize()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(args.steps)]
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        wl.step(args.warmup + i, evs[i])
-    stop.record()
-    torch.cuda.synchronize()
-    total_ms = start.elapsed_time(stop)
-    gu_ms = sum(a.elapsed_time(b) for a, b in evs) / args.steps
-    uniq = wl.unique_experts(args.steps)
-    bps = wl.bytes_per_step(uniq)
+    G = _chunk(args.steps)
+    wl = MoeBlock(args.batch, G)
+    _log(f"moe_block batch={args.batch}: weights ready; {G} steps per graph")
+    g_block = _capture(lambda: [wl.block(i) for i in range(G)])
+    _time_graph(g_block, max(1, args.warmup // G))
+    total_ms = _time_graph(g_block, args.steps // G)
     ms = total_ms / args.steps
-    achieved = wl.gateup_bytes() / (gu_ms * 1e-3) / 1e9
+    bps, uniq = wl.bytes_per_step(G)
+    # dominant kernel: the routed gate/up, G launches per graph on the same inputs
+    for i in range(G):
+        wl.ops.moe_router_scores(wl.bank[i], wl.scale, wl.proj, 1e-6, out=wl.scores[i])
+    g_gu = _capture(lambda: [wl.gateup(i) for i in range(G)])
+    _time_graph(g_gu, 2)
+    gu_us = _time_graph(g_gu, max(1, args.steps // G)) / (max(1, args.steps // G) * G) * 1e3
+    achieved = wl.gateup_bytes() / (gu_us * 1e-6) / 1e9
     res = {
         "metric": METRIC,
         "value": args.batch / (ms * 1e-3),
@@ -173,15 +201,16 @@ def run_moe_block(args) -> dict:
         "dtype": "bf16",
         "config": {
             "workload": "moe_decode_block", "hidden": wl.H, "experts": wl.E, "top_k": wl.K,
-            "moe_intermediate": wl.F, "batch": args.batch, "seed": wl.SEED,
+            "moe_intermediate": wl.F, "batch": args.batch, "seed": wl.SEED, "inputs_rotated": G,
             "bytes_per_step": bps, "mean_unique_experts": uniq,
             "block_hbm_gbs": bps / (ms * 1e-3) / 1e9,
             "block_frac_of_peak": bps / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "kernels_per_step": 3, "launch": "HIP graph",
         },
         "roofline": {
-            "kernel": "moe_gateup_kernel", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+            "kernel": "moe_gateup_kernel (routed)", "bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
             "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS, "traffic": None,
-            "bytes_per_launch": wl.gateup_bytes(), "avg_launch_us": gu_ms * 1e3,
+            "bytes_per_launch": wl.gateup_bytes(), "avg_launch_us": gu_us,
         },
     }
     if not args.no_cpu_baseline:
@@ -189,7 +218,32 @@ def run_moe_block(args) -> dict:
     return res
 
 
-WORKLOADS = {"moe_block": run_moe_block}
+def run_copy(args) -> dict:
+    import torch
+
+    n = 1 << 30
+    a = torch.empty(n, dtype=torch.uint8, device="cuda:0")
+    b = torch.empty_like(a)
+    for _ in range(args.warmup):
+        b.copy_(a)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(args.steps):
+        b.copy_(a)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    gbs = 2 * n / (ms * 1e-3) / 1e9
+    return {
+        "metric": "device copy GB/s (read + write)", "value": gbs, "unit": "GB/s", "ms_per_step": ms,
+        "dtype": "u8", "config": {"workload": "copy_1GiB", "bytes_read": n, "bytes_written": n},
+        "roofline": {"kernel": "copy", "bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
+WORKLOADS = {"moe_block": run_moe_block, "copy": run_copy}
 
 
 def main() -> int:

@@ -40,6 +40,12 @@ extern "C" {
 int g4mi_version(void);
 const char* g4mi_last_error_string(void);
 
+/* Diagnostics (no counterpart in the reference): per-lane group sums over
+ * aligned groups of 2..64 lanes of `waves` wave64s, in f32 and f64, written as
+ * out[(w*6 + j)*64 + lane] for group width 2^(j+1).  Lets a test pin the lane
+ * layout of the cross-lane reductions every kernel uses. */
+int g4mi_selftest_lane_reductions(const float* in, float* out, double* out_d, int32_t waves, void* stream);
+
 /* ---------------------------------------------------------------- init
  * Fills out[0:n) with bf16(std * z), z ~ N(0,1) from Philox4x32-10 keyed by
  * `key` (element i uses counter i/2) and a Box-Muller transform in f64.
@@ -52,39 +58,62 @@ int g4mi_fill_normal_bf16(uint16_t* out, int64_t n, uint64_t key, double stdv, v
 int g4mi_philox4x32_10(const uint32_t* ctr, uint64_t key, uint32_t* out, int64_t nblocks, void* stream);
 
 /* ---------------------------------------------------------------- MoE (K1-K3)
- * Router + top-k: model.py:224-232 (_router), fused with the
+ * Router scores: model.py:225-227 (_router up to the f32 cast), fused with the
  * pre_feedforward_layernorm_2 RMSNorm of model.py:315 when pre_norm_w != NULL.
- *   x [N,H] bf16 (residual if pre_norm_w given, else already normalised)
- *   router_scale [H], router_proj [E,H], per_expert_scale [E] bf16
- *   out_w [N,k] f32, out_i [N,k] int32, both in descending-probability order,
- *   ties to the lower expert index (jax.lax.top_k).
- * x and router_proj 16-byte aligned; H % 8 == 0, H <= 16384, E <= 256, k <= 32. */
+ *   x [N,H] bf16 (residual if pre_norm_w given, else already normalised),
+ *   router_scale [H], router_proj [E,H] bf16 -> scores [N,E] f32 holding the
+ *   bf16-rounded logits.  x and router_proj 16-byte aligned; H % 8 == 0,
+ *   H <= 16384, E <= 256. */
+int g4mi_moe_router_scores(const uint16_t* x, const uint16_t* pre_norm_w, const uint16_t* router_scale,
+                           const uint16_t* router_proj, int64_t N, int64_t H, int64_t E, float eps, float* scores,
+                           void* stream);
+
+/* Router + top-k: model.py:224-232 (_router).  As g4mi_moe_router_scores, then
+ * f32 softmax, top-k (descending probability, ties to the lower expert index
+ * as jax.lax.top_k), renormalisation and per_expert_scale [E]:
+ *   out_w [N,k] f32, out_i [N,k] int32.  k <= 32. */
 int64_t g4mi_moe_router_workspace_bytes(int64_t N, int64_t E);
 int g4mi_moe_router_topk(const uint16_t* x, const uint16_t* pre_norm_w, const uint16_t* router_scale,
                          const uint16_t* router_proj, const uint16_t* per_expert_scale, int64_t N, int64_t H,
                          int64_t E, int64_t k, float eps, float* out_w, int32_t* out_i, void* ws,
                          int64_t ws_bytes, void* stream);
 
-/* Selected-expert GEMVs + weighted combine: model.py:262-294 (_moe, decode
- * "slice" path) with combine = G4MI_COMBINE_BF16_RUNNING, or the dense-MoE
- * contraction of model.py:241-250 with combine = G4MI_COMBINE_F32.
- *   xn [N,H] bf16 (pre_feedforward_layernorm_2 output), gate_up [E,2,F,H],
- *   down [E,H,F] bf16, top_w [N,k] f32, top_i [N,k] int32 -> out [N,H] bf16.
- * Reads only the k selected experts' rows.  H = 256*i, F = 64*i (i <= 16). */
-int64_t g4mi_moe_experts_workspace_bytes(int64_t N, int64_t F, int64_t k);
-
-/* The two halves of g4mi_moe_experts_decode, for callers that schedule them
- * separately.  gate/up: act[N,k,F] bf16 = bf16(bf16(bf16(gelu(g)) * u) * bf16(w))
- * per selected expert (model.py:267-271).  down: the per-expert down GEMV
- * (model.py:272-273) and the combine (model.py:289-293 / model.py:250). */
+/* Selected-expert gate/up GEMV + activation, model.py:267-271:
+ *   act[N,k,F] bf16 = bf16(bf16(bf16(gelu(g)) * u) * bf16(top_w)) where (g, u)
+ *   are the gate/up rows of expert top_i[n,slot] applied to xn [N,H].
+ * gate_up [E,2,F,H] bf16 (gate rows then up rows).  Reads only the selected
+ * experts' rows.  H = 256*i, F = 64*i (1 <= i <= 16), k <= 32. */
 int g4mi_moe_gateup(const uint16_t* xn, const uint16_t* gate_up, const float* top_w, const int32_t* top_i,
                     int64_t N, int64_t H, int64_t F, int64_t E, int64_t k, uint16_t* act, void* stream);
+
+/* The same with the routing taken from router scores [N,E] (softmax + top-k of
+ * model.py:228-231 done inside); also stores top_w [N,k] / top_i [N,k]. */
+int g4mi_moe_gateup_routed(const uint16_t* xn, const float* scores, const uint16_t* per_expert_scale,
+                           const uint16_t* gate_up, int64_t N, int64_t H, int64_t F, int64_t E, int64_t k,
+                           uint16_t* act, float* top_w, int32_t* top_i, void* stream);
+
+/* Selected-expert down GEMV (model.py:272-273) and combine:
+ * G4MI_COMBINE_BF16_RUNNING = the decode path's bf16 running sum in top-k
+ * order (model.py:289-293); G4MI_COMBINE_F32 = one f32 contraction over the
+ * experts (the dense prefill path, model.py:250).  down [E,H,F] bf16. */
 int g4mi_moe_down(const uint16_t* act, const uint16_t* down, const int32_t* top_i, int64_t N, int64_t H,
                   int64_t F, int64_t E, int64_t k, int32_t combine, uint16_t* out, void* stream);
+
+/* gate/up + down for given routing: model.py:262-294 (decode) or 241-250 (dense). */
+int64_t g4mi_moe_experts_workspace_bytes(int64_t N, int64_t F, int64_t k);
 int g4mi_moe_experts_decode(const uint16_t* xn, const uint16_t* gate_up, const uint16_t* down,
                             const float* top_w, const int32_t* top_i, int64_t N, int64_t H, int64_t F,
                             int64_t E, int64_t k, int32_t combine, uint16_t* out, void* ws, int64_t ws_bytes,
                             void* stream);
+
+/* The whole MoE decode block of model.py:235-294 on xn [N,H] (the
+ * pre_feedforward_layernorm_2 output): router scores, then gate/up with the
+ * selection fused in, then down + combine.  Three kernels, no host sync. */
+int64_t g4mi_moe_block_workspace_bytes(int64_t N, int64_t E, int64_t F, int64_t k);
+int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, const uint16_t* router_proj,
+                          const uint16_t* per_expert_scale, const uint16_t* gate_up, const uint16_t* down,
+                          int64_t N, int64_t H, int64_t F, int64_t E, int64_t k, float eps, int32_t combine,
+                          uint16_t* out, float* top_w, int32_t* top_i, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

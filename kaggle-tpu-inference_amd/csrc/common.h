@@ -77,17 +77,46 @@ __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_no
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 
 // ------------------------------------------------------------------ reductions
-// Butterfly sum over groups of W consecutive lanes (W a power of two <= 64).
+// Cross-lane sums: DPP quad/mirror moves inside a row of 16 lanes (no LDS
+// round trip), then one ds_bpermute per step across rows.  Every lane of a
+// group ends with the same, bitwise identical, total (IEEE add commutes).
+// (The gfx950 permlane16/32_swap builtins are avoided: with both operands the
+// same value the compiler drops the swapped-out second result.)
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const unsigned long long b = __builtin_bit_cast(unsigned long long, v);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)b, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(b >> 32), CTRL, 0xF, 0xF, false);
+  return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+constexpr int kDppXor1 = 0xB1;   // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;   // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+
+// Sum over aligned groups of W consecutive lanes (W in {1,2,4,...,64}).
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  if constexpr (W >= 2) v += dpp_f<kDppXor1>(v);
+  if constexpr (W >= 4) v += dpp_f<kDppXor2>(v);
+  if constexpr (W >= 8) v += dpp_f<kDppHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_f<kDppMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, kWave);
   return v;
 }
 template <int W>
 __device__ __forceinline__ double group_sum_f64(double v) {
-#pragma unroll
-  for (int m = W / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
+  if constexpr (W >= 2) v += dpp_d<kDppXor1>(v);
+  if constexpr (W >= 4) v += dpp_d<kDppXor2>(v);
+  if constexpr (W >= 8) v += dpp_d<kDppHalfMirror>(v);
+  if constexpr (W >= 16) v += dpp_d<kDppMirror>(v);
+  if constexpr (W >= 32) v += __shfl_xor(v, 16, kWave);
+  if constexpr (W >= 64) v += __shfl_xor(v, 32, kWave);
   return v;
 }
 template <int W>

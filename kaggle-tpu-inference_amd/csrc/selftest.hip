@@ -1,0 +1,36 @@
+// Diagnostics: exercises the cross-lane reduction helpers every kernel relies
+// on, so a test can check their lane layout against a host computation.
+#include "capi_util.h"
+#include "common.h"
+
+namespace g4mi {
+
+// in: 64*nw floats; out: for each wave and each W in {2,4,8,16,32,64} the
+// per-lane group sum (f32 and f64) -> out[(w*6 + j)*64 + lane], out_d likewise.
+__global__ void selftest_reduce_kernel(const float* __restrict__ in, float* __restrict__ out,
+                                       double* __restrict__ out_d) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const float v = in[threadIdx.x];
+  const double d = (double)v;
+  float r[6];
+  double rd[6];
+  r[0] = group_sum<2>(v); r[1] = group_sum<4>(v); r[2] = group_sum<8>(v);
+  r[3] = group_sum<16>(v); r[4] = group_sum<32>(v); r[5] = group_sum<64>(v);
+  rd[0] = group_sum_f64<2>(d); rd[1] = group_sum_f64<4>(d); rd[2] = group_sum_f64<8>(d);
+  rd[3] = group_sum_f64<16>(d); rd[4] = group_sum_f64<32>(d); rd[5] = group_sum_f64<64>(d);
+  for (int j = 0; j < 6; ++j) {
+    out[(w * 6 + j) * 64 + lane] = r[j];
+    out_d[(w * 6 + j) * 64 + lane] = rd[j];
+  }
+}
+
+}  // namespace g4mi
+
+extern "C" int g4mi_selftest_lane_reductions(const float* in, float* out, double* out_d, int32_t waves,
+                                             void* stream) {
+  G4MI_REQUIRE(in && out && out_d, G4MI_EINVAL, "selftest_lane_reductions: null pointer");
+  G4MI_REQUIRE(waves >= 1 && waves <= 16, G4MI_EINVAL, "selftest_lane_reductions: waves in [1,16]");
+  hipLaunchKernelGGL(g4mi::selftest_reduce_kernel, dim3(1), dim3(64 * waves), 0, g4mi::as_stream(stream), in, out,
+                     out_d);
+  return g4mi::check_launch("selftest_lane_reductions");
+}

@@ -191,3 +191,72 @@ def moe_down(act, down, top_i, combine="bf16_running", out=None):
     _lib.call("g4mi_moe_down", _ptr(act), _ptr(down), _ptr(top_i), n, h, f, e, k, mode, _ptr(out),
               stream_handle(act.device))
     return out
+
+
+def moe_router_scores(x, router_scale, router_proj, eps, pre_norm_w=None, out=None):
+    """Router logits (bf16-rounded, as f32) [N, E] (model.py:225-227)."""
+    n, h = x.shape
+    e = router_proj.shape[0]
+    _need(x, BF16, "x")
+    _need(router_scale, BF16, "router_scale", (h,))
+    _need(router_proj, BF16, "router_proj", (e, h))
+    if pre_norm_w is not None:
+        _need(pre_norm_w, BF16, "pre_norm_w", (h,))
+    if out is None:
+        out = torch.empty((n, e), dtype=torch.float32, device=x.device)
+    _need(out, torch.float32, "out", (n, e))
+    _lib.call("g4mi_moe_router_scores", _ptr(x), _ptr(pre_norm_w), _ptr(router_scale), _ptr(router_proj), n, h, e,
+              float(eps), _ptr(out), stream_handle(x.device))
+    return out
+
+
+def moe_block(xn, router_scale, router_proj, per_expert_scale, gate_up, down, k, eps, combine="bf16_running",
+              out=None, route=None):
+    """The whole MoE decode block (model.py:235-294) on xn [N, H]; returns
+    (out [N, H] bf16, top_w [N, k] f32, top_i [N, k] int32)."""
+    n, h = xn.shape
+    e, _, f, _ = gate_up.shape
+    _need(xn, BF16, "xn")
+    _need(router_scale, BF16, "router_scale", (h,))
+    _need(router_proj, BF16, "router_proj", (e, h))
+    _need(per_expert_scale, BF16, "per_expert_scale", (e,))
+    _need(gate_up, BF16, "gate_up", (e, 2, f, h))
+    _need(down, BF16, "down", (e, h, f))
+    mode = {"bf16_running": _lib.COMBINE_BF16_RUNNING, "f32": _lib.COMBINE_F32}[combine]
+    if out is None:
+        out = torch.empty((n, h), dtype=BF16, device=xn.device)
+    _need(out, BF16, "out", (n, h))
+    if route is None:
+        route = (torch.empty((n, k), dtype=torch.float32, device=xn.device),
+                 torch.empty((n, k), dtype=torch.int32, device=xn.device))
+    top_w, top_i = route
+    _need(top_w, torch.float32, "top_w", (n, k))
+    _need(top_i, torch.int32, "top_i", (n, k))
+    nbytes = _lib.lib().g4mi_moe_block_workspace_bytes(n, e, f, k)
+    ws = WORKSPACE.get(xn.device, "moe_block", nbytes)
+    _lib.call("g4mi_moe_block_decode", _ptr(xn), _ptr(router_scale), _ptr(router_proj), _ptr(per_expert_scale),
+              _ptr(gate_up), _ptr(down), n, h, f, e, k, float(eps), mode, _ptr(out), _ptr(top_w), _ptr(top_i),
+              _ptr(ws), ws.numel(), stream_handle(xn.device))
+    return out, top_w, top_i
+
+
+def moe_gateup_routed(xn, scores, per_expert_scale, gate_up, k, act=None, route=None):
+    """gate/up with the softmax + top-k selection fused (model.py:228-231, 267-271)."""
+    n, h = xn.shape
+    e, _, f, _ = gate_up.shape
+    _need(xn, BF16, "xn")
+    _need(scores, torch.float32, "scores", (n, e))
+    _need(per_expert_scale, BF16, "per_expert_scale", (e,))
+    _need(gate_up, BF16, "gate_up", (e, 2, f, h))
+    if act is None:
+        act = torch.empty((n, k, f), dtype=BF16, device=xn.device)
+    _need(act, BF16, "act", (n, k, f))
+    if route is None:
+        route = (torch.empty((n, k), dtype=torch.float32, device=xn.device),
+                 torch.empty((n, k), dtype=torch.int32, device=xn.device))
+    top_w, top_i = route
+    _need(top_w, torch.float32, "top_w", (n, k))
+    _need(top_i, torch.int32, "top_i", (n, k))
+    _lib.call("g4mi_moe_gateup_routed", _ptr(xn), _ptr(scores), _ptr(per_expert_scale), _ptr(gate_up), n, h, f, e,
+              k, _ptr(act), _ptr(top_w), _ptr(top_i), stream_handle(xn.device))
+    return act, top_w, top_i

@@ -186,3 +186,50 @@ def test_router_workspace_reuse_across_batch_sizes(c2):
         torch.cuda.synchronize()
         _, ei = twin.router(cfg, cpu, x.cpu())
         assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32)), n
+
+
+@pytest.mark.parametrize("n", [1, 4, 8])
+def test_router_scores_bit_exact(c2, n):
+    cfg, g, cpu = c2
+    x = _gen((n, cfg.hidden_size), 1, f"x.n{n}", 1.0)
+    s = ops.moe_router_scores(x, g["router.scale"], g["router.proj"], cfg.rms_norm_eps)
+    torch.cuda.synchronize()
+    xc = twin.rms_norm(x.cpu(), None, cfg.rms_norm_eps)
+    c = float(twin.rb(torch.tensor(cfg.hidden_size ** -0.5, dtype=torch.float32)))
+    x2 = twin.rb(twin.f32(twin.rb(twin.f32(xc) * twin.f32(cpu["router.scale"]))) * np.float32(c))
+    exp = twin.f32(twin.rb(torch.einsum("nh,eh->ne", x2.double(), cpu["router.proj"].double())))
+    assert np.array_equal(s.cpu().numpy(), exp.numpy())
+
+
+@pytest.mark.parametrize("n", [1, 4, 8])
+def test_moe_block_decode_c2(c2, n):
+    """Router scores -> gate/up with fused selection -> down, against the oracle."""
+    cfg, g, cpu = c2
+    x = _gen((n, cfg.hidden_size), 1, f"x.block{n}", 1.0)
+    out, tw, ti = ops.moe_block(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                g["experts.gate_up_proj"], g["experts.down_proj"], cfg.top_k_experts, cfg.rms_norm_eps)
+    torch.cuda.synchronize()
+    ew, ei = twin.router(cfg, cpu, x.cpu())
+    assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32))
+    np.testing.assert_allclose(tw.cpu().numpy(), ew.numpy(), rtol=2.5e-7, atol=0)
+    _check_out(out, twin.moe(cfg, cpu, x.cpu(), dense=False), f"moe block n={n}")
+
+
+def test_moe_block_tiny_and_f32_combine():
+    """Tiny-model shapes (16 experts top-4) through the fused block, both combines."""
+    cfg = tiny_parity_config()
+    lp = twin.layer_params(twin.random_params(cfg, 0), 2)
+    gl = {k: v.to(DEV) for k, v in lp.items()}
+    flat = twin.rms_norm(_gen((32, cfg.hidden_size), 9, "flat", 1.0).cpu(), lp["pre_feedforward_layernorm_2"],
+                         cfg.rms_norm_eps)
+    out, tw, ti = ops.moe_block(flat.to(DEV), gl["router.scale"], gl["router.proj"], gl["router.per_expert_scale"],
+                                gl["experts.gate_up_proj"], gl["experts.down_proj"], cfg.top_k_experts,
+                                cfg.rms_norm_eps)
+    out32, _, _ = ops.moe_block(flat.to(DEV), gl["router.scale"], gl["router.proj"], gl["router.per_expert_scale"],
+                                gl["experts.gate_up_proj"], gl["experts.down_proj"], cfg.top_k_experts,
+                                cfg.rms_norm_eps, combine="f32")
+    torch.cuda.synchronize()
+    _, ei = twin.router(cfg, lp, flat)
+    assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32))
+    _check_out(out, twin.moe(cfg, lp, flat, dense=False), "tiny block")
+    _check_out(out32, twin.moe(cfg, lp, flat, dense=True), "tiny block dense")
