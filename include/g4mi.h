@@ -115,6 +115,93 @@ int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, cons
                           int64_t N, int64_t H, int64_t F, int64_t E, int64_t k, float eps, int32_t combine,
                           uint16_t* out, float* top_w, int32_t* top_i, void* ws, int64_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- attention (K5)
+ * Split-K decode attention over a paged bf16 KV cache, model.py:197-213 with
+ * the decode masks of model.py:402-408 (sliding: pos-window < kv <= pos, full:
+ * kv <= pos), scale 1.0, optional logit softcap (0 = off, the reference).
+ *   q_raw [B,NH,D], k_raw/v_raw [B,KV,D] bf16: the raw projections of the new
+ *   token (v_raw NULL on k==v layers: V = rms_norm(k_raw)); q_norm/k_norm [D];
+ *   rope_cos/rope_sin [>=lmax, D/2] bf16; k_pages/v_pages [num_pages,KV,PAGE,D];
+ *   page_table [B,max_pages] int32; pos [B] int32 (device).
+ * With append != 0 the new K/V are normalised, roped and written at pos.
+ * ctx [B,NH,D] bf16.  D in {64,128,256,512}; NH/KV in {1,2,4,8};
+ * n_split_max >= g4mi_attention_min_splits(span), span = window (when
+ * 0 < window < lmax) else lmax (a split holds <= 256 positions).  A position
+ * outside [0, lmax) attends to nothing (ctx = 0). */
+int64_t g4mi_attention_min_splits(int64_t lmax);
+int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max);
+int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                          const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                          const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                          const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B, int64_t NH,
+                          int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap, float eps,
+                          int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx, void* ws,
+                          int64_t ws_bytes, void* stream);
+
+/* Cache append of T tokens of one sequence (model.py:202-206, the
+ * dynamic_update_slice of model.py:205-206): k = rope(rms_norm(k_raw, k_norm)),
+ * v = rms_norm(v_raw) written at positions pos[T] through page_table_row. */
+int g4mi_kv_append(const uint16_t* k_raw, const uint16_t* v_raw, const uint16_t* k_norm, const uint16_t* rope_cos,
+                   const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                   const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t T, int64_t KV, int64_t D,
+                   int64_t page_size, int64_t lmax, float eps, void* stream);
+
+/* ---------------------------------------------------------------- decode layer (K4, K6, K7)
+ * Batch-1 pieces of one decode step; all vectors are bf16 of length H unless
+ * stated.  H = 256*i (i <= 16).
+ *
+ * g4mi_layer_in: the q/k/v projection rows (model.py:197-201) applied to
+ * rms_norm(x, input_layernorm) (model.py:301), where x is
+ *   mode 0: bf16(embed[tok[0]] * bf16(sqrt(H)))               (model.py:355-357)
+ *   mode 1: the previous layer's tail bf16(bf16(x1 + rms_norm(hs, post_ff)) *
+ *           layer_scalar), hs = bf16(rms_norm(mlp_out, post_ff_1) +
+ *           rms_norm(moe_out, post_ff_2)) (hs = mlp_out when moe_out is NULL)
+ *                                                              (model.py:312-322)
+ *   mode 2: x_in.
+ * x is also stored to x_out.  qkv_out = [q rows | k rows | v rows] bf16. */
+int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64_t vocab, const uint16_t* x_in,
+                  const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
+                  const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                  const uint16_t* input_ln, uint16_t* x_out, const uint16_t* wq, int64_t q_rows, const uint16_t* wk,
+                  int64_t k_rows, const uint16_t* wv, int64_t v_rows, uint16_t* qkv_out, int64_t H, float eps,
+                  void* stream);
+
+/* out[rows] = ctx[K] . w[rows, K]: the o_proj of model.py:214.  K = 512*i or 256*i (i <= 16). */
+int g4mi_oproj(const uint16_t* ctx, const uint16_t* w, int64_t rows, int64_t K, uint16_t* out, void* stream);
+
+/* x1 = bf16(x + rms_norm(o, post_attention_layernorm)) (model.py:303-304);
+ * act_mlp[I] = bf16(bf16(gelu(g)) * u) of the dense MLP on rms_norm(x1,
+ * pre_feedforward_layernorm) (model.py:218-220, 310); with router_proj,
+ * xe = rms_norm(x1, pre_feedforward_layernorm_2) (model.py:315) and the
+ * router scores [E] on it (model.py:225-227). */
+int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_ln, const uint16_t* pre_ff_ln,
+                const uint16_t* pre_ff2_ln, uint16_t* x1_out, uint16_t* xe_out, const uint16_t* gate,
+                const uint16_t* up, int64_t I, uint16_t* act_mlp, const uint16_t* router_scale,
+                const uint16_t* router_proj, int64_t E, float* scores, int64_t H, float eps, void* stream);
+
+/* mlp_out[H] = act_mlp . down[H, I] (model.py:221) and, with experts_down,
+ * moe_out[H] = the combine of the k selected experts' down rows applied to
+ * act_moe [k, F] (model.py:272-293 / model.py:250 by `combine`).  k <= 8. */
+int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint16_t* mlp_out,
+                 const uint16_t* act_moe, const uint16_t* experts_down, const int32_t* top_i, int64_t E, int64_t k,
+                 int64_t F, int32_t combine, uint16_t* moe_out, int64_t H, void* stream);
+
+/* The last layer's tail (as g4mi_layer_in mode 1), the final norm
+ * (model.py:373), logits[V] f32 = softcap(f32(bf16(x . embed[v])))
+ * (model.py:381-385, softcap 0 = off), and the per-block maxima
+ * blk_val/blk_idx [g4mi_lm_head_blocks(V)] for g4mi_argmax_finalize. */
+int64_t g4mi_lm_head_blocks(int64_t V);
+int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
+                 const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                 const uint16_t* final_norm, const uint16_t* embed, int64_t V, int64_t H, float softcap, float eps,
+                 float* logits, float* blk_val, int32_t* blk_idx, void* stream);
+
+/* Greedy token (model.py:416: first index of the maximum) from the per-block
+ * maxima -> tok[0].  With pos != NULL also pos[0] += 1 and hist[pos[0]] = token
+ * (when within hist_len), so a captured decode step advances on its own. */
+int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n, int32_t* tok, int32_t* pos,
+                         int32_t* hist, int64_t hist_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,445 @@
+// Decode attention over a paged bf16 KV cache (model.py:197-213).
+//
+// Cache layout per layer: pages [num_pages, KV, PAGE, D] bf16 for K and for V
+// (the reference keeps separate K and V even for k==v layers, model.py:201-206);
+// a page table [B, max_pages] int32 maps position p of sequence b to page
+// pt[b][p / PAGE], slot p % PAGE.  One (page, kv head) is PAGE*D contiguous
+// values, so a split of consecutive positions streams contiguous memory.
+//
+// Three kernels per call, split-K over positions:
+//   scores: q = rope(rms_norm(q_raw, q_norm)) for the G query heads of a KV
+//           head; the block whose split ends at `pos` also builds
+//           k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) and appends
+//           them to the cache; s = f32(bf16(q . k)) (scale 1.0), optional
+//           softcap, causal/sliding range; per-split max and sum of exp.
+//   pv:     merges the split statistics, p = bf16(exp(s - m) / sum) -- the
+//           reference rounds the normalised probabilities to bf16 before the
+//           PV product (model.py:212) -- and accumulates p . V in f32.
+//   reduce: ctx = bf16(sum of the split partials), in split order.
+// Masked positions contribute exp(-1e30 - m) = 0 in the reference, so only the
+// attended range [lo, pos] is visited.
+//
+// Device-side positions and page indices are range-checked: an out-of-range
+// position attends to nothing (ctx = 0, no cache write) and an out-of-range
+// page entry is skipped, so bad inputs cannot address outside the buffers.
+#include "capi_util.h"
+#include "common.h"
+
+namespace g4mi {
+
+constexpr int kChunkMin = 64;   // positions per split, at least
+constexpr int kChunkMax = 256;  // positions per split, at most (LDS score buffer)
+
+struct AttnDims {
+  int B, NH, KV, G, D, page, max_pages, num_pages, window, n_split_max, lmax;
+  float softcap, eps;
+};
+
+// Attended range of a sequence at position `pos`, cut into n_eff splits.
+struct Range {
+  int lo, len, chunk, n_eff;
+};
+__device__ __forceinline__ Range attn_range(const AttnDims& a, int pos) {
+  Range r;
+  if (pos < 0 || pos >= a.lmax || pos >= a.max_pages * a.page) {
+    r.lo = 0; r.len = 0; r.chunk = kChunkMin; r.n_eff = 0;
+    return r;
+  }
+  const int end = pos + 1;
+  r.lo = (a.window > 0) ? max(0, end - a.window) : 0;
+  r.len = end - r.lo;
+  r.chunk = max((r.len + a.n_split_max - 1) / a.n_split_max, kChunkMin);
+  r.n_eff = (r.len + r.chunk - 1) / r.chunk;
+  return r;
+}
+
+// Element offset of (position p, kv head) in the page pool, or -1 when the
+// page table entry is out of range.
+__device__ __forceinline__ long long page_off(const AttnDims& a, const int32_t* pt_row, int p, int kv) {
+  const int page = pt_row[p / a.page];
+  if (page < 0 || page >= a.num_pages) return -1;
+  return ((((long long)page * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+}
+
+__device__ __forceinline__ float wave_max_bfly(float m) {
+#pragma unroll
+  for (int s = 1; s < 64; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, kWave));
+  return m;
+}
+
+// rms_norm(+weight) and optional RoPE of one head of D values by one wave;
+// lane l owns the D/64 consecutive values starting at l*(D/64), so the RoPE
+// partner (d +- D/2) of a value sits in lane l^32.  cos/sin are bf16 rows of
+// length D/2 at the token's position (the reference duplicates the halves,
+// model.py:66).  Writes the bf16-valued results to dst[d] (f32).
+template <int D>
+__device__ void norm_rope_head(const uint16_t* __restrict__ src, const uint16_t* __restrict__ w,
+                               const uint16_t* __restrict__ cs, const uint16_t* __restrict__ sn, float eps,
+                               bool rope, float* __restrict__ dst) {
+  constexpr int PL = D / 64;
+  const int lane = threadIdx.x & 63;
+  float x[PL];
+  double ss = 0.0;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    x[i] = bf2f(src[lane * PL + i]);
+    ss = fma((double)x[i], (double)x[i], ss);
+  }
+  const float r = rms_scale(group_sum_f64<64>(ss), D, eps);
+#pragma unroll
+  for (int i = 0; i < PL; ++i) x[i] = (w != nullptr) ? rbf(x[i] * r * bf2f(w[lane * PL + i])) : rbf(x[i] * r);
+  if (rope) {
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const int d = lane * PL + i;
+      const float partner = __shfl_xor(x[i], 32, kWave);
+      const float rot = (d < D / 2) ? -partner : partner;
+      const int j = d % (D / 2);
+      x[i] = rbf(rbf(x[i] * bf2f(cs[j])) + rbf(rot * bf2f(sn[j])));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PL; ++i) dst[lane * PL + i] = x[i];
+}
+
+// ------------------------------------------------------------------ scores
+// grid (n_split_max, KV, B), 256 threads.  Wave steps cover PPW positions with
+// LPP = D/8 lanes each (one 16-byte chunk per lane).
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_scores_kernel(
+    AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
+    const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
+    const uint16_t* __restrict__ rope_cos, const uint16_t* __restrict__ rope_sin, uint16_t* __restrict__ k_pages,
+    uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table, const int32_t* __restrict__ pos_arr,
+    int append, float* __restrict__ ws_scores, float* __restrict__ ws_stats) {
+  constexpr int LPP = D / 8;
+  constexpr int PPW = 64 / LPP;
+  __shared__ float qs[G * D];
+  __shared__ float knew[D];
+  __shared__ float vnew[D];
+  __shared__ float sc[G][kChunkMax];
+  __shared__ float redm[4][G];
+  __shared__ float redl[4][G];
+  const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = pos_arr[b];
+  const Range R = attn_range(a, pos);
+  if (split >= R.n_eff) return;
+  const int start = R.lo + split * R.chunk;
+  const int end = min(R.lo + R.len, start + R.chunk);
+  const int npos = end - start;
+  const uint16_t* cs = rope_cos + (size_t)pos * (D / 2);
+  const uint16_t* sn = rope_sin + (size_t)pos * (D / 2);
+  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
+
+  for (int g = wave; g < G; g += 4)
+    norm_rope_head<D>(q_raw + ((size_t)b * a.NH + kv * G + g) * D, q_norm, cs, sn, a.eps, true, qs + g * D);
+  const bool mine = append && (end == pos + 1);
+  if (mine) {
+    const uint16_t* kr = k_raw + ((size_t)b * a.KV + kv) * D;
+    const uint16_t* vr = (v_raw != nullptr) ? v_raw + ((size_t)b * a.KV + kv) * D : kr;
+    if (wave == 0) norm_rope_head<D>(kr, k_norm, cs, sn, a.eps, true, knew);
+    if (wave == 1) norm_rope_head<D>(vr, nullptr, cs, sn, a.eps, false, vnew);
+    __syncthreads();
+    const long long off = page_off(a, pt_row, pos, kv);
+    if (off >= 0)
+      for (int d = tid; d < D; d += 256) {
+        k_pages[off + d] = f2bf(knew[d]);
+        v_pages[off + d] = f2bf(vnew[d]);
+      }
+  }
+  __syncthreads();
+
+  const int sub = lane % LPP, slot = lane / LPP;
+  float q[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[g][i] = qs[g * D + sub * 8 + i];
+  const float cap = a.softcap;
+  for (int base = wave * PPW; base < npos; base += 4 * PPW) {
+    const int j = base + slot;
+    const int p = start + j;
+    float kf[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kf[i] = 0.0f;
+    bool ok = false;
+    if (j < npos) {
+      if (mine && p == pos) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[i] = knew[sub * 8 + i];
+        ok = true;
+      } else {
+        const long long off = page_off(a, pt_row, p, kv);
+        if (off >= 0) {
+          unpack8(ld16(k_pages + off + sub * 8), kf);
+          ok = true;
+        }
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc = fmaf(q[g][i], kf[i], acc);
+      acc = group_sum<LPP>(acc);
+      float s = rbf(acc);
+      if (cap > 0.0f) s = tanhf(s / cap) * cap;
+      if (j < npos && sub == 0) sc[g][j] = ok ? s : -INFINITY;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    float m = -INFINITY;
+    for (int j = tid; j < npos; j += 256) m = fmaxf(m, sc[g][j]);
+    m = wave_max_bfly(m);
+    if (lane == 0) redm[wave][g] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float m = fmaxf(fmaxf(redm[0][g], redm[1][g]), fmaxf(redm[2][g], redm[3][g]));
+    float* srow = ws_scores + ((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo);
+    float l = 0.0f;
+    for (int j = tid; j < npos; j += 256) {
+      const float s = sc[g][j];
+      l += (s == -INFINITY) ? 0.0f : expf(s - m);
+      srow[j] = s;
+    }
+    l = group_sum<64>(l);
+    if (lane == 0) redl[wave][g] = l;
+  }
+  __syncthreads();
+  if (tid < G) {
+    const int h = kv * G + tid;
+    const float m = fmaxf(fmaxf(redm[0][tid], redm[1][tid]), fmaxf(redm[2][tid], redm[3][tid]));
+    float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
+    float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
+    sm[split] = m;
+    sl[split] = redl[0][tid] + redl[1][tid] + redl[2][tid] + redl[3][tid];
+  }
+}
+
+// ------------------------------------------------------------------ pv
+// grid (n_split_max, KV, B), 256 threads.  Wave w owns the values
+// [w*D/4, (w+1)*D/4) of every head; LPV = D/32 lanes per position, so the
+// position-partials reduce inside the wave and no cross-wave pass is needed.
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
+                                                      const int32_t* __restrict__ page_table,
+                                                      const int32_t* __restrict__ pos_arr,
+                                                      const float* __restrict__ ws_scores,
+                                                      const float* __restrict__ ws_stats, float* __restrict__ ws_part) {
+  constexpr int LPV = D / 32;
+  constexpr int PPV = 64 / LPV;
+  __shared__ float pr[G][kChunkMax];
+  __shared__ float mg[G], sg[G];
+  const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int pos = pos_arr[b];
+  const Range R = attn_range(a, pos);
+  if (split >= R.n_eff) return;
+  const int start = R.lo + split * R.chunk;
+  const int end = min(R.lo + R.len, start + R.chunk);
+  const int npos = end - start;
+  if (tid < G) {
+    const int h = kv * G + tid;
+    const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
+    const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
+    float m = -INFINITY;
+    for (int i = 0; i < R.n_eff; ++i) m = fmaxf(m, sm[i]);
+    float s = 0.0f;
+    for (int i = 0; i < R.n_eff; ++i) s += (sm[i] == -INFINITY) ? 0.0f : expf(sm[i] - m) * sl[i];
+    mg[tid] = m;
+    sg[tid] = s;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float* srow = ws_scores + ((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo);
+    for (int j = tid; j < npos; j += 256) {
+      const float s = srow[j];
+      pr[g][j] = (s == -INFINITY) ? 0.0f : rbf(expf(s - mg[g]) / sg[g]);
+    }
+  }
+  __syncthreads();
+  const int sub = lane % LPV, slot = lane / LPV;
+  const int dofs = wave * (D / 4) + sub * 8;
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
+  for (int j = slot; j < npos; j += PPV) {
+    const long long off = page_off(a, pt_row, start + j, kv);
+    if (off < 0) continue;
+    float vf[8];
+    unpack8(ld16(v_pages + off + dofs), vf);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float p = pr[g][j];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+    }
+  }
+  float* part = ws_part + (((size_t)b * a.n_split_max + split) * a.NH + kv * G) * D;
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = acc[g][i];
+#pragma unroll
+      for (int m = LPV; m < 64; m <<= 1) v += __shfl_xor(v, m, kWave);
+      if (slot == 0) part[g * D + dofs + i] = v;
+    }
+}
+
+// ------------------------------------------------------------------ reduce
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int32_t* __restrict__ pos_arr,
+                                                          const float* __restrict__ ws_part,
+                                                          uint16_t* __restrict__ ctx) {
+  const int b = blockIdx.y;
+  const int idx = blockIdx.x * 256 + threadIdx.x;  // h*D + d
+  if (idx >= a.NH * a.D) return;
+  const Range R = attn_range(a, pos_arr[b]);
+  float s = 0.0f;
+  for (int i = 0; i < R.n_eff; ++i) s += ws_part[(((size_t)b * a.n_split_max + i) * a.NH) * a.D + idx];
+  ctx[(size_t)b * a.NH * a.D + idx] = f2bf(s);
+}
+
+// ------------------------------------------------------------------ append
+// k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) of T tokens of one
+// sequence written at positions pos[t] (model.py:202-206).  grid (T, KV).
+template <int D>
+__global__ __launch_bounds__(128) void kv_append_kernel(AttnDims a, const uint16_t* __restrict__ k_raw,
+                                                        const uint16_t* __restrict__ v_raw,
+                                                        const uint16_t* __restrict__ k_norm,
+                                                        const uint16_t* __restrict__ rope_cos,
+                                                        const uint16_t* __restrict__ rope_sin,
+                                                        uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages,
+                                                        const int32_t* __restrict__ page_table,
+                                                        const int32_t* __restrict__ pos_arr) {
+  __shared__ float kn[D], vn[D];
+  const int t = blockIdx.x, kv = blockIdx.y, wave = threadIdx.x >> 6;
+  const int pos = pos_arr[t];
+  if (pos < 0 || pos >= a.lmax || pos >= a.max_pages * a.page) return;
+  const uint16_t* cs = rope_cos + (size_t)pos * (D / 2);
+  const uint16_t* sn = rope_sin + (size_t)pos * (D / 2);
+  const uint16_t* kr = k_raw + ((size_t)t * a.KV + kv) * D;
+  const uint16_t* vr = (v_raw != nullptr) ? v_raw + ((size_t)t * a.KV + kv) * D : kr;
+  if (wave == 0) norm_rope_head<D>(kr, k_norm, cs, sn, a.eps, true, kn);
+  if (wave == 1) norm_rope_head<D>(vr, nullptr, cs, sn, a.eps, false, vn);
+  __syncthreads();
+  const long long off = page_off(a, page_table, pos, kv);
+  if (off < 0) return;
+  for (int d = threadIdx.x; d < D; d += blockDim.x) {
+    k_pages[off + d] = f2bf(kn[d]);
+    v_pages[off + d] = f2bf(vn[d]);
+  }
+}
+
+// ------------------------------------------------------------------ launch
+template <int D, int G>
+static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint16_t* q_raw, const uint16_t* k_raw,
+                        const uint16_t* v_raw, const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* cs,
+                        const uint16_t* sn, uint16_t* kp, uint16_t* vp, const int32_t* pt, const int32_t* pos,
+                        int append, float* ws_scores, float* ws_stats, float* ws_part) {
+  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm, cs,
+                     sn, kp, vp, pt, pos, append, ws_scores, ws_stats);
+  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(256), 0, st, a, vp, pt, pos, ws_scores, ws_stats, ws_part);
+}
+
+static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
+
+}  // namespace g4mi
+
+using namespace g4mi;
+
+extern "C" {
+
+int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max) {
+  return al256(B * NH * lmax * 4) + al256(2 * B * NH * n_split_max * 4) + al256(B * n_split_max * NH * D * 4);
+}
+
+int64_t g4mi_attention_min_splits(int64_t lmax) { return (lmax + kChunkMax - 1) / kChunkMax; }
+
+int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                          const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                          const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                          const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B, int64_t NH,
+                          int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap, float eps,
+                          int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx, void* ws,
+                          int64_t ws_bytes, void* stream) {
+  G4MI_REQUIRE(q_raw && q_norm && rope_cos && rope_sin && k_pages && v_pages && page_table && pos && ctx && ws,
+               G4MI_EINVAL, "decode_attention: null pointer argument");
+  G4MI_REQUIRE(!append || (k_raw && k_norm), G4MI_EINVAL, "decode_attention: append needs k_raw and k_norm");
+  G4MI_REQUIRE(B >= 1 && B <= 65535 && KV >= 1 && KV <= 65535 && NH >= KV && NH % KV == 0, G4MI_EINVAL,
+               "decode_attention: bad B=%lld NH=%lld KV=%lld", (long long)B, (long long)NH, (long long)KV);
+  const int64_t G = NH / KV;
+  G4MI_REQUIRE(D == 64 || D == 128 || D == 256 || D == 512, G4MI_EUNSUPPORTED,
+               "decode_attention: head_dim %lld not in {64,128,256,512}", (long long)D);
+  G4MI_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, G4MI_EUNSUPPORTED,
+               "decode_attention: %lld query heads per KV head not in {1,2,4,8}", (long long)G);
+  G4MI_REQUIRE(page_size >= 1 && max_pages >= 1 && num_pages >= 1 && lmax >= 1, G4MI_EINVAL,
+               "decode_attention: bad page_size/max_pages/num_pages/lmax");
+  G4MI_REQUIRE(window >= 0, G4MI_EINVAL, "decode_attention: negative window");
+  const int64_t span = (window > 0 && window < lmax) ? window : lmax;  // most positions one query attends
+  G4MI_REQUIRE(n_split_max >= g4mi_attention_min_splits(span) && n_split_max <= 65535, G4MI_EINVAL,
+               "decode_attention: n_split_max %lld < %lld (a split holds at most %d positions)",
+               (long long)n_split_max, (long long)g4mi_attention_min_splits(span), kChunkMax);
+  G4MI_REQUIRE(((uintptr_t)k_pages & 15u) == 0 && ((uintptr_t)v_pages & 15u) == 0, G4MI_EALIGN,
+               "decode_attention: cache pages must be 16-byte aligned");
+  G4MI_REQUIRE(ws_bytes >= g4mi_decode_attention_workspace_bytes(B, NH, D, lmax, n_split_max), G4MI_EWORKSPACE,
+               "decode_attention: workspace too small");
+  AttnDims a;
+  a.B = (int)B; a.NH = (int)NH; a.KV = (int)KV; a.G = (int)G; a.D = (int)D; a.page = (int)page_size;
+  a.max_pages = (int)max_pages; a.num_pages = (int)num_pages; a.window = (int)window;
+  a.n_split_max = (int)n_split_max; a.lmax = (int)lmax; a.softcap = softcap; a.eps = eps;
+  float* ws_scores = (float*)ws;
+  float* ws_stats = (float*)((char*)ws + al256(B * NH * lmax * 4));
+  float* ws_part = (float*)((char*)ws_stats + al256(2 * B * NH * n_split_max * 4));
+  hipStream_t st = as_stream(stream);
+  dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
+#define G4MI_ATT(DD, GG)                                                                                         \
+  if (D == DD && G == GG)                                                                                        \
+    launch_attn<DD, GG>(a, grid, st, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, \
+                        page_table, pos, append, ws_scores, ws_stats, ws_part);
+  G4MI_ATT(64, 1) G4MI_ATT(64, 2) G4MI_ATT(64, 4) G4MI_ATT(64, 8)
+  G4MI_ATT(128, 1) G4MI_ATT(128, 2) G4MI_ATT(128, 4) G4MI_ATT(128, 8)
+  G4MI_ATT(256, 1) G4MI_ATT(256, 2) G4MI_ATT(256, 4) G4MI_ATT(256, 8)
+  G4MI_ATT(512, 1) G4MI_ATT(512, 2) G4MI_ATT(512, 4) G4MI_ATT(512, 8)
+#undef G4MI_ATT
+  hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)((NH * D + 255) / 256), (unsigned)B), dim3(256), 0, st, a,
+                     pos, ws_part, ctx);
+  return check_launch("decode_attention");
+}
+
+int g4mi_kv_append(const uint16_t* k_raw, const uint16_t* v_raw, const uint16_t* k_norm, const uint16_t* rope_cos,
+                   const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                   const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t T, int64_t KV, int64_t D,
+                   int64_t page_size, int64_t lmax, float eps, void* stream) {
+  G4MI_REQUIRE(k_raw && k_norm && rope_cos && rope_sin && k_pages && v_pages && page_table && pos, G4MI_EINVAL,
+               "kv_append: null pointer argument");
+  G4MI_REQUIRE(T >= 1 && T <= 65535 && KV >= 1 && KV <= 65535, G4MI_EINVAL, "kv_append: bad T/KV");
+  G4MI_REQUIRE(D == 64 || D == 128 || D == 256 || D == 512, G4MI_EUNSUPPORTED, "kv_append: bad head_dim");
+  G4MI_REQUIRE(page_size >= 1 && max_pages >= 1 && num_pages >= 1 && lmax >= 1, G4MI_EINVAL,
+               "kv_append: bad page geometry");
+  AttnDims a = {};
+  a.KV = (int)KV; a.D = (int)D; a.page = (int)page_size; a.max_pages = (int)max_pages;
+  a.num_pages = (int)num_pages; a.lmax = (int)lmax; a.eps = eps;
+  hipStream_t st = as_stream(stream);
+  switch (D) {
+#define G4MI_APP(DD)                                                                                          \
+  case DD:                                                                                                    \
+    hipLaunchKernelGGL(kv_append_kernel<DD>, dim3((unsigned)T, (unsigned)KV), dim3(128), 0, st, a, k_raw, v_raw, \
+                       k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table, pos);                        \
+    break;
+    G4MI_APP(64) G4MI_APP(128) G4MI_APP(256) G4MI_APP(512)
+#undef G4MI_APP
+  }
+  return check_launch("kv_append");
+}
+
+}  // extern "C"

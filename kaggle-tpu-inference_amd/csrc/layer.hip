@@ -1,0 +1,661 @@
+// The dense parts of one decode layer and the lm_head (model.py:297-322,
+// model.py:355-385), batch 1:
+//
+//   layer_in   prologue: layer 0 embeds the token (x = bf16(embed[tok] *
+//              bf16(sqrt(H))), model.py:355-357); later layers finish the
+//              previous layer (h1 = rms(mlp, post_ff_1), h2 = rms(moe,
+//              post_ff_2), h = rms(bf16(h1+h2), post_ff), x = bf16(bf16(x1+h) *
+//              layer_scalar), model.py:313-322); then rms(x, input_ln).
+//              Body: the q/k/v projection rows (model.py:197-201).
+//   oproj      ctx . o_proj (model.py:214).
+//   ffn_in     prologue: x1 = bf16(x + rms(o, post_attention_ln)); xm =
+//              rms(x1, pre_ff); xe = rms(x1, pre_ff_2) (model.py:303-315).
+//              Body: dense gate/up rows with gelu*up (model.py:218-220) and
+//              the router scores on xe (model.py:225-227).
+//   ffn_out    per output row: the dense down row (model.py:221) and the
+//              selected experts' down rows with the combine (model.py:272-293).
+//   lm_head    prologue: the last layer's tail and the final norm
+//              (model.py:373); body: tied-embedding rows, f32 softcap
+//              (model.py:381-385); per-block argmax.
+//   argmax     first index of the maximum over all blocks (model.py:416);
+//              writes the token, advances the position, records history.
+//
+// Every block rebuilds its prologue vector in LDS (the vectors are ~6 KB and
+// L2-resident) after issuing its weight loads, so the prologue latency hides
+// under the HBM latency of its own rows.  RMSNorm scales use exact f64 sums.
+#include <string.h>
+
+#include "capi_util.h"
+#include "common.h"
+
+namespace g4mi {
+
+constexpr int kVecChunks = 2;  // 16-byte chunks per thread: H <= 256*8*2 = 4096
+
+// A length-H bf16 vector spread over a 256-thread block: thread t owns the
+// 16-byte chunks t and t+256.
+struct Vec {
+  u32x4 c[kVecChunks];
+};
+
+__device__ __forceinline__ void vload(Vec& v, const uint16_t* __restrict__ p, int nch) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    v.c[j] = (c < nch) ? ld16((const u32x4*)p + c) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+__device__ __forceinline__ double vsumsq(const Vec& v, int nch) {
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j)
+    if ((int)threadIdx.x + 256 * j < nch) s = sumsq8_f64(v.c[j], s);
+  return s;
+}
+// v = bf16(v * r * w)  (w may be null)
+__device__ __forceinline__ void vscale(Vec& v, float r, const uint16_t* __restrict__ w, int nch) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nch) {
+      if (w != nullptr) {
+        const u32x4 wc = ld16((const u32x4*)w + c);
+        v.c[j] = scale8(v.c[j], r, &wc);
+      } else {
+        v.c[j] = scale8(v.c[j], r, nullptr);
+      }
+    }
+  }
+}
+// a = bf16(a + b)
+__device__ __forceinline__ void vadd(Vec& a, const Vec& b, int nch) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) {
+    float x[8], y[8];
+    unpack8(a.c[j], x);
+    unpack8(b.c[j], y);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = x[i] + y[i];
+    a.c[j].x = pack2(x[0], x[1]); a.c[j].y = pack2(x[2], x[3]);
+    a.c[j].z = pack2(x[4], x[5]); a.c[j].w = pack2(x[6], x[7]);
+  }
+}
+// a = bf16(a * s)
+__device__ __forceinline__ void vmul(Vec& a, float s) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) a.c[j] = scale8(a.c[j], s, nullptr);
+}
+__device__ __forceinline__ void vstore(const Vec& v, u32x4* dst, int nch) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nch) dst[c] = v.c[j];
+  }
+}
+__device__ __forceinline__ float vrms(const Vec& v, int nch, int H, float eps, double* red) {
+  return rms_scale(block_sum_f64(vsumsq(v, nch), red), H, eps);
+}
+
+// Tail of the previous layer: x = bf16(bf16(x1 + rms(hs, post_ff)) * ls),
+// hs = bf16(rms(mlp, post_ff_1) + rms(moe, post_ff_2)), or hs = mlp without MoE.
+struct TailArgs {
+  const uint16_t *x1, *mlp, *moe, *w_pf1, *w_pf2, *w_pf, *ls;
+};
+__device__ void tail_vec(Vec& x, const TailArgs& t, int nch, int H, float eps, double* red) {
+  Vec a, b;
+  vload(a, t.mlp, nch);
+  if (t.moe != nullptr) {
+    vload(b, t.moe, nch);
+    const float r1 = vrms(a, nch, H, eps, red);
+    const float r2 = vrms(b, nch, H, eps, red);
+    vscale(a, r1, t.w_pf1, nch);
+    vscale(b, r2, t.w_pf2, nch);
+    vadd(a, b, nch);
+  }
+  const float r3 = vrms(a, nch, H, eps, red);
+  vscale(a, r3, t.w_pf, nch);
+  vload(x, t.x1, nch);
+  vadd(x, a, nch);
+  vmul(x, bf2f(t.ls[0]));
+}
+
+// ------------------------------------------------------------------ GEMV core
+// S lanes per row, IT 16-byte chunks per lane (K = 8*S*IT).
+template <int S, int IT>
+__device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int sub, u32x4* w) {
+#pragma unroll
+  for (int i = 0; i < IT; ++i) w[i] = ld_stream((const u32x4*)row + sub + S * i);
+}
+template <int S, int IT>
+__device__ __forceinline__ float dot_row(const u32x4* w, const u32x4* __restrict__ xs, int sub) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) acc = dot8(w[i], xs[sub + S * i], acc);
+  return group_sum<S>(acc);
+}
+
+// ------------------------------------------------------------------ layer_in
+enum { kInEmbed = 0, kInTail = 1, kInPlain = 2 };
+struct InArgs {
+  int mode;
+  const int32_t* tok;
+  const uint16_t* embed;
+  int vocab;
+  float embed_c;          // bf16(sqrt(H))
+  const uint16_t* x_in;   // kInPlain
+  TailArgs tail;          // kInTail
+  const uint16_t* w_in;   // input_layernorm
+  uint16_t* x_out;        // the residual x (written by block 0)
+  const uint16_t* W[3];   // q, k, v projection rows [rows, H]
+  int rows[3];
+  uint16_t* out;          // [rows0 + rows1 + rows2]
+  int H;
+  float eps;
+};
+
+template <int IT>
+__global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
+  constexpr int H = IT * 256;
+  constexpr int NCH = H / 8;
+  __shared__ u32x4 xs[NCH];
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const int total = a.rows[0] + a.rows[1] + a.rows[2];
+  const int r = blockIdx.x * 8 + wave * 2 + half;
+  u32x4 w[IT];
+  const uint16_t* row = nullptr;
+  if (r < total) {
+    int rr = r, m = 0;
+    while (rr >= a.rows[m]) { rr -= a.rows[m]; ++m; }
+    row = a.W[m] + (size_t)rr * H;
+    load_row<32, IT>(row, l, w);
+  }
+  Vec x;
+  if (a.mode == kInEmbed) {
+    int t = a.tok[0];
+    t = (t < 0 || t >= a.vocab) ? 0 : t;
+    vload(x, a.embed + (size_t)t * H, NCH);
+    vmul(x, a.embed_c);
+  } else if (a.mode == kInTail) {
+    tail_vec(x, a.tail, NCH, H, a.eps, red);
+  } else {
+    vload(x, a.x_in, NCH);
+  }
+  if (blockIdx.x == 0) vstore(x, (u32x4*)a.x_out, NCH);
+  const float rn = vrms(x, NCH, H, a.eps, red);
+  vscale(x, rn, a.w_in, NCH);
+  vstore(x, xs, NCH);
+  __syncthreads();
+  if (r < total) {
+    const float acc = dot_row<32, IT>(w, xs, l);
+    if (l == 0) a.out[r] = f2bf(acc);
+  }
+}
+
+// ------------------------------------------------------------------ oproj
+// out[H] = ctx[K] . W[H, K]; S lanes per row (64/S rows per wave).
+template <int S, int IT>
+__global__ __launch_bounds__(256) void oproj_kernel(const uint16_t* __restrict__ ctx, const uint16_t* __restrict__ W,
+                                                    int rows, uint16_t* __restrict__ out) {
+  constexpr int K = 8 * S * IT;
+  constexpr int RPW = 64 / S;
+  __shared__ u32x4 xs[K / 8];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % S;
+  const int r = (blockIdx.x * 4 + wave) * RPW + lane / S;
+  u32x4 w[IT];
+  if (r < rows) load_row<S, IT>(W + (size_t)r * K, sub, w);
+  for (int c = tid; c < K / 8; c += 256) xs[c] = ld16((const u32x4*)ctx + c);
+  __syncthreads();
+  if (r < rows) {
+    const float acc = dot_row<S, IT>(w, xs, sub);
+    if (sub == 0) out[r] = f2bf(acc);
+  }
+}
+
+// ------------------------------------------------------------------ ffn_in
+struct FfnInArgs {
+  const uint16_t *x, *o, *w_pa, *w_pf, *w_pf2;
+  uint16_t *x1_out, *xe_out;
+  const uint16_t *gate, *up;   // dense MLP [I, H]
+  int I;
+  uint16_t* act_mlp;           // [I]
+  int dense_blocks;            // blocks [0, dense_blocks) do dense rows
+  const uint16_t *r_scale, *r_proj;  // router (null: no MoE)
+  int E;
+  float r_c;                   // bf16(H^-0.5)
+  float* scores;               // [E]
+  int H;
+  float eps;
+};
+
+template <int IT>
+__global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
+  constexpr int H = IT * 256;
+  constexpr int NCH = H / 8;
+  __shared__ u32x4 xs[NCH];
+  __shared__ double red[4];
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const bool dense = (int)blockIdx.x < a.dense_blocks;
+  int row = -1;
+  u32x4 w[IT];
+  if (dense) {
+    const int f = blockIdx.x * 4 + wave;  // one (gate, up) pair per wave
+    if (f < a.I) {
+      row = f;
+      load_row<32, IT>((half ? a.up : a.gate) + (size_t)f * H, l, w);
+    }
+  } else {
+    const int e = (blockIdx.x - a.dense_blocks) * 8 + wave * 2 + half;
+    if (e < a.E) {
+      row = e;
+      load_row<32, IT>(a.r_proj + (size_t)e * H, l, w);
+    }
+  }
+  // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
+  Vec x, o;
+  vload(o, a.o, NCH);
+  const float ro = vrms(o, NCH, H, a.eps, red);
+  vscale(o, ro, a.w_pa, NCH);
+  vload(x, a.x, NCH);
+  vadd(x, o, NCH);
+  if (blockIdx.x == 0) vstore(x, (u32x4*)a.x1_out, NCH);
+  const float r1 = vrms(x, NCH, H, a.eps, red);
+  if (dense) {
+    vscale(x, r1, a.w_pf, NCH);
+    vstore(x, xs, NCH);
+  } else {
+    Vec xe = x;
+    vscale(xe, r1, a.w_pf2, NCH);
+    if (blockIdx.x == a.dense_blocks) vstore(xe, (u32x4*)a.xe_out, NCH);
+    // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
+    const float r2 = vrms(xe, NCH, H, a.eps, red);
+#pragma unroll
+    for (int j = 0; j < kVecChunks; ++j) {
+      const int c = tid + 256 * j;
+      if (c < NCH) {
+        float f[8], g[8];
+        unpack8(xe.c[j], f);
+        unpack8(ld16((const u32x4*)a.r_scale + c), g);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r2) * g[q]) * a.r_c);
+        u32x4 v;
+        v.x = pack2(f[0], f[1]); v.y = pack2(f[2], f[3]); v.z = pack2(f[4], f[5]); v.w = pack2(f[6], f[7]);
+        xs[c] = v;
+      }
+    }
+  }
+  __syncthreads();
+  if (row < 0) return;
+  if (dense) {
+    const float acc = dot_row<32, IT>(w, xs, l);
+    const float up = __shfl(acc, 32, kWave);
+    if (lane == 0) a.act_mlp[row] = f2bf(rbf(gelu_tanh(rbf(acc))) * rbf(up));
+  } else {
+    double d0 = 0.0, d1 = 0.0;
+#pragma unroll
+    for (int i = 0; i < IT; ++i) {
+      if (i & 1) d1 = dot8_f64(w[i], xs[l + 32 * i], d1);
+      else d0 = dot8_f64(w[i], xs[l + 32 * i], d0);
+    }
+    const double acc = group_sum_f64<32>(d0 + d1);
+    if (l == 0) a.scores[row] = rbf((float)acc);
+  }
+}
+
+// ------------------------------------------------------------------ ffn_out
+// One wave per output row h: the dense down row (I values, 64 lanes) and the
+// k selected experts' down rows (8 lanes per expert slot, FIT = F/64 chunks).
+struct FfnOutArgs {
+  const uint16_t* act_mlp;  // [I]
+  const uint16_t* down;     // [H, I]
+  int I;
+  uint16_t* mlp_out;        // [H]
+  const uint16_t* act_moe;  // [k, F]
+  const uint16_t* e_down;   // [E, H, F] (null: no MoE)
+  const int32_t* top_i;     // [k]
+  int E, K;
+  int bf16_running;
+  uint16_t* moe_out;        // [H]
+  int H;
+};
+
+template <int FIT>
+__global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
+  constexpr int F = FIT * 64;
+  extern __shared__ u32x4 act_lds[];  // I/8 chunks
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int h = blockIdx.x * 4 + wave;
+  const int ich = a.I / 8;
+  constexpr int DIT = 8;  // dense chunks per lane, at most (I <= 4096)
+  u32x4 wd[DIT];
+  const bool hv = h < a.H;
+  if (hv) {
+    const u32x4* drow = (const u32x4*)(a.down + (size_t)h * a.I);
+#pragma unroll
+    for (int i = 0; i < DIT; ++i) {
+      const int c = lane + 64 * i;
+      wd[i] = (c < ich) ? ld_stream(drow + c) : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // expert rows: lane group g = slot, 8 lanes, FIT chunks each
+  const int g = lane >> 3, l8 = lane & 7;
+  u32x4 we[FIT];
+  int e = -1;
+  if (a.e_down != nullptr && hv && g < a.K) {
+    e = a.top_i[g];
+    if (e >= 0 && e < a.E) {
+      const u32x4* erow = (const u32x4*)(a.e_down + ((size_t)e * a.H + h) * F);
+#pragma unroll
+      for (int i = 0; i < FIT; ++i) we[i] = ld_stream(erow + l8 + 8 * i);
+    } else {
+      e = -1;
+    }
+  }
+  for (int c = tid; c < ich; c += 256) act_lds[c] = ld16((const u32x4*)a.act_mlp + c);
+  __syncthreads();
+  if (!hv) return;
+  float acc = 0.0f;
+#pragma unroll
+  for (int i = 0; i < DIT; ++i) {
+    const int c = lane + 64 * i;
+    if (c < ich) acc = dot8(wd[i], act_lds[c], acc);
+  }
+  acc = group_sum<64>(acc);
+  if (lane == 0) a.mlp_out[h] = f2bf(acc);
+  if (a.e_down == nullptr) return;
+  float part = 0.0f;
+  if (e >= 0) {
+    const u32x4* av = (const u32x4*)(a.act_moe + (size_t)g * F);
+#pragma unroll
+    for (int i = 0; i < FIT; ++i) part = dot8(we[i], ld16(av + l8 + 8 * i), part);
+  }
+  part = group_sum<8>(part);
+  float run = 0.0f;
+  for (int q = 0; q < a.K && q < 8; ++q) {
+    const float pq = __shfl(part, 8 * q, kWave);
+    if (a.bf16_running) run = (q == 0) ? rbf(pq) : rbf(run + rbf(pq));
+    else run = (q == 0) ? pq : run + pq;
+  }
+  if (lane == 0) a.moe_out[h] = f2bf(run);
+}
+
+// ------------------------------------------------------------------ lm_head
+struct LmArgs {
+  TailArgs tail;
+  const uint16_t* w_norm;   // final norm
+  const uint16_t* embed;    // [V, H]
+  int V;
+  float softcap;            // 0 = off
+  float* logits;            // [V] f32
+  float* blk_val;           // [nblocks]
+  int32_t* blk_idx;
+  int rows_per_block;
+  int H;
+  float eps;
+};
+
+__device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+template <int IT>
+__global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
+  constexpr int H = IT * 256;
+  constexpr int NCH = H / 8;
+  __shared__ u32x4 xs[NCH];
+  __shared__ double red[4];
+  __shared__ float bvs[8];
+  __shared__ int bis[8];
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const int r0 = blockIdx.x * a.rows_per_block;
+  const int r1 = min(a.V, r0 + a.rows_per_block);
+  // first row pair of this wave, loads issued before the prologue
+  int r = r0 + wave * 2 + half;
+  u32x4 w[IT];
+  if (r < r1) load_row<32, IT>(a.embed + (size_t)r * H, l, w);
+  Vec x;
+  tail_vec(x, a.tail, NCH, H, a.eps, red);
+  const float rn = vrms(x, NCH, H, a.eps, red);
+  vscale(x, rn, a.w_norm, NCH);
+  vstore(x, xs, NCH);
+  __syncthreads();
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  const float cap = a.softcap;
+  for (; r - half < r1; r += 8) {
+    u32x4 wn[IT];
+    const int rn2 = r + 8;
+    if (rn2 < r1) load_row<32, IT>(a.embed + (size_t)rn2 * H, l, wn);
+    if (r < r1) {
+      const float acc = dot_row<32, IT>(w, xs, l);
+      float v = rbf(acc);
+      if (cap > 0.0f) v = tanhf(v / cap) * cap;
+      if (l == 0) {
+        a.logits[r] = v;
+        better(bv, bi, v, r);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = wn[i];
+  }
+  // lanes 0 and 32 hold their half's best
+  if (l == 0) {
+    bvs[wave * 2 + half] = bv;
+    bis[wave * 2 + half] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    float v = bvs[0];
+    int i = bis[0];
+    for (int q = 1; q < 8; ++q) better(v, i, bvs[q], bis[q]);
+    a.blk_val[blockIdx.x] = v;
+    a.blk_idx[blockIdx.x] = i;
+  }
+}
+
+// One block: token = argmax over the per-block maxima (value desc, index asc).
+// Writes tok[0]; when pos != null advances pos[0] and stores the token at
+// hist[new pos] (hist_len entries, ignored past the end).
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ blk_val,
+                                                     const int32_t* __restrict__ blk_idx, int n, int32_t* tok,
+                                                     int32_t* pos, int32_t* hist, int hist_len) {
+  __shared__ float vs[256];
+  __shared__ int is[256];
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int j = threadIdx.x; j < n; j += 256) better(bv, bi, blk_val[j], blk_idx[j]);
+  vs[threadIdx.x] = bv;
+  is[threadIdx.x] = bi;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if ((int)threadIdx.x < s) {
+      float v = vs[threadIdx.x];
+      int i = is[threadIdx.x];
+      better(v, i, vs[threadIdx.x + s], is[threadIdx.x + s]);
+      vs[threadIdx.x] = v;
+      is[threadIdx.x] = i;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const int t = is[0];
+    tok[0] = t;
+    if (pos != nullptr) {
+      const int p = pos[0] + 1;
+      pos[0] = p;
+      if (hist != nullptr && p >= 0 && p < hist_len) hist[p] = t;
+    }
+  }
+}
+
+static float bf16_round_host(double v) {
+  float f = (float)v;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+}  // namespace g4mi
+
+using namespace g4mi;
+
+#define G4MI_IT16(M) M(1) M(2) M(3) M(4) M(5) M(6) M(7) M(8) M(9) M(10) M(11) M(12) M(13) M(14) M(15) M(16)
+
+extern "C" {
+
+int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64_t vocab, const uint16_t* x_in,
+                  const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
+                  const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                  const uint16_t* input_ln, uint16_t* x_out, const uint16_t* wq, int64_t q_rows, const uint16_t* wk,
+                  int64_t k_rows, const uint16_t* wv, int64_t v_rows, uint16_t* qkv_out, int64_t H, float eps,
+                  void* stream) {
+  G4MI_REQUIRE(mode >= 0 && mode <= 2, G4MI_EINVAL, "layer_in: bad mode %d", mode);
+  G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
+               "layer_in: H=%lld must be 256*i, i <= 16", (long long)H);
+  G4MI_REQUIRE(input_ln && x_out && qkv_out && wq && q_rows >= 1 && k_rows >= 0 && v_rows >= 0, G4MI_EINVAL,
+               "layer_in: missing argument");
+  G4MI_REQUIRE(mode != 0 || (tok && embed && vocab >= 1), G4MI_EINVAL, "layer_in: embed mode needs tok/embed");
+  G4MI_REQUIRE(mode != 1 || (x1 && mlp_out && post_ff_ln && layer_scalar), G4MI_EINVAL,
+               "layer_in: tail mode needs x1/mlp_out/post_ff_ln/layer_scalar");
+  G4MI_REQUIRE(mode != 1 || moe_out == nullptr || (post_ff1_ln && post_ff2_ln), G4MI_EINVAL,
+               "layer_in: tail mode with MoE needs post_feedforward_layernorm_1/2");
+  G4MI_REQUIRE(mode != 2 || x_in, G4MI_EINVAL, "layer_in: plain mode needs x_in");
+  G4MI_REQUIRE((k_rows == 0 || wk) && (v_rows == 0 || wv), G4MI_EINVAL, "layer_in: missing k/v weights");
+  InArgs a;
+  a.mode = mode; a.tok = tok; a.embed = embed; a.vocab = (int)vocab;
+  a.embed_c = bf16_round_host((double)(float)sqrt((double)H));
+  a.x_in = x_in;
+  a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
+  a.w_in = input_ln; a.x_out = x_out;
+  a.W[0] = wq; a.W[1] = wk; a.W[2] = wv;
+  a.rows[0] = (int)q_rows; a.rows[1] = (int)k_rows; a.rows[2] = (int)v_rows;
+  a.out = qkv_out; a.H = (int)H; a.eps = eps;
+  const int total = (int)(q_rows + k_rows + v_rows);
+  dim3 grid((unsigned)((total + 7) / 8));
+  hipStream_t st = as_stream(stream);
+  switch (H / 256) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL(layer_in_kernel<I>, grid, dim3(256), 0, st, a); break;
+    G4MI_IT16(G4MI_C)
+#undef G4MI_C
+  }
+  return check_launch("layer_in");
+}
+
+int g4mi_oproj(const uint16_t* ctx, const uint16_t* w, int64_t rows, int64_t K, uint16_t* out, void* stream) {
+  G4MI_REQUIRE(ctx && w && out && rows >= 1, G4MI_EINVAL, "oproj: missing argument");
+  hipStream_t st = as_stream(stream);
+  if (K % 512 == 0 && K / 512 >= 1 && K / 512 <= 16) {
+    dim3 grid((unsigned)((rows + 3) / 4));
+    switch (K / 512) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<64, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, out); break;
+      G4MI_IT16(G4MI_C)
+#undef G4MI_C
+    }
+  } else if (K % 256 == 0 && K / 256 <= 16) {
+    dim3 grid((unsigned)((rows + 7) / 8));
+    switch (K / 256) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<32, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, out); break;
+      G4MI_IT16(G4MI_C)
+#undef G4MI_C
+    }
+  } else {
+    G4MI_REQUIRE(false, G4MI_EUNSUPPORTED, "oproj: K=%lld must be 512*i or 256*i (i <= 16)", (long long)K);
+  }
+  return check_launch("oproj");
+}
+
+int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_ln, const uint16_t* pre_ff_ln,
+                const uint16_t* pre_ff2_ln, uint16_t* x1_out, uint16_t* xe_out, const uint16_t* gate,
+                const uint16_t* up, int64_t I, uint16_t* act_mlp, const uint16_t* router_scale,
+                const uint16_t* router_proj, int64_t E, float* scores, int64_t H, float eps, void* stream) {
+  G4MI_REQUIRE(x && o && post_attn_ln && pre_ff_ln && x1_out && gate && up && act_mlp && I >= 1, G4MI_EINVAL,
+               "ffn_in: missing argument");
+  G4MI_REQUIRE(router_proj == nullptr || (router_scale && pre_ff2_ln && xe_out && scores && E >= 1 && E <= 65536),
+               G4MI_EINVAL, "ffn_in: router needs scale, pre_ff_2 norm, xe_out and scores");
+  G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
+               "ffn_in: H=%lld must be 256*i, i <= 16", (long long)H);
+  FfnInArgs a;
+  a.x = x; a.o = o; a.w_pa = post_attn_ln; a.w_pf = pre_ff_ln; a.w_pf2 = pre_ff2_ln;
+  a.x1_out = x1_out; a.xe_out = xe_out; a.gate = gate; a.up = up; a.I = (int)I; a.act_mlp = act_mlp;
+  a.dense_blocks = (int)((I + 3) / 4);
+  a.r_scale = router_scale; a.r_proj = router_proj; a.E = router_proj ? (int)E : 0;
+  a.r_c = bf16_round_host(1.0 / sqrt((double)H));
+  a.scores = scores; a.H = (int)H; a.eps = eps;
+  const int rblocks = router_proj ? (int)((E + 7) / 8) : 0;
+  dim3 grid((unsigned)(a.dense_blocks + rblocks));
+  hipStream_t st = as_stream(stream);
+  switch (H / 256) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL(ffn_in_kernel<I>, grid, dim3(256), 0, st, a); break;
+    G4MI_IT16(G4MI_C)
+#undef G4MI_C
+  }
+  return check_launch("ffn_in");
+}
+
+int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint16_t* mlp_out,
+                 const uint16_t* act_moe, const uint16_t* experts_down, const int32_t* top_i, int64_t E, int64_t k,
+                 int64_t F, int32_t combine, uint16_t* moe_out, int64_t H, void* stream) {
+  G4MI_REQUIRE(act_mlp && down && mlp_out && H >= 1, G4MI_EINVAL, "ffn_out: missing argument");
+  G4MI_REQUIRE(I % 8 == 0 && I >= 8 && I <= 4096, G4MI_EUNSUPPORTED, "ffn_out: I=%lld must be 8*i <= 4096",
+               (long long)I);
+  G4MI_REQUIRE(experts_down == nullptr || (act_moe && top_i && moe_out && k >= 1 && k <= 8 && E >= 1), G4MI_EINVAL,
+               "ffn_out: expert path needs act_moe/top_i/moe_out and 1 <= k <= 8");
+  G4MI_REQUIRE(experts_down == nullptr || (F % 64 == 0 && F / 64 >= 1 && F / 64 <= 16), G4MI_EUNSUPPORTED,
+               "ffn_out: F=%lld must be 64*i, i <= 16", (long long)F);
+  G4MI_REQUIRE(combine == G4MI_COMBINE_BF16_RUNNING || combine == G4MI_COMBINE_F32, G4MI_EINVAL,
+               "ffn_out: unknown combine mode %d", combine);
+  FfnOutArgs a;
+  a.act_mlp = act_mlp; a.down = down; a.I = (int)I; a.mlp_out = mlp_out;
+  a.act_moe = act_moe; a.e_down = experts_down; a.top_i = top_i; a.E = (int)E; a.K = (int)k;
+  a.bf16_running = combine == G4MI_COMBINE_BF16_RUNNING; a.moe_out = moe_out; a.H = (int)H;
+  dim3 grid((unsigned)((H + 3) / 4));
+  const size_t lds = (size_t)(I / 8) * 16;
+  hipStream_t st = as_stream(stream);
+  const int fit = experts_down ? (int)(F / 64) : 1;
+  switch (fit) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL(ffn_out_kernel<I>, grid, dim3(256), lds, st, a); break;
+    G4MI_IT16(G4MI_C)
+#undef G4MI_C
+  }
+  return check_launch("ffn_out");
+}
+
+int64_t g4mi_lm_head_blocks(int64_t V) { return (V + 255) / 256; }
+
+int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
+                 const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                 const uint16_t* final_norm, const uint16_t* embed, int64_t V, int64_t H, float softcap, float eps,
+                 float* logits, float* blk_val, int32_t* blk_idx, void* stream) {
+  G4MI_REQUIRE(x1 && mlp_out && post_ff_ln && layer_scalar && final_norm && embed && logits && blk_val && blk_idx,
+               G4MI_EINVAL, "lm_head: missing argument");
+  G4MI_REQUIRE(moe_out == nullptr || (post_ff1_ln && post_ff2_ln), G4MI_EINVAL,
+               "lm_head: MoE tail needs post_feedforward_layernorm_1/2");
+  G4MI_REQUIRE(V >= 1 && V <= (int64_t)1 << 30, G4MI_EINVAL, "lm_head: bad vocab");
+  G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
+               "lm_head: H=%lld must be 256*i, i <= 16", (long long)H);
+  LmArgs a;
+  a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
+  a.w_norm = final_norm; a.embed = embed; a.V = (int)V; a.softcap = softcap; a.logits = logits;
+  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = 256; a.H = (int)H; a.eps = eps;
+  dim3 grid((unsigned)g4mi_lm_head_blocks(V));
+  hipStream_t st = as_stream(stream);
+  switch (H / 256) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL(lmhead_kernel<I>, grid, dim3(256), 0, st, a); break;
+    G4MI_IT16(G4MI_C)
+#undef G4MI_C
+  }
+  return check_launch("lm_head");
+}
+
+int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n, int32_t* tok, int32_t* pos,
+                         int32_t* hist, int64_t hist_len, void* stream) {
+  G4MI_REQUIRE(blk_val && blk_idx && tok && n >= 1, G4MI_EINVAL, "argmax_finalize: missing argument");
+  hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, as_stream(stream), blk_val, blk_idx, (int)n, tok, pos,
+                     hist, (int)hist_len);
+  return check_launch("argmax_finalize");
+}
+
+}  // extern "C"

@@ -43,6 +43,34 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _i64, _p],
     ),
     "g4mi_moe_block_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "g4mi_attention_min_splits": (_i64, [_i64]),
+    "g4mi_decode_attention_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "g4mi_decode_attention": (
+        _int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
+         _i32, _i64, _i64, _p, _p, _i64, _p],
+    ),
+    "g4mi_layer_in": (
+        _int,
+        [_i32, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _p, _i64, _f32,
+         _p],
+    ),
+    "g4mi_oproj": (_int, [_p, _p, _i64, _i64, _p, _p]),
+    "g4mi_ffn_in": (
+        _int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _f32, _p],
+    ),
+    "g4mi_ffn_out": (_int, [_p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p]),
+    "g4mi_lm_head_blocks": (_i64, [_i64]),
+    "g4mi_lm_head": (
+        _int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
+    ),
+    "g4mi_argmax_finalize": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p]),
+    "g4mi_kv_append": (
+        _int,
+        [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p],
+    ),
     "g4mi_moe_block_decode": (
         _int,
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p, _p, _p, _p, _i64, _p],

@@ -62,3 +62,267 @@ def cache_shapes(cfg: TextConfig, batch: int, max_len: int) -> list[tuple[int, .
 def cache_bytes(cfg: TextConfig, batch: int, max_len: int) -> int:
     """bf16 bytes of the K and V caches (model.py:188-189)."""
     return sum(2 * 2 * math.prod(s) for s in cache_shapes(cfg, batch, max_len))
+
+
+# --------------------------------------------------------------------- RoPE
+def rope_inv_freq(head_dim: int, theta: float, partial_rotary_factor: float = 1.0):
+    """Inverse frequencies (model.py:54-61): theta^(-2i/d) computed in f64 for
+    the rotated pairs, zero for the NoPE tail of a partial rotation, as f32."""
+    import numpy as np
+
+    n_rot = int(partial_rotary_factor * head_dim // 2)
+    inv = np.zeros(head_dim // 2, dtype=np.float64)
+    if n_rot:
+        inv[:n_rot] = 1.0 / (theta ** (np.arange(n_rot, dtype=np.float64) * 2.0 / head_dim))
+    return inv.astype(np.float32)
+
+
+def rope_table(head_dim: int, theta: float, partial: float, max_pos: int, device="cuda"):
+    """(cos, sin) bf16 tables [max_pos, head_dim/2] of the angles
+    f32(pos) * inv_freq (f32 product, model.py:65); each entry is the f64
+    cosine/sine of that f32 angle rounded to f32, then to bf16 (the reference
+    casts the tables to the activation dtype in apply_rope, model.py:76-77).
+    The duplicated second half of the reference's table is not stored."""
+    import numpy as np
+
+    inv = rope_inv_freq(head_dim, theta, partial)
+    ang = (np.arange(max_pos, dtype=np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    cos = torch.from_numpy(np.cos(ang.astype(np.float64)).astype(np.float32))
+    sin = torch.from_numpy(np.sin(ang.astype(np.float64)).astype(np.float32))
+    return cos.to(torch.bfloat16).to(device), sin.to(torch.bfloat16).to(device)
+
+
+# --------------------------------------------------------------------- cache
+PAGE_SIZE = 64
+
+
+def init_cache(cfg: TextConfig, mesh=None, batch: int = 1, max_len: int = 4096, dtype=torch.bfloat16,
+               device="cuda", page_size: int = PAGE_SIZE) -> dict:
+    """Zero K and V caches, one pair per layer (model.py:178-185), stored as
+    pages: k[i], v[i] are [batch*max_pages, KV, PAGE, D] bf16 and
+    cache["page_table"] [batch, max_pages] int32 maps position p of sequence
+    b to page page_table[b, p // PAGE].  `mesh` is accepted for signature
+    compatibility (one GPU, no mesh)."""
+    if dtype != torch.bfloat16:
+        raise ValueError("the cache is bf16")
+    max_pages = (max_len + page_size - 1) // page_size
+    pools_k, pools_v = [], []
+    for lt in cfg.layer_types:
+        shape = (batch * max_pages, cfg.kv_heads_for(lt), page_size, cfg.head_dim_for(lt))
+        pools_k.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
+        pools_v.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
+    pt = torch.arange(batch * max_pages, dtype=torch.int32, device=device).reshape(batch, max_pages)
+    return {"k": pools_k, "v": pools_v, "page_table": pt, "page_size": page_size, "max_len": max_len,
+            "batch": batch}
+
+
+def cache_positions(cache: dict, layer: int, batch: int = 0, upto: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """The logical [max_len, KV, D] K and V of one layer and sequence (for tests
+    and inspection): pages gathered through the page table."""
+    pt = cache["page_table"][batch].long()
+    kp, vp = cache["k"][layer], cache["v"][layer]
+    n, kv, page, d = kp.shape
+    k = kp[pt].permute(0, 2, 1, 3).reshape(-1, kv, d)
+    v = vp[pt].permute(0, 2, 1, 3).reshape(-1, kv, d)
+    upto = cache["max_len"] if upto is None else upto
+    return k[:upto], v[:upto]
+
+
+# --------------------------------------------------------------------- masks
+def prefill_masks(cfg: TextConfig, t: int, prompt_len) -> dict:
+    """Causal masks of a t-token prefill (model.py:392-399): kv <= q, kv <
+    prompt_len, and kv > q - window on sliding layers.  The kernels apply the
+    same predicates implicitly; the dict also carries `prompt_len`."""
+    q = torch.arange(t)[:, None]
+    kv = torch.arange(t)[None, :]
+    p = int(prompt_len)
+    valid = (kv <= q) & (kv < p)
+    return {FULL: valid[None, None, None], SLIDING: (valid & (kv > q - cfg.sliding_window))[None, None, None],
+            "prompt_len": p}
+
+
+def decode_masks(cfg: TextConfig, max_len: int, pos) -> dict:
+    """Decode masks at position pos (model.py:402-408)."""
+    kv = torch.arange(max_len)[None, :]
+    p = int(pos)
+    valid = kv <= p
+    return {FULL: valid[None, None, None], SLIDING: (valid & (kv > p - cfg.sliding_window))[None, None, None],
+            "pos": p}
+
+
+# --------------------------------------------------------------------- decode step
+class DecodeRunner:
+    """Launches one batch-1 token step of the model on the current stream.
+
+    Per layer: layer_in (tail of the previous layer + input norm + q/k/v),
+    decode attention (append + scores + pv + reduce), o_proj, ffn_in
+    (post-attention norm + dense gate/up + router scores), routed expert
+    gate/up, ffn_out (dense and expert down + combine); then lm_head and the
+    greedy argmax.  All buffers are allocated once, so a step can be captured
+    in a HIP graph and replayed; the token and position live in device
+    memory (`tok`, `pos`)."""
+
+    def __init__(self, cfg: TextConfig, params: dict, cache: dict, device="cuda", hist_len: int | None = None):
+        from . import ops
+
+        self.ops = ops
+        self.cfg, self.params, self.cache = cfg, params, cache
+        self.device = torch.device(device)
+        dev = self.device
+        H = cfg.hidden_size
+        self.max_len = cache["max_len"]
+        self.page_table = cache["page_table"][0:1].contiguous()
+        self.layers = [{k[len(f"layers.{i}."):]: v for k, v in params.items() if k.startswith(f"layers.{i}.")}
+                       for i in range(cfg.num_hidden_layers)]
+        bf = torch.bfloat16
+        qkv_max = max(cfg.num_attention_heads * cfg.head_dim_for(lt) + 2 * cfg.kv_heads_for(lt) * cfg.head_dim_for(lt)
+                      for lt in cfg.layer_types)
+        ctx_max = max(cfg.num_attention_heads * cfg.head_dim_for(lt) for lt in cfg.layer_types)
+        z = lambda n, dt=bf: torch.zeros(n, dtype=dt, device=dev)  # noqa: E731
+        self.x, self.x1, self.xe, self.o = z(H), z(H), z(H), z(H)
+        self.mlp_out, self.moe_out = z(H), z(H)
+        self.qkv, self.ctx = z(qkv_max), z(ctx_max)
+        self.act_mlp = z(cfg.intermediate_size)
+        L = cfg.num_hidden_layers
+        if cfg.enable_moe_block:
+            self.act_moe = z(cfg.top_k_experts * cfg.moe_intermediate_size)
+            self.scores = z(cfg.num_experts, torch.float32)
+            self.top_w = z((L, cfg.top_k_experts), torch.float32)
+            self.top_i = z((L, cfg.top_k_experts), torch.int32)
+        self.logits = z(cfg.vocab_size, torch.float32)
+        nb = ops.lm_head_blocks(cfg.vocab_size)
+        self.blk_val, self.blk_idx = z(nb, torch.float32), z(nb, torch.int32)
+        self.tok = z(1, torch.int32)
+        self.pos = z(1, torch.int32)
+        self.hist = z(hist_len if hist_len is not None else self.max_len + 1, torch.int32)
+        # RoPE tables per layer type, and attention workspaces
+        self.rope = {
+            SLIDING: rope_table(cfg.head_dim, cfg.rope_theta_sliding, 1.0, self.max_len, dev),
+            FULL: rope_table(cfg.global_head_dim, cfg.rope_theta_full, cfg.rope_partial_rotary_factor_full,
+                             self.max_len, dev),
+        }
+        self.lmax = {SLIDING: min(cfg.sliding_window, self.max_len), FULL: self.max_len}
+        self.splits = {}
+        ws = 0
+        for lt in set(cfg.layer_types):
+            d = cfg.head_dim_for(lt)
+            lmax = self.max_len  # positions are addressed up to max_len on every layer
+            ns = self._splits(lt)
+            self.splits[lt] = ns
+            ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, cfg.num_attention_heads, d, lmax, ns))
+        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+
+    def _splits(self, lt: str) -> int:
+        cfg = self.cfg
+        kv = cfg.kv_heads_for(lt)
+        span = min(cfg.sliding_window, self.max_len) if lt == SLIDING else self.max_len
+        want = max(1, 256 // kv)  # ~256 blocks per KV pass at full length
+        need = self.ops.attention_min_splits(span)
+        return max(need, min(want, (span + 63) // 64))
+
+    def launch(self, combine: str = "bf16_running", advance: bool = True):
+        """Enqueues one token step reading tok/pos; with `advance` the argmax
+        kernel writes the next token to tok, increments pos and records the
+        token in hist[pos]."""
+        ops, cfg, p = self.ops, self.cfg, self.params
+        H, eps, NH = cfg.hidden_size, cfg.rms_norm_eps, cfg.num_attention_heads
+        moe = cfg.enable_moe_block
+        for i, lt in enumerate(cfg.layer_types):
+            lp = self.layers[i]
+            d, kv = cfg.head_dim_for(lt), cfg.kv_heads_for(lt)
+            q_rows, k_rows = NH * d, kv * d
+            v_rows = 0 if cfg.k_eq_v_for(lt) else kv * d
+            if i == 0:
+                ops.layer_in(0, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
+                             q_rows, k_rows, v_rows, self.qkv, tok=self.tok, embed=p["embed"])
+            else:
+                prev = self.layers[i - 1]
+                ops.layer_in(1, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
+                             q_rows, k_rows, v_rows, self.qkv, x1=self.x1, mlp_out=self.mlp_out,
+                             moe_out=self.moe_out if moe else None,
+                             post_ff1=prev.get("post_feedforward_layernorm_1"),
+                             post_ff2=prev.get("post_feedforward_layernorm_2"),
+                             post_ff=prev["post_feedforward_layernorm"], layer_scalar=prev["layer_scalar"])
+            q = self.qkv[:q_rows].view(1, NH, d)
+            k = self.qkv[q_rows:q_rows + k_rows].view(1, kv, d)
+            v = self.qkv[q_rows + k_rows:q_rows + k_rows + v_rows].view(1, kv, d) if v_rows else None
+            cos, sin = self.rope[lt]
+            ctx = self.ctx[:NH * d].view(1, NH, d)
+            ops.decode_attention(q, k, v, lp["q_norm"], lp["k_norm"], cos, sin, self.cache["k"][i],
+                                 self.cache["v"][i], self.page_table, self.pos,
+                                 cfg.sliding_window if lt == SLIDING else 0, cfg.attn_logit_softcapping, eps,
+                                 self.max_len, self.splits[lt], append=True, ctx=ctx, ws=self.attn_ws)
+            ops.oproj(self.ctx, lp["o_proj"], H, NH * d, self.o)
+            ops.ffn_in(self.x, self.o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
+                       lp.get("pre_feedforward_layernorm_2"), self.x1, self.xe, lp["mlp.gate_proj"],
+                       lp["mlp.up_proj"], self.act_mlp, lp.get("router.scale"), lp.get("router.proj"),
+                       self.scores if moe else None, H, eps)
+            if moe:
+                ops.moe_gateup_routed(self.xe.view(1, H), self.scores.view(1, -1), lp["router.per_expert_scale"],
+                                      lp["experts.gate_up_proj"], cfg.top_k_experts,
+                                      act=self.act_moe.view(1, cfg.top_k_experts, -1),
+                                      route=(self.top_w[i:i + 1], self.top_i[i:i + 1]))
+            ops.ffn_out(self.act_mlp, lp["mlp.down_proj"], self.mlp_out, self.act_moe if moe else None,
+                        lp.get("experts.down_proj"), self.top_i[i] if moe else None, cfg.top_k_experts, combine,
+                        self.moe_out if moe else None, H)
+        last = self.layers[-1]
+        ops.lm_head(self.x1, self.mlp_out, self.moe_out if moe else None, last.get("post_feedforward_layernorm_1"),
+                    last.get("post_feedforward_layernorm_2"), last["post_feedforward_layernorm"],
+                    last["layer_scalar"], p["norm"], p["embed"], cfg.final_logit_softcapping, eps, self.logits,
+                    self.blk_val, self.blk_idx)
+        ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos if advance else None,
+                            self.hist if advance else None)
+
+    def set_state(self, token: int, pos: int) -> None:
+        self.tok.fill_(int(token))
+        self.pos.fill_(int(pos))
+
+
+_RUNNERS: dict = {}
+
+
+def runner_for(cfg: TextConfig, params: dict, cache: dict) -> DecodeRunner:
+    """The DecodeRunner bound to this (params, cache) pair, built on first use."""
+    key = (id(params), id(cache["k"][0]))
+    r = _RUNNERS.get(key)
+    if r is None or r.params is not params or r.cache is not cache:
+        r = DecodeRunner(cfg, params, cache, device=cache["k"][0].device)
+        _RUNNERS.clear()
+        _RUNNERS[key] = r
+    return r
+
+
+def forward(cfg: TextConfig, mesh, params: dict, tokens, positions, cache: dict, write_at, masks: dict, kv_len: int,
+            dense_moe: bool, last_index=None):
+    """Logits for `tokens` [1, T] at `positions` (model.py:333-386); returns
+    (logits f32 [1, T or 1, V], cache).  The cache is updated in place (the
+    reference donates it) and returned.
+
+    Tokens are processed one position at a time with the decode kernels: row t
+    of the reference's causal prefill attends exactly the cached positions
+    <= t, so this equals the T x T masked prefill.  dense_moe selects the
+    dense-MoE contraction (one f32 sum over the experts, model.py:241-250)
+    instead of the decode path's bf16 running sum.  Padded prefill positions
+    (>= the masks' prompt_len) are skipped: the reference never attends them
+    and only last_index (< prompt_len) is read back."""
+    tok = torch.as_tensor(tokens).reshape(-1).tolist()
+    pos = torch.as_tensor(positions).reshape(-1).tolist()
+    if len(pos) != len(tok):
+        raise ValueError("tokens and positions differ in length")
+    n = len(tok)
+    if isinstance(masks, dict) and "prompt_len" in masks:
+        n = min(n, int(masks["prompt_len"]))
+    r = runner_for(cfg, params, cache)
+    combine = "f32" if dense_moe else "bf16_running"
+    keep = range(n) if last_index is None else [int(last_index)]
+    out = torch.empty((1, len(keep), cfg.vocab_size), dtype=torch.float32, device=r.device)
+    j = 0
+    for t in range(n):
+        if not 0 <= pos[t] < r.max_len:
+            raise ValueError(f"position {pos[t]} outside the cache (max_len {r.max_len})")
+        r.set_state(tok[t], pos[t])
+        r.launch(combine, advance=False)
+        if last_index is None or t == int(last_index):
+            out[0, j].copy_(r.logits)
+            j += 1
+    return out, cache

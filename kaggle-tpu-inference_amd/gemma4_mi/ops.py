@@ -260,3 +260,124 @@ def moe_gateup_routed(xn, scores, per_expert_scale, gate_up, k, act=None, route=
     _lib.call("g4mi_moe_gateup_routed", _ptr(xn), _ptr(scores), _ptr(per_expert_scale), _ptr(gate_up), n, h, f, e,
               k, _ptr(act), _ptr(top_w), _ptr(top_i), stream_handle(xn.device))
     return act, top_w, top_i
+
+
+# -------------------------------------------------------------------- attention
+def attention_min_splits(lmax: int) -> int:
+    return int(_lib.lib().g4mi_attention_min_splits(lmax))
+
+
+def decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table, pos,
+                     window, softcap, eps, lmax, n_split_max=None, append=True, ctx=None, ws=None):
+    """Split-K decode attention over the paged cache (model.py:197-213) for B
+    sequences: q_raw [B, NH, D], k_raw / v_raw [B, KV, D] (v_raw None on k==v
+    layers), pages [num_pages, KV, PAGE, D], page_table [B, max_pages],
+    pos [B] int32 (device).  Appends the new K/V at pos when `append`.
+    Returns ctx [B, NH, D] bf16."""
+    b, nh, d = q_raw.shape
+    num_pages, kv, page, d2 = k_pages.shape
+    if d2 != d:
+        raise ValueError("head_dim mismatch between q and the cache")
+    _need(q_raw, BF16, "q_raw")
+    if append:
+        _need(k_raw, BF16, "k_raw", (b, kv, d))
+        if v_raw is not None:
+            _need(v_raw, BF16, "v_raw", (b, kv, d))
+    _need(q_norm, BF16, "q_norm", (d,))
+    _need(k_norm, BF16, "k_norm", (d,))
+    _need(rope_cos, BF16, "rope_cos")
+    _need(rope_sin, BF16, "rope_sin", tuple(rope_cos.shape))
+    _need(k_pages, BF16, "k_pages")
+    _need(v_pages, BF16, "v_pages", tuple(k_pages.shape))
+    _need(page_table, torch.int32, "page_table")
+    _need(pos, torch.int32, "pos", (b,))
+    if rope_cos.shape[1] != d // 2 or rope_cos.shape[0] < lmax:
+        raise ValueError("rope tables must be [>= lmax, head_dim/2]")
+    max_pages = page_table.shape[1]
+    if page_table.shape[0] != b:
+        raise ValueError("page_table must have one row per sequence")
+    if n_split_max is None:
+        n_split_max = max(attention_min_splits(lmax), 1)
+    if ctx is None:
+        ctx = torch.empty((b, nh, d), dtype=BF16, device=q_raw.device)
+    _need(ctx, BF16, "ctx", (b, nh, d))
+    nbytes = _lib.lib().g4mi_decode_attention_workspace_bytes(b, nh, d, lmax, n_split_max)
+    if ws is None:
+        ws = WORKSPACE.get(q_raw.device, "attention", nbytes)
+    _lib.call("g4mi_decode_attention", _ptr(q_raw), _ptr(k_raw), _ptr(v_raw), _ptr(q_norm), _ptr(k_norm),
+              _ptr(rope_cos), _ptr(rope_sin), _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table), max_pages,
+              _ptr(pos), b, nh, kv, d, page, int(window), float(softcap or 0.0), float(eps), 1 if append else 0,
+              int(lmax), int(n_split_max), _ptr(ctx), _ptr(ws), ws.numel(), stream_handle(q_raw.device))
+    return ctx
+
+
+def kv_append(k_raw, v_raw, k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table_row, pos, lmax, eps):
+    """Writes rope(rms_norm(k_raw, k_norm)) and rms_norm(v_raw) of T tokens of
+    one sequence at positions pos [T] (model.py:202-206).  k_raw [T, KV, D]."""
+    t, kv, d = k_raw.shape
+    num_pages, kv2, page, d2 = k_pages.shape
+    if (kv2, d2) != (kv, d):
+        raise ValueError("cache geometry does not match k_raw")
+    _need(k_raw, BF16, "k_raw")
+    if v_raw is not None:
+        _need(v_raw, BF16, "v_raw", (t, kv, d))
+    _need(k_norm, BF16, "k_norm", (d,))
+    _need(k_pages, BF16, "k_pages")
+    _need(v_pages, BF16, "v_pages", tuple(k_pages.shape))
+    _need(page_table_row, torch.int32, "page_table_row")
+    _need(pos, torch.int32, "pos", (t,))
+    _lib.call("g4mi_kv_append", _ptr(k_raw), _ptr(v_raw), _ptr(k_norm), _ptr(rope_cos), _ptr(rope_sin),
+              _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table_row), page_table_row.numel(), _ptr(pos), t, kv,
+              d, page, int(lmax), float(eps), stream_handle(k_raw.device))
+
+
+# ------------------------------------------------------------------- layer ops
+def layer_in(mode, H, eps, input_ln, x_out, wq, wk, wv, q_rows, k_rows, v_rows, qkv_out, tok=None, embed=None,
+             x_in=None, x1=None, mlp_out=None, moe_out=None, post_ff1=None, post_ff2=None, post_ff=None,
+             layer_scalar=None):
+    """q/k/v projection of rms_norm(x, input_ln) with x from the embedding
+    (mode 0), the previous layer's tail (mode 1) or x_in (mode 2)."""
+    vocab = embed.shape[0] if embed is not None else 0
+    _lib.call("g4mi_layer_in", int(mode), _ptr(tok), _ptr(embed), vocab, _ptr(x_in), _ptr(x1), _ptr(mlp_out),
+              _ptr(moe_out), _ptr(post_ff1), _ptr(post_ff2), _ptr(post_ff), _ptr(layer_scalar), _ptr(input_ln),
+              _ptr(x_out), _ptr(wq), q_rows, _ptr(wk), k_rows, _ptr(wv), v_rows, _ptr(qkv_out), H, float(eps),
+              stream_handle(x_out.device))
+
+
+def oproj(ctx, w, rows, K, out):
+    _lib.call("g4mi_oproj", _ptr(ctx), _ptr(w), rows, K, _ptr(out), stream_handle(out.device))
+
+
+def ffn_in(x, o, post_attn_ln, pre_ff_ln, pre_ff2_ln, x1_out, xe_out, gate, up, act_mlp, router_scale, router_proj,
+           scores, H, eps):
+    I = gate.shape[0]
+    E = router_proj.shape[0] if router_proj is not None else 0
+    _lib.call("g4mi_ffn_in", _ptr(x), _ptr(o), _ptr(post_attn_ln), _ptr(pre_ff_ln), _ptr(pre_ff2_ln), _ptr(x1_out),
+              _ptr(xe_out), _ptr(gate), _ptr(up), I, _ptr(act_mlp), _ptr(router_scale), _ptr(router_proj), E,
+              _ptr(scores), H, float(eps), stream_handle(x.device))
+
+
+def ffn_out(act_mlp, down, mlp_out, act_moe, experts_down, top_i, k, combine, moe_out, H):
+    I = down.shape[1]
+    E = experts_down.shape[0] if experts_down is not None else 0
+    F = experts_down.shape[2] if experts_down is not None else 0
+    mode = {"bf16_running": _lib.COMBINE_BF16_RUNNING, "f32": _lib.COMBINE_F32}[combine]
+    _lib.call("g4mi_ffn_out", _ptr(act_mlp), _ptr(down), I, _ptr(mlp_out), _ptr(act_moe), _ptr(experts_down),
+              _ptr(top_i), E, k, F, mode, _ptr(moe_out), H, stream_handle(mlp_out.device))
+
+
+def lm_head_blocks(V: int) -> int:
+    return int(_lib.lib().g4mi_lm_head_blocks(V))
+
+
+def lm_head(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, final_norm, embed, softcap, eps,
+            logits, blk_val, blk_idx):
+    V, H = embed.shape
+    _lib.call("g4mi_lm_head", _ptr(x1), _ptr(mlp_out), _ptr(moe_out), _ptr(post_ff1), _ptr(post_ff2),
+              _ptr(post_ff), _ptr(layer_scalar), _ptr(final_norm), _ptr(embed), V, H, float(softcap or 0.0),
+              float(eps), _ptr(logits), _ptr(blk_val), _ptr(blk_idx), stream_handle(embed.device))
+
+
+def argmax_finalize(blk_val, blk_idx, tok, pos=None, hist=None):
+    _lib.call("g4mi_argmax_finalize", _ptr(blk_val), _ptr(blk_idx), blk_val.numel(), _ptr(tok), _ptr(pos),
+              _ptr(hist), 0 if hist is None else hist.numel(), stream_handle(tok.device))

@@ -169,29 +169,38 @@ def init_cache(cfg, batch: int, max_len: int) -> dict:
 
 
 # ----------------------------------------------------------------- blocks
-def attention(cfg, lp, x, layer_type, cos, sin, cache_k, cache_v, write_at, mask, kv_len, precise=True):
-    """model.py:195-215.  x [B,T,H] bf16 (input_layernorm output); mask bool
-    broadcastable to [B,KV,G,T,kv_len].  Returns (out [B,T,H], cache_k, cache_v)."""
-    eps = cfg.rms_norm_eps
-    q = ein("bth,kgdh->btkgd", x, lp["q_proj"], precise)
-    q = apply_rope(rms_norm(q, lp["q_norm"], eps), cos, sin)
-    k_raw = ein("bth,kdh->btkd", x, lp["k_proj"], precise)
-    v_raw = k_raw if cfg.k_eq_v_for(layer_type) else ein("bth,kdh->btkd", x, lp["v_proj"], precise)
-    k = apply_rope(rms_norm(k_raw, lp["k_norm"], eps), cos, sin)
+def attention_core(q, k_raw, v_raw, q_norm, k_norm, cos, sin, cache_k, cache_v, write_at, mask, kv_len, eps,
+                   softcap=None, precise=True):
+    """model.py:198-213 from the raw projections on: q [B,T,KV,G,D], k_raw/v_raw
+    [B,T,KV,D] bf16 (v_raw is k_raw on k==v layers).  Returns (ctx
+    [B,T,KV,G,D] bf16, cache_k, cache_v)."""
+    q = apply_rope(rms_norm(q, q_norm, eps), cos, sin)
+    k = apply_rope(rms_norm(k_raw, k_norm, eps), cos, sin)
     v = rms_norm(v_raw, None, eps)
-    t = x.shape[1]
+    t = q.shape[1]
     cache_k = cache_k.clone()
     cache_v = cache_v.clone()
     cache_k[:, write_at : write_at + t] = k
     cache_v[:, write_at : write_at + t] = v
     kk, vv = cache_k[:, :kv_len], cache_v[:, :kv_len]
     scores = f32(ein("btkgd,bskd->bkgts", q, kk, precise))
-    cap = getattr(cfg, "attn_logit_softcapping", None)
-    if cap:
-        scores = torch.tanh(scores / np.float32(cap)) * np.float32(cap)
+    if softcap:
+        scores = torch.tanh(scores / np.float32(softcap)) * np.float32(softcap)
     scores = torch.where(torch.as_tensor(mask), scores, torch.tensor(NEG_INF, dtype=torch.float32))
     probs = rb(torch.softmax(scores, dim=-1))
     ctx = ein("bkgts,bskd->btkgd", probs, vv, precise)
+    return ctx, cache_k, cache_v
+
+
+def attention(cfg, lp, x, layer_type, cos, sin, cache_k, cache_v, write_at, mask, kv_len, precise=True):
+    """model.py:195-215.  x [B,T,H] bf16 (input_layernorm output); mask bool
+    broadcastable to [B,KV,G,T,kv_len].  Returns (out [B,T,H], cache_k, cache_v)."""
+    q = ein("bth,kgdh->btkgd", x, lp["q_proj"], precise)
+    k_raw = ein("bth,kdh->btkd", x, lp["k_proj"], precise)
+    v_raw = k_raw if cfg.k_eq_v_for(layer_type) else ein("bth,kdh->btkd", x, lp["v_proj"], precise)
+    ctx, cache_k, cache_v = attention_core(q, k_raw, v_raw, lp["q_norm"], lp["k_norm"], cos, sin, cache_k, cache_v,
+                                           write_at, mask, kv_len, cfg.rms_norm_eps,
+                                           getattr(cfg, "attn_logit_softcapping", None), precise)
     out = ein("btkgd,hkgd->bth", ctx, lp["o_proj"], precise)
     return out, cache_k, cache_v
 

@@ -1,0 +1,169 @@
+"""GPU parity of split-K decode attention over the paged cache against the
+CPU oracle (model.py:197-213 restated in oracle/twin.py).
+
+Cases: small shapes with shuffled page tables, full and sliding masks, two
+sequences at different positions; k==v with softcap; and the two isolated
+attention workloads at 32K positions (sliding window 1024 with 16 q / 8 KV
+heads at head_dim 256; full k==v with 16 q / 2 KV heads at head_dim 512;
+RoPE applied, softcap 50, seed 2).
+
+Tolerances: the appended K/V rows are bit-exact (same deterministic norm and
+RoPE recipe); ctx (bf16) has corr >= 0.9999, every element within 2^-7 of
+the output's max magnitude and >= 95% of elements bit-identical (the GPU
+accumulates dots in f32 in another order than the oracle's f64, which moves
+some bf16-rounded probabilities by one ulp).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from gemma4_mi import model as gm
+from gemma4_mi import ops
+from gemma4_mi.weights import tensor_key
+from oracle import twin
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _gen(shape, seed, name, std=1.0):
+    t = torch.empty(shape, dtype=torch.bfloat16, device=DEV)
+    ops.fill_normal_(t, tensor_key(seed, name), std)
+    return t
+
+
+def _pages_from_contig(contig, page, perm, num_pages):
+    """contig [lmax, KV, D] -> pages [num_pages, KV, page, D] through perm."""
+    lmax, kv, d = contig.shape
+    pages = torch.zeros((num_pages, kv, page, d), dtype=torch.bfloat16, device=contig.device)
+    for i in range((lmax + page - 1) // page):
+        blk = contig[i * page: (i + 1) * page]
+        pages[perm[i], :, : blk.shape[0]] = blk.permute(1, 0, 2)
+    return pages
+
+
+def _contig_from_pages(pages, page, perm, lmax):
+    num, kv, _, d = pages.shape
+    out = torch.empty((lmax, kv, d), dtype=pages.dtype, device=pages.device)
+    for i in range((lmax + page - 1) // page):
+        n = min(page, lmax - i * page)
+        out[i * page: i * page + n] = pages[perm[i], :, :n].permute(1, 0, 2)
+    return out
+
+
+def _check(got, exp, what, min_same=0.95):
+    g = got.float().cpu().numpy().ravel()
+    e = exp.float().cpu().numpy().ravel()
+    scale = float(np.abs(e).max())
+    err = np.abs(g - e)
+    corr = float(np.corrcoef(g, e)[0, 1])
+    same = float(np.mean(got.cpu().view(torch.int16).numpy().ravel() == exp.cpu().view(torch.int16).numpy().ravel()))
+    print(f"{what}: max|d|={err.max():.3e} scale={scale:.3e} corr={corr:.7f} bit-identical={same:.4f}")
+    assert corr >= 0.9999, what
+    assert err.max() <= scale * 2.0 ** -7, what
+    assert same >= min_same, what
+
+
+def _run_case(B, NH, KV, D, lmax, page, positions, window, softcap, k_eq_v, theta, partial, seed, compact=False):
+    G = NH // KV
+    eps = 1e-6
+    q_raw = _gen((B, NH, D), seed, "q")
+    k_raw = _gen((B, KV, D), seed, "k")
+    v_raw = None if k_eq_v else _gen((B, KV, D), seed, "v")
+    q_norm = _gen((D,), seed, "q_norm", 0.5)
+    k_norm = _gen((D,), seed, "k_norm", 0.5)
+    cos, sin = gm.rope_table(D, theta, partial, lmax, DEV)
+    max_pages = (lmax + page - 1) // page
+    num_pages = B * max_pages + 3
+    g = torch.Generator().manual_seed(seed)
+    perm_all = torch.randperm(num_pages, generator=g)
+    pt = torch.stack([perm_all[b * max_pages:(b + 1) * max_pages] for b in range(B)]).to(torch.int32)
+    ck = [_gen((lmax, KV, D), seed, f"cache_k{b}") for b in range(B)]
+    cv = [_gen((lmax, KV, D), seed, f"cache_v{b}") for b in range(B)]
+    kp = torch.zeros((num_pages, KV, page, D), dtype=torch.bfloat16, device=DEV)
+    vp = torch.zeros_like(kp)
+    for b in range(B):
+        for i in range(max_pages):
+            n = min(page, lmax - i * page)
+            kp[pt[b, i], :, :n] = ck[b][i * page: i * page + n].permute(1, 0, 2)
+            vp[pt[b, i], :, :n] = cv[b][i * page: i * page + n].permute(1, 0, 2)
+    pos = torch.tensor(positions, dtype=torch.int32, device=DEV)
+    ctx = ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, pt.to(DEV), pos, window,
+                               softcap, eps, lmax)
+    torch.cuda.synchronize()
+
+    inv = twin.rope_inv_freq(D, theta, partial)
+    for b, p in enumerate(positions):
+        c, s = twin.rope_tables([p], inv)
+        qb = q_raw[b].cpu().reshape(1, 1, KV, G, D)
+        kb = k_raw[b].cpu().reshape(1, 1, KV, D)
+        vb = kb if k_eq_v else v_raw[b].cpu().reshape(1, 1, KV, D)
+        lo = max(0, p + 1 - window) if window else 0
+        if compact:  # only the attended rows: masked rows contribute exact zeros
+            ckc = ck[b][lo: p + 1].cpu()[None]
+            cvc = cv[b][lo: p + 1].cpu()[None]
+            n = p + 1 - lo
+            mask = torch.ones((1, 1, 1, 1, n), dtype=torch.bool)
+            ectx, ek, ev = twin.attention_core(qb, kb, vb, q_norm.cpu(), k_norm.cpu(), c, s, ckc, cvc, n - 1, mask, n,
+                                               eps, softcap)
+            k_row, v_row = ek[0, n - 1], ev[0, n - 1]
+        else:
+            class C:
+                sliding_window = window
+            mk = twin.decode_masks(C, lmax, p)
+            mask = mk[twin.SLIDING] if window else mk[twin.FULL]
+            ectx, ek, ev = twin.attention_core(qb, kb, vb, q_norm.cpu(), k_norm.cpu(), c, s, ck[b].cpu()[None],
+                                               cv[b].cpu()[None], p, mask, lmax, eps, softcap)
+            k_row, v_row = ek[0, p], ev[0, p]
+        got_k = _contig_from_pages(kp, page, pt[b].tolist(), lmax)[p].cpu()
+        got_v = _contig_from_pages(vp, page, pt[b].tolist(), lmax)[p].cpu()
+        assert torch.equal(got_k.view(torch.int16), k_row.view(torch.int16)), f"appended K row, seq {b}"
+        assert torch.equal(got_v.view(torch.int16), v_row.view(torch.int16)), f"appended V row, seq {b}"
+        _check(ctx[b].reshape(-1), ectx.reshape(-1), f"ctx seq {b} pos {p}")
+
+
+def test_small_full_two_sequences():
+    _run_case(2, 4, 2, 64, 300, 16, [37, 250], 0, 0.0, False, 1e4, 1.0, 21)
+
+
+def test_small_sliding_two_sequences():
+    _run_case(2, 4, 2, 64, 300, 16, [20, 299], 64, 0.0, False, 1e4, 1.0, 22)
+
+
+def test_small_position_zero_and_page_boundary():
+    _run_case(2, 4, 2, 64, 96, 16, [0, 16], 64, 0.0, False, 1e4, 1.0, 23)
+
+
+def test_k_eq_v_softcap_eight_heads_per_kv():
+    _run_case(1, 8, 1, 128, 520, 64, [519], 0, 50.0, True, 1e6, 0.25, 24)
+
+
+def test_isolated_sliding_attention_32k():
+    """16 q / 8 KV heads, head_dim 256, window 1024, 32K positions, softcap 50."""
+    _run_case(1, 16, 8, 256, 32768, 64, [32767], 1024, 50.0, False, 1e4, 1.0, 2, compact=True)
+
+
+def test_isolated_full_kv_shared_attention_32k():
+    """16 q / 2 KV heads, head_dim 512, k==v, 32,768 cached positions, softcap 50."""
+    _run_case(1, 16, 2, 512, 32768, 64, [32767], 0, 50.0, True, 1e6, 0.25, 2, compact=True)
+
+
+def test_out_of_range_position_attends_to_nothing():
+    """A device position beyond the cache leaves it untouched and yields ctx = 0."""
+    B, NH, KV, D, lmax, page = 1, 4, 2, 64, 64, 16
+    q = _gen((B, NH, D), 5, "q")
+    k = _gen((B, KV, D), 5, "k")
+    qn = _gen((D,), 5, "qn")
+    cos, sin = gm.rope_table(D, 1e4, 1.0, lmax, DEV)
+    kp = _gen((4, KV, page, D), 5, "kp")
+    vp = _gen((4, KV, page, D), 5, "vp")
+    kp0, vp0 = kp.clone(), vp.clone()
+    pt = torch.arange(4, dtype=torch.int32, device=DEV)[None]
+    ctx = ops.decode_attention(q, k, k, qn, qn, cos, sin, kp, vp, pt, torch.tensor([lmax + 5], dtype=torch.int32,
+                               device=DEV), 0, 0.0, 1e-6, lmax)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ctx).item() == 0
+    assert torch.equal(kp, kp0) and torch.equal(vp, vp0)
