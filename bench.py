@@ -10,6 +10,12 @@ Prints ONE JSON line (rank 0, N=1):
                model.py) timed on this host's cores on a bounded sample
 
 Workloads (--workload):
+  decode     (default) the 26B-A4B-shaped model (30 layers: 25 sliding window
+             1024 / 5 full k==v; hidden 2816; 128 experts top-8 of width 704
+             beside a 2112 dense MLP; vocab 262,144), random-init bf16 weights
+             N(0, 0.02), seed 3, 47 GiB in HBM; a 32,768-position cache; a
+             54-token uniform-random prompt, then greedy batch-1 decode:
+             warm-up steps + timed steps = 768 tokens.  value = decode tok/s.
   moe_block  the isolated MoE decode block: hidden 2816, router 2816x128,
              128 experts top-8 of width 704, bf16, seed 1, batch --batch
              (1, 4 or 8).  One HIP graph holds up to 64 consecutive steps, each
@@ -243,19 +249,200 @@ def run_copy(args) -> dict:
     }
 
 
-WORKLOADS = {"moe_block": run_moe_block, "copy": run_copy}
+# ------------------------------------------------------------------ full-model decode
+def _e2e_decode(args) -> dict:
+    """Batch-1 greedy decode of the 26B-A4B-shaped model with a 32K cache."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi import model as gm
+    from gemma4_mi import ops
+    from gemma4_mi.config import gemma4_26b_a4b_config
+    from gemma4_mi.weights import decode_bytes, init_random_params, param_bytes
+
+    cfg = gemma4_26b_a4b_config()
+    seed, prompt_len = 3, args.prompt_len
+    t0 = time.perf_counter()
+    params = init_random_params(cfg, seed, device="cuda:0")
+    torch.cuda.synchronize()
+    _log(f"weights: {param_bytes(cfg) / 2**30:.1f} GiB generated in {time.perf_counter() - t0:.1f}s")
+    cache = gm.init_cache(cfg, None, 1, args.max_len, device="cuda:0")
+    r = gm.DecodeRunner(cfg, params, cache, device="cuda:0")
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab_size, size=prompt_len).tolist()
+
+    g_pre = _capture_step(r, "f32")
+    g_dec = _capture_step(r, "bf16_running")
+    _log("decode step captured (%d kernels per token)" % (8 * cfg.num_hidden_layers + 2))
+
+    # prefill (TTFT): one dense-MoE step per prompt token, first token on the host
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for t, tok in enumerate(prompt):
+        r.set_state(tok, t)
+        g_pre.replay()
+    first = int(r.tok.item())
+    ttft = time.perf_counter() - t0
+    # decode: W warm-up steps, then exactly K timed steps
+    for _ in range(args.warmup):
+        g_dec.replay()
+    torch.cuda.synchronize()
+    p0 = int(r.pos.item())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        g_dec.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    p1 = int(r.pos.item())
+    toks = r.hist[prompt_len: p1 + 1].cpu().tolist()
+    bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
+    return {"cfg": cfg, "params": params, "cache": cache, "runner": r, "ms": ms, "ttft": ttft, "first": first,
+            "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt}
+
+
+def _capture_step(r, combine):
+    return _capture(lambda: r.launch(combine, advance=True))
+
+
+def _gateup_timing(cfg, params, n: int, steps: int) -> tuple[float, float]:
+    """Average duration (us) of the routed expert gate/up kernel over `n`
+    launches per graph cycling through the layers (different experts each
+    launch), and its algorithmic bytes per launch."""
+    import torch
+
+    from gemma4_mi import ops
+    from gemma4_mi.weights import tensor_key
+
+    H, E, K, F = cfg.hidden_size, cfg.num_experts, cfg.top_k_experts, cfg.moe_intermediate_size
+    L = cfg.num_hidden_layers
+    xe = torch.empty((n, 1, H), dtype=torch.bfloat16, device="cuda:0")
+    ops.fill_normal_(xe, tensor_key(7, "bench.xe"), 1.0)
+    scores = torch.empty((n, 1, E), dtype=torch.float32, device="cuda:0")
+    act = torch.empty((n, 1, K, F), dtype=torch.bfloat16, device="cuda:0")
+    tw = torch.empty((n, 1, K), dtype=torch.float32, device="cuda:0")
+    ti = torch.empty((n, 1, K), dtype=torch.int32, device="cuda:0")
+    lp = lambda i, k: params[f"layers.{i % L}.{k}"]  # noqa: E731
+    for i in range(n):
+        ops.moe_router_scores(xe[i], lp(i, "router.scale"), lp(i, "router.proj"), cfg.rms_norm_eps, out=scores[i])
+    g = _capture(lambda: [ops.moe_gateup_routed(xe[i], scores[i], lp(i, "router.per_expert_scale"),
+                                                lp(i, "experts.gate_up_proj"), K, act=act[i], route=(tw[i], ti[i]))
+                          for i in range(n)])
+    _time_graph(g, 2)
+    reps = max(1, steps // n)
+    us = _time_graph(g, reps) / (reps * n) * 1e3
+    nbytes = K * 2 * F * H * 2 + H * 2 + E * 4 + K * F * 2
+    return us, nbytes
+
+
+def _cpu_decode_baseline(res, budget_s: float, max_steps: int) -> dict:
+    """The oracle (torch-CPU restatement of model.py, bf16 GEMMs) continuing the
+    GPU's prefix: K/V of the prompt copied from the GPU cache, then greedy decode
+    steps on the host cores until the budget is spent."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi import model as gm
+    from oracle import twin
+
+    cfg, params, cache = res["cfg"], res["params"], res["cache"]
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    t0 = time.perf_counter()
+    cpu_params = {k: v.cpu() for k, v in params.items()}
+    max_len = cache["max_len"]
+    p = len(res["prompt"])
+    ocache = {"k": [], "v": []}
+    for i in range(cfg.num_hidden_layers):
+        k, v = gm.cache_positions(cache, i)
+        kk = torch.zeros((1,) + tuple(k.shape), dtype=torch.bfloat16)
+        vv = torch.zeros_like(kk)
+        kk[0, :p] = k[:p].cpu()
+        vv[0, :p] = v[:p].cpu()
+        ocache["k"].append(kk)
+        ocache["v"].append(vv)
+    _log(f"cpu baseline: state copied to host in {time.perf_counter() - t0:.1f}s")
+    tok, pos = res["first"], p
+    done, t_start, el = 0, None, 0.0
+    while done < max_steps:
+        ts = time.perf_counter()
+        lg, ocache = twin.forward(cfg, cpu_params, np.array([[tok]]), np.array([pos]), ocache, pos,
+                                  twin.decode_masks(cfg, max_len, pos), max_len, False, None, precise=False,
+                                  inplace=True)
+        tok, pos = twin.greedy(lg[0, 0]), pos + 1
+        if t_start is None:  # first step is the warm-up
+            t_start = time.perf_counter()
+            continue
+        done += 1
+        el = time.perf_counter() - t_start
+        if el >= budget_s:
+            break
+    return {
+        "value": done / el if el > 0 else None, "unit": "tok/s", "cores": threads, "kind": "port",
+        "sample": f"{done} batch-1 decode steps (after 1 warm-up) of the 26B-A4B-shaped model from position {p + 1}, "
+                  f"attending the whole {max_len}-position cache as the reference's decode does; torch-CPU oracle "
+                  f"with bf16 GEMMs on {threads} threads of {_cpu_name()}",
+    }
+
+
+def run_decode(args) -> dict:
+    import numpy as np
+
+    res = _e2e_decode(args)
+    cfg = res["cfg"]
+    ms = res["ms"]
+    tps = 1000.0 / ms
+    gu_us, gu_bytes = _gateup_timing(cfg, res["params"], 60, 600)
+    achieved = gu_bytes / (gu_us * 1e-6) / 1e9
+    e2e_gbs = res["bytes_tok"] * tps / 1e9
+    out = {
+        "metric": METRIC,
+        "value": tps,
+        "unit": "tok/s",
+        "ms_per_step": ms,
+        "dtype": "bf16",
+        "config": {
+            "workload": "gemma4-26B-A4B-shaped random-init decode, batch 1, 32K resident cache",
+            "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "experts": cfg.num_experts,
+            "top_k": cfg.top_k_experts, "vocab": cfg.vocab_size, "max_len": args.max_len, "seed": 3,
+            "prompt_len": args.prompt_len, "positions_timed": [res["p0"], res["p1"]],
+            "ttft_s": res["ttft"], "itl_ms": ms,
+            "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
+            "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS,
+            "kernels_per_token": 8 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token",
+            "prefill": "token-by-token decode kernels with the dense-MoE combine",
+            "first_tokens": res["tokens"][:8],
+        },
+        "roofline": {
+            "kernel": "moe_gateup_kernel (routed, 8 experts x 1408 rows x 2816)", "bound": "hbm",
+            "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
+        },
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = _cpu_decode_baseline(res, args.cpu_seconds, 8)
+    return out
+
+
+WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy}
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="moe_block")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (decode: 704, moe_block: 1000)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (decode: 64, moe_block: 100)")
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode")
+    ap.add_argument("--max-len", type=int, default=32768)
+    ap.add_argument("--prompt-len", type=int, default=54)
     ap.add_argument("--batch", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 704 if args.workload == "decode" else 1000
+    if args.warmup is None:
+        args.warmup = 64 if args.workload == "decode" else 100
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (--gpus {args.gpus} refused)",
               file=sys.stderr)

@@ -67,39 +67,45 @@ __device__ __forceinline__ float wave_max_bfly(float m) {
   return m;
 }
 
-// rms_norm(+weight) and optional RoPE of one head of D values by one wave;
-// lane l owns the D/64 consecutive values starting at l*(D/64), so the RoPE
-// partner (d +- D/2) of a value sits in lane l^32.  cos/sin are bf16 rows of
-// length D/2 at the token's position (the reference duplicates the halves,
-// model.py:66).  Writes the bf16-valued results to dst[d] (f32).
+// Per-lane slice of one head: lane l owns the PL = D/64 consecutive values
+// starting at l*PL, so the RoPE partner (d +- D/2) of a value sits in lane l^32.
+template <int PL>
+__device__ __forceinline__ void load_slice(const uint16_t* __restrict__ p, float* x) {
+  if constexpr (PL == 8) {
+    unpack8(ld16(p), x);
+  } else if constexpr (PL == 4) {
+    const uint2 v = *(const uint2*)p;
+    x[0] = bf_lo(v.x); x[1] = bf_hi(v.x); x[2] = bf_lo(v.y); x[3] = bf_hi(v.y);
+  } else if constexpr (PL == 2) {
+    const uint32_t v = *(const uint32_t*)p;
+    x[0] = bf_lo(v); x[1] = bf_hi(v);
+  } else {
+    x[0] = bf2f(*p);
+  }
+}
+
+// rms_norm(x, w) (w may be null) and optional RoPE of one head held as
+// per-lane slices (see load_slice); cs/sn are the lane's cos/sin values
+// (the reference duplicates the table halves, model.py:66).  In place.
 template <int D>
-__device__ void norm_rope_head(const uint16_t* __restrict__ src, const uint16_t* __restrict__ w,
-                               const uint16_t* __restrict__ cs, const uint16_t* __restrict__ sn, float eps,
-                               bool rope, float* __restrict__ dst) {
+__device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const float* cs, const float* sn, float eps,
+                                                bool rope) {
   constexpr int PL = D / 64;
   const int lane = threadIdx.x & 63;
-  float x[PL];
   double ss = 0.0;
 #pragma unroll
-  for (int i = 0; i < PL; ++i) {
-    x[i] = bf2f(src[lane * PL + i]);
-    ss = fma((double)x[i], (double)x[i], ss);
-  }
+  for (int i = 0; i < PL; ++i) ss = fma((double)x[i], (double)x[i], ss);
   const float r = rms_scale(group_sum_f64<64>(ss), D, eps);
 #pragma unroll
-  for (int i = 0; i < PL; ++i) x[i] = (w != nullptr) ? rbf(x[i] * r * bf2f(w[lane * PL + i])) : rbf(x[i] * r);
+  for (int i = 0; i < PL; ++i) x[i] = (w != nullptr) ? rbf(x[i] * r * w[i]) : rbf(x[i] * r);
   if (rope) {
 #pragma unroll
     for (int i = 0; i < PL; ++i) {
-      const int d = lane * PL + i;
       const float partner = __shfl_xor(x[i], 32, kWave);
-      const float rot = (d < D / 2) ? -partner : partner;
-      const int j = d % (D / 2);
-      x[i] = rbf(rbf(x[i] * bf2f(cs[j])) + rbf(rot * bf2f(sn[j])));
+      const float rot = (lane * PL + i < D / 2) ? -partner : partner;
+      x[i] = rbf(rbf(x[i] * cs[i]) + rbf(rot * sn[i]));
     }
   }
-#pragma unroll
-  for (int i = 0; i < PL; ++i) dst[lane * PL + i] = x[i];
 }
 
 // ------------------------------------------------------------------ scores
@@ -128,19 +134,47 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
-  const uint16_t* cs = rope_cos + (size_t)pos * (D / 2);
-  const uint16_t* sn = rope_sin + (size_t)pos * (D / 2);
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
 
-  for (int g = wave; g < G; g += 4)
-    norm_rope_head<D>(q_raw + ((size_t)b * a.NH + kv * G + g) * D, q_norm, cs, sn, a.eps, true, qs + g * D);
+  // Prologue, all loads first: wave w owns q heads w, w+4 (G <= 8); with the
+  // append, waves 2 and 3 also own the new K and V rows.
+  constexpr int PL = D / 64;
+  constexpr int GW = (G + 3) / 4;
+  const int so = lane * PL;                 // this lane's slice offset
+  const int jo = so % (D / 2);              // its cos/sin offset
   const bool mine = append && (end == pos + 1);
-  if (mine) {
+  float qx[GW][PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
+#pragma unroll
+  for (int u = 0; u < GW; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) load_slice<PL>(q_raw + ((size_t)b * a.NH + kv * G + g) * D + so, qx[u]);
+  }
+  load_slice<PL>(q_norm + so, qw);
+  load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
+  load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
+  if (mine && wave >= 2) {
     const uint16_t* kr = k_raw + ((size_t)b * a.KV + kv) * D;
     const uint16_t* vr = (v_raw != nullptr) ? v_raw + ((size_t)b * a.KV + kv) * D : kr;
-    if (wave == 0) norm_rope_head<D>(kr, k_norm, cs, sn, a.eps, true, knew);
-    if (wave == 1) norm_rope_head<D>(vr, nullptr, cs, sn, a.eps, false, vnew);
-    __syncthreads();
+    load_slice<PL>((wave == 2 ? kr : vr) + so, kvx);
+    load_slice<PL>(k_norm + so, kw);
+  }
+#pragma unroll
+  for (int u = 0; u < GW; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      norm_rope_slice<D>(qx[u], qw, cs, sn, a.eps, true);
+#pragma unroll
+      for (int i = 0; i < PL; ++i) qs[g * D + so + i] = qx[u][i];
+    }
+  }
+  if (mine && wave >= 2) {
+    norm_rope_slice<D>(kvx, wave == 2 ? kw : nullptr, cs, sn, a.eps, wave == 2);
+    float* dst = (wave == 2) ? knew : vnew;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) dst[so + i] = kvx[i];
+  }
+  __syncthreads();
+  if (mine) {
     const long long off = page_off(a, pt_row, pos, kv);
     if (off >= 0)
       for (int d = tid; d < D; d += 256) {
@@ -148,7 +182,6 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
         v_pages[off + d] = f2bf(vnew[d]);
       }
   }
-  __syncthreads();
 
   const int sub = lane % LPP, slot = lane / LPP;
   float q[G][8];
@@ -157,35 +190,39 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) q[g][i] = qs[g * D + sub * 8 + i];
   const float cap = a.softcap;
-  for (int base = wave * PPW; base < npos; base += 4 * PPW) {
-    const int j = base + slot;
-    const int p = start + j;
-    float kf[8];
+  constexpr int U = 4;  // position steps per batch: U K loads in flight per lane
+  for (int base = wave * PPW * U; base < npos; base += 4 * PPW * U) {
+    // branch-free: page lookups for the batch, then the K loads from clamped
+    // addresses; masking is applied to the values (see layer.hip on vmcnt)
+    long long off[U];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kf[i] = 0.0f;
-    bool ok = false;
-    if (j < npos) {
-      if (mine && p == pos) {
+    for (int u = 0; u < U; ++u) off[u] = page_off(a, pt_row, start + min(base + u * PPW + slot, npos - 1), kv);
+    float kf[U][8];
+    bool ok[U];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) kf[i] = knew[sub * 8 + i];
-        ok = true;
-      } else {
-        const long long off = page_off(a, pt_row, p, kv);
-        if (off >= 0) {
-          unpack8(ld16(k_pages + off + sub * 8), kf);
-          ok = true;
-        }
+    for (int u = 0; u < U; ++u) {
+      const int j = base + u * PPW + slot;
+      unpack8(ld16(k_pages + max(off[u], 0ll) + sub * 8), kf[u]);
+      ok[u] = (j < npos) && (off[u] >= 0);
+      if (mine && start + j == pos && j < npos) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) kf[u][i] = knew[sub * 8 + i];
+        ok[u] = true;
       }
     }
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float acc = 0.0f;
+    for (int u = 0; u < U; ++u) {
+      const int j = base + u * PPW + slot;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc = fmaf(q[g][i], kf[i], acc);
-      acc = group_sum<LPP>(acc);
-      float s = rbf(acc);
-      if (cap > 0.0f) s = tanhf(s / cap) * cap;
-      if (j < npos && sub == 0) sc[g][j] = ok ? s : -INFINITY;
+      for (int g = 0; g < G; ++g) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc = fmaf(q[g][i], kf[u][i], acc);
+        acc = group_sum<LPP>(acc);
+        float sv = rbf(acc);
+        if (cap > 0.0f) sv = tanhf(sv / cap) * cap;
+        if (j < npos && sub == 0) sc[g][j] = ok[u] ? sv : -INFINITY;
+      }
     }
   }
   __syncthreads();
@@ -243,16 +280,21 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
-  if (tid < G) {
-    const int h = kv * G + tid;
+  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
+  for (int g = wave; g < G; g += 4) {
+    const int h = kv * G + g;
     const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
     const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
     float m = -INFINITY;
-    for (int i = 0; i < R.n_eff; ++i) m = fmaxf(m, sm[i]);
-    float s = 0.0f;
-    for (int i = 0; i < R.n_eff; ++i) s += (sm[i] == -INFINITY) ? 0.0f : expf(sm[i] - m) * sl[i];
-    mg[tid] = m;
-    sg[tid] = s;
+    for (int i = lane; i < R.n_eff; i += 64) m = fmaxf(m, sm[i]);
+    m = wave_max_bfly(m);
+    float t = 0.0f;
+    for (int i = lane; i < R.n_eff; i += 64) t += (sm[i] == -INFINITY) ? 0.0f : expf(sm[i] - m) * sl[i];
+    t = group_sum<64>(t);
+    if (lane == 0) {
+      mg[g] = m;
+      sg[g] = t;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -272,16 +314,24 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
-  for (int j = slot; j < npos; j += PPV) {
-    const long long off = page_off(a, pt_row, start + j, kv);
-    if (off < 0) continue;
-    float vf[8];
-    unpack8(ld16(v_pages + off + dofs), vf);
+  constexpr int U = 4;  // positions per batch: U V loads in flight per lane
+  for (int j0 = slot; j0 < npos; j0 += PPV * U) {
+    long long off[U];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const float p = pr[g][j];
+    for (int u = 0; u < U; ++u) off[u] = page_off(a, pt_row, start + min(j0 + u * PPV, npos - 1), kv);
+    float vf[U][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+    for (int u = 0; u < U; ++u) unpack8(ld16(v_pages + max(off[u], 0ll) + dofs), vf[u]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = j0 + u * PPV;
+      const bool ok = (j < npos) && (off[u] >= 0);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = ok ? pr[g][min(j, npos - 1)] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[u][i], acc[g][i]);
+      }
     }
   }
   float* part = ws_part + (((size_t)b * a.n_split_max + split) * a.NH + kv * G) * D;
@@ -304,9 +354,22 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int3
   const int idx = blockIdx.x * 256 + threadIdx.x;  // h*D + d
   if (idx >= a.NH * a.D) return;
   const Range R = attn_range(a, pos_arr[b]);
-  float s = 0.0f;
-  for (int i = 0; i < R.n_eff; ++i) s += ws_part[(((size_t)b * a.n_split_max + i) * a.NH) * a.D + idx];
-  ctx[(size_t)b * a.NH * a.D + idx] = f2bf(s);
+  const size_t stride = (size_t)a.NH * a.D;
+  const float* src = ws_part + (size_t)b * a.n_split_max * stride + idx;
+  float acc[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
+  int i = 0;
+  for (; i + 8 <= R.n_eff; i += 8) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(i + u) * stride];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += v[u];
+  }
+  for (; i < R.n_eff; ++i) acc[0] += src[(size_t)i * stride];
+  const float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+  ctx[(size_t)b * stride + idx] = f2bf(s);
 }
 
 // ------------------------------------------------------------------ append
@@ -322,15 +385,22 @@ __global__ __launch_bounds__(128) void kv_append_kernel(AttnDims a, const uint16
                                                         const int32_t* __restrict__ page_table,
                                                         const int32_t* __restrict__ pos_arr) {
   __shared__ float kn[D], vn[D];
-  const int t = blockIdx.x, kv = blockIdx.y, wave = threadIdx.x >> 6;
+  constexpr int PL = D / 64;
+  const int t = blockIdx.x, kv = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int pos = pos_arr[t];
   if (pos < 0 || pos >= a.lmax || pos >= a.max_pages * a.page) return;
-  const uint16_t* cs = rope_cos + (size_t)pos * (D / 2);
-  const uint16_t* sn = rope_sin + (size_t)pos * (D / 2);
+  const int so = lane * PL, jo = so % (D / 2);
   const uint16_t* kr = k_raw + ((size_t)t * a.KV + kv) * D;
   const uint16_t* vr = (v_raw != nullptr) ? v_raw + ((size_t)t * a.KV + kv) * D : kr;
-  if (wave == 0) norm_rope_head<D>(kr, k_norm, cs, sn, a.eps, true, kn);
-  if (wave == 1) norm_rope_head<D>(vr, nullptr, cs, sn, a.eps, false, vn);
+  float x[PL], w[PL], cs[PL], sn[PL];
+  load_slice<PL>((wave == 0 ? kr : vr) + so, x);
+  load_slice<PL>(k_norm + so, w);
+  load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
+  load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
+  norm_rope_slice<D>(x, wave == 0 ? w : nullptr, cs, sn, a.eps, wave == 0);
+  float* dst = (wave == 0) ? kn : vn;
+#pragma unroll
+  for (int i = 0; i < PL; ++i) dst[so + i] = x[i];
   __syncthreads();
   const long long off = page_off(a, page_table, pos, kv);
   if (off < 0) return;

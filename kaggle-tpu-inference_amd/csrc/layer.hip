@@ -26,6 +26,8 @@
 #include <string.h>
 
 #include "capi_util.h"
+#include <cstdlib>
+
 #include "common.h"
 
 namespace g4mi {
@@ -96,27 +98,65 @@ __device__ __forceinline__ float vrms(const Vec& v, int nch, int H, float eps, d
   return rms_scale(block_sum_f64(vsumsq(v, nch), red), H, eps);
 }
 
+// v = bf16(v * r * w) with the weight already in registers
+__device__ __forceinline__ void vscale_w(Vec& v, float r, const Vec& w) {
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) v.c[j] = scale8(v.c[j], r, &w.c[j]);
+}
+// Two block sums in one reduction round (exact f64 inputs).
+__device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red) {
+  a = group_sum_f64<kWave>(a);
+  b = group_sum_f64<kWave>(b);
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) {
+    red[w] = a;
+    red[4 + w] = b;
+  }
+  __syncthreads();
+  double ta = 0.0, tb = 0.0;
+  for (int i = 0; i < nw; ++i) {
+    ta += red[i];
+    tb += red[4 + i];
+  }
+  a = ta;
+  b = tb;
+}
+
 // Tail of the previous layer: x = bf16(bf16(x1 + rms(hs, post_ff)) * ls),
 // hs = bf16(rms(mlp, post_ff_1) + rms(moe, post_ff_2)), or hs = mlp without MoE.
+// All operands are loaded up front (one memory round trip), then three
+// dependent reduction rounds follow.  `red` holds 8 doubles.
 struct TailArgs {
   const uint16_t *x1, *mlp, *moe, *w_pf1, *w_pf2, *w_pf, *ls;
 };
-__device__ void tail_vec(Vec& x, const TailArgs& t, int nch, int H, float eps, double* red) {
-  Vec a, b;
-  vload(a, t.mlp, nch);
+struct TailRegs {
+  Vec a, b, x1, w1, w2, w3;
+  uint16_t ls;
+};
+__device__ __forceinline__ void tail_load(TailRegs& T, const TailArgs& t, int nch) {
+  vload(T.a, t.mlp, nch);
+  vload(T.x1, t.x1, nch);
+  vload(T.w3, t.w_pf, nch);
   if (t.moe != nullptr) {
-    vload(b, t.moe, nch);
-    const float r1 = vrms(a, nch, H, eps, red);
-    const float r2 = vrms(b, nch, H, eps, red);
-    vscale(a, r1, t.w_pf1, nch);
-    vscale(b, r2, t.w_pf2, nch);
-    vadd(a, b, nch);
+    vload(T.b, t.moe, nch);
+    vload(T.w1, t.w_pf1, nch);
+    vload(T.w2, t.w_pf2, nch);
   }
-  const float r3 = vrms(a, nch, H, eps, red);
-  vscale(a, r3, t.w_pf, nch);
-  vload(x, t.x1, nch);
-  vadd(x, a, nch);
-  vmul(x, bf2f(t.ls[0]));
+  T.ls = t.ls[0];
+}
+__device__ __forceinline__ void tail_compute(Vec& x, TailRegs& T, bool moe, int nch, int H, float eps, double* red) {
+  if (moe) {
+    double s1 = vsumsq(T.a, nch), s2 = vsumsq(T.b, nch);
+    block_sum2_f64(s1, s2, red);
+    vscale_w(T.a, rms_scale(s1, H, eps), T.w1);
+    vscale_w(T.b, rms_scale(s2, H, eps), T.w2);
+    vadd(T.a, T.b, nch);
+  }
+  vscale_w(T.a, vrms(T.a, nch, H, eps, red), T.w3);
+  x = T.x1;
+  vadd(x, T.a, nch);
+  vmul(x, bf2f(T.ls));
 }
 
 // ------------------------------------------------------------------ GEMV core
@@ -149,46 +189,77 @@ struct InArgs {
   const uint16_t* W[3];   // q, k, v projection rows [rows, H]
   int rows[3];
   uint16_t* out;          // [rows0 + rows1 + rows2]
+  int pairs_per_block;
   int H;
   float eps;
 };
 
+// Row walk shared by the GEMV kernels: a block owns `ppb` consecutive row
+// pairs (ppb a multiple of 4); wave w handles pairs w, w+4, ... and half-wave
+// h row 2*pair+h.  Each wave keeps the next pair's loads in flight while it
+// reduces the current one, so a block per CU streams at full rate and the
+// block's prologue is computed once per CU instead of once per 8 rows.
 template <int IT>
+struct PairWalk {
+  int p, pend, plast;
+  __device__ __forceinline__ PairWalk(int ppb, int npairs) {
+    const int wave = threadIdx.x >> 6;
+    const int p0 = blockIdx.x * ppb;
+    p = p0 + wave;
+    pend = min(p0 + ppb, npairs);
+    plast = max(pend - 1, 0);
+  }
+};
+
+template <int IT, int MODE>
 __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[4];
-  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
-  const int total = a.rows[0] + a.rows[1] + a.rows[2];
-  const int r = blockIdx.x * 8 + wave * 2 + half;
-  u32x4 w[IT];
-  const uint16_t* row = nullptr;
-  if (r < total) {
-    int rr = r, m = 0;
-    while (rr >= a.rows[m]) { rr -= a.rows[m]; ++m; }
-    row = a.W[m] + (size_t)rr * H;
-    load_row<32, IT>(row, l, w);
-  }
-  Vec x;
-  if (a.mode == kInEmbed) {
+  __shared__ double red[8];
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31;
+  const int q_rows = a.rows[0], k_rows = a.rows[1];
+  const int total = q_rows + k_rows + a.rows[2];
+  auto rowptr = [&](int pair) {
+    const int rc = min(2 * pair + half, total - 1);
+    return (rc < q_rows) ? a.W[0] + (size_t)rc * H
+           : (rc < q_rows + k_rows) ? a.W[1] + (size_t)(rc - q_rows) * H
+                                    : a.W[2] + (size_t)(rc - q_rows - k_rows) * H;
+  };
+  // Loads are counted in issue order (s_waitcnt vmcnt), so the small
+  // L2-resident prologue operands are requested before the weight rows and
+  // the prologue runs while the rows stream in.  MODE is a template
+  // parameter and the row loads are unconditional (clamped addresses), so no
+  // branch merge forces an early full wait.
+  Vec x, win;
+  TailRegs T;
+  vload(win, a.w_in, NCH);
+  if constexpr (MODE == kInEmbed) {
     int t = a.tok[0];
     t = (t < 0 || t >= a.vocab) ? 0 : t;
     vload(x, a.embed + (size_t)t * H, NCH);
-    vmul(x, a.embed_c);
-  } else if (a.mode == kInTail) {
-    tail_vec(x, a.tail, NCH, H, a.eps, red);
+  } else if constexpr (MODE == kInTail) {
+    tail_load(T, a.tail, NCH);
   } else {
     vload(x, a.x_in, NCH);
   }
+  PairWalk<IT> pw(a.pairs_per_block, (total + 1) / 2);
+  u32x4 w[IT];
+  load_row<32, IT>(rowptr(min(pw.p, pw.plast)), l, w);
+  if constexpr (MODE == kInEmbed) vmul(x, a.embed_c);
+  if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
   if (blockIdx.x == 0) vstore(x, (u32x4*)a.x_out, NCH);
-  const float rn = vrms(x, NCH, H, a.eps, red);
-  vscale(x, rn, a.w_in, NCH);
+  vscale_w(x, vrms(x, NCH, H, a.eps, red), win);
   vstore(x, xs, NCH);
   __syncthreads();
-  if (r < total) {
+  for (; pw.p < pw.pend; pw.p += 4) {
+    u32x4 wn[IT];
+    load_row<32, IT>(rowptr(min(pw.p + 4, pw.plast)), l, wn);
     const float acc = dot_row<32, IT>(w, xs, l);
-    if (l == 0) a.out[r] = f2bf(acc);
+    const int r = 2 * pw.p + half;
+    if (r < total && l == 0) a.out[r] = f2bf(acc);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = wn[i];
   }
 }
 
@@ -196,19 +267,28 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
 // out[H] = ctx[K] . W[H, K]; S lanes per row (64/S rows per wave).
 template <int S, int IT>
 __global__ __launch_bounds__(256) void oproj_kernel(const uint16_t* __restrict__ ctx, const uint16_t* __restrict__ W,
-                                                    int rows, uint16_t* __restrict__ out) {
+                                                    int rows, int groups_per_block, uint16_t* __restrict__ out) {
   constexpr int K = 8 * S * IT;
-  constexpr int RPW = 64 / S;
+  constexpr int RPW = 64 / S;  // rows per wave step (a "group")
   __shared__ u32x4 xs[K / 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % S;
-  const int r = (blockIdx.x * 4 + wave) * RPW + lane / S;
-  u32x4 w[IT];
-  if (r < rows) load_row<S, IT>(W + (size_t)r * K, sub, w);
+  const int ngroups = (rows + RPW - 1) / RPW;
+  const int g0 = blockIdx.x * groups_per_block;
+  const int gend = min(g0 + groups_per_block, ngroups), glast = max(gend - 1, 0);
+  int gi = g0 + wave;
+  auto rowp = [&](int grp) { return W + (size_t)min(grp * RPW + lane / S, rows - 1) * K; };
   for (int c = tid; c < K / 8; c += 256) xs[c] = ld16((const u32x4*)ctx + c);
+  u32x4 w[IT];
+  load_row<S, IT>(rowp(min(gi, glast)), sub, w);
   __syncthreads();
-  if (r < rows) {
+  for (; gi < gend; gi += 4) {
+    u32x4 wn[IT];
+    load_row<S, IT>(rowp(min(gi + 4, glast)), sub, wn);
     const float acc = dot_row<S, IT>(w, xs, sub);
-    if (sub == 0) out[r] = f2bf(acc);
+    const int r = gi * RPW + lane / S;
+    if (r < rows && sub == 0) out[r] = f2bf(acc);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = wn[i];
   }
 }
 
@@ -220,6 +300,7 @@ struct FfnInArgs {
   int I;
   uint16_t* act_mlp;           // [I]
   int dense_blocks;            // blocks [0, dense_blocks) do dense rows
+  int tasks_per_block;         // dense (gate, up) pairs per dense block (multiple of 4)
   const uint16_t *r_scale, *r_proj;  // router (null: no MoE)
   int E;
   float r_c;                   // bf16(H^-0.5)
@@ -233,39 +314,36 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[4];
+  __shared__ double red[8];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
   const bool dense = (int)blockIdx.x < a.dense_blocks;
-  int row = -1;
-  u32x4 w[IT];
-  if (dense) {
-    const int f = blockIdx.x * 4 + wave;  // one (gate, up) pair per wave
-    if (f < a.I) {
-      row = f;
-      load_row<32, IT>((half ? a.up : a.gate) + (size_t)f * H, l, w);
-    }
-  } else {
-    const int e = (blockIdx.x - a.dense_blocks) * 8 + wave * 2 + half;
-    if (e < a.E) {
-      row = e;
-      load_row<32, IT>(a.r_proj + (size_t)e * H, l, w);
-    }
-  }
-  // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
-  Vec x, o;
+  // prologue operands first (see layer_in), then the weight rows
+  Vec x, o, wpa, wf, rsc;
   vload(o, a.o, NCH);
-  const float ro = vrms(o, NCH, H, a.eps, red);
-  vscale(o, ro, a.w_pa, NCH);
   vload(x, a.x, NCH);
+  vload(wpa, a.w_pa, NCH);
+  vload(wf, dense ? a.w_pf : a.w_pf2, NCH);
+  if (!dense) vload(rsc, a.r_scale, NCH);
+  // dense: this block owns tasks (one (gate, up) row pair each) [t0, tend),
+  // wave w takes t0+w, t0+w+4, ...; router blocks own 8 expert rows each.
+  const int t0 = blockIdx.x * a.tasks_per_block;
+  const int tend = min(t0 + a.tasks_per_block, a.I), tlast = max(tend - 1, 0);
+  int t = t0 + wave;
+  const int e = (blockIdx.x - a.dense_blocks) * 8 + wave * 2 + half;
+  auto dense_row = [&](int f) { return (half ? a.up : a.gate) + (size_t)f * H; };
+  u32x4 w[IT];
+  load_row<32, IT>(dense ? dense_row(min(t, tlast)) : a.r_proj + (size_t)min(e, a.E - 1) * H, l, w);
+  // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
+  vscale_w(o, vrms(o, NCH, H, a.eps, red), wpa);
   vadd(x, o, NCH);
   if (blockIdx.x == 0) vstore(x, (u32x4*)a.x1_out, NCH);
   const float r1 = vrms(x, NCH, H, a.eps, red);
   if (dense) {
-    vscale(x, r1, a.w_pf, NCH);
+    vscale_w(x, r1, wf);
     vstore(x, xs, NCH);
   } else {
     Vec xe = x;
-    vscale(xe, r1, a.w_pf2, NCH);
+    vscale_w(xe, r1, wf);
     if (blockIdx.x == a.dense_blocks) vstore(xe, (u32x4*)a.xe_out, NCH);
     // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
     const float r2 = vrms(xe, NCH, H, a.eps, red);
@@ -275,7 +353,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
       if (c < NCH) {
         float f[8], g[8];
         unpack8(xe.c[j], f);
-        unpack8(ld16((const u32x4*)a.r_scale + c), g);
+        unpack8(rsc.c[j], g);
 #pragma unroll
         for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r2) * g[q]) * a.r_c);
         u32x4 v;
@@ -285,11 +363,16 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     }
   }
   __syncthreads();
-  if (row < 0) return;
   if (dense) {
-    const float acc = dot_row<32, IT>(w, xs, l);
-    const float up = __shfl(acc, 32, kWave);
-    if (lane == 0) a.act_mlp[row] = f2bf(rbf(gelu_tanh(rbf(acc))) * rbf(up));
+    for (; t < tend; t += 4) {
+      u32x4 wn[IT];
+      load_row<32, IT>(dense_row(min(t + 4, tlast)), l, wn);
+      const float acc = dot_row<32, IT>(w, xs, l);
+      const float up = __shfl(acc, 32, kWave);
+      if (lane == 0) a.act_mlp[t] = f2bf(rbf(gelu_tanh(rbf(acc))) * rbf(up));
+#pragma unroll
+      for (int i = 0; i < IT; ++i) w[i] = wn[i];
+    }
   } else {
     double d0 = 0.0, d1 = 0.0;
 #pragma unroll
@@ -298,7 +381,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
       else d0 = dot8_f64(w[i], xs[l + 32 * i], d0);
     }
     const double acc = group_sum_f64<32>(d0 + d1);
-    if (l == 0) a.scores[row] = rbf((float)acc);
+    if (e < a.E && l == 0) a.scores[e] = rbf((float)acc);
   }
 }
 
@@ -327,31 +410,33 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   const int h = blockIdx.x * 4 + wave;
   const int ich = a.I / 8;
   constexpr int DIT = 8;  // dense chunks per lane, at most (I <= 4096)
-  u32x4 wd[DIT];
   const bool hv = h < a.H;
-  if (hv) {
-    const u32x4* drow = (const u32x4*)(a.down + (size_t)h * a.I);
-#pragma unroll
-    for (int i = 0; i < DIT; ++i) {
-      const int c = lane + 64 * i;
-      wd[i] = (c < ich) ? ld_stream(drow + c) : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
-  // expert rows: lane group g = slot, 8 lanes, FIT chunks each
+  const int hc = min(h, a.H - 1);
   const int g = lane >> 3, l8 = lane & 7;
-  u32x4 we[FIT];
-  int e = -1;
-  if (a.e_down != nullptr && hv && g < a.K) {
-    e = a.top_i[g];
-    if (e >= 0 && e < a.E) {
-      const u32x4* erow = (const u32x4*)(a.e_down + ((size_t)e * a.H + h) * F);
+  // small operands first (issue order = completion order for vmcnt): the
+  // routed expert of this lane group and this thread's share of act_mlp
+  const int ei = (a.e_down != nullptr) ? a.top_i[min(g, a.K - 1)] : -1;
+  constexpr int ACT_PER = 2;  // act_mlp chunks per thread: I <= 8 * 256 * 2
+  u32x4 av[ACT_PER];
 #pragma unroll
-      for (int i = 0; i < FIT; ++i) we[i] = ld_stream(erow + l8 + 8 * i);
-    } else {
-      e = -1;
-    }
+  for (int j = 0; j < ACT_PER; ++j) av[j] = ld16((const u32x4*)a.act_mlp + min(tid + 256 * j, ich - 1));
+  // weight rows, unconditional with clamped addresses
+  u32x4 wd[DIT];
+  {
+    const u32x4* drow = (const u32x4*)(a.down + (size_t)hc * a.I);
+#pragma unroll
+    for (int i = 0; i < DIT; ++i) wd[i] = ld_stream(drow + min(lane + 64 * i, ich - 1));
   }
-  for (int c = tid; c < ich; c += 256) act_lds[c] = ld16((const u32x4*)a.act_mlp + c);
+  const int e = (g < a.K && ei >= 0 && ei < a.E) ? ei : -1;
+  u32x4 we[FIT];
+  if (a.e_down != nullptr) {
+    const u32x4* erow = (const u32x4*)(a.e_down + ((size_t)max(e, 0) * a.H + hc) * F);
+#pragma unroll
+    for (int i = 0; i < FIT; ++i) we[i] = ld_stream(erow + l8 + 8 * i);
+  }
+#pragma unroll
+  for (int j = 0; j < ACT_PER; ++j)
+    if (tid + 256 * j < ich) act_lds[tid + 256 * j] = av[j];
   __syncthreads();
   if (!hv) return;
   float acc = 0.0f;
@@ -403,7 +488,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[4];
+  __shared__ double red[8];
   __shared__ float bvs[8];
   __shared__ int bis[8];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
@@ -411,12 +496,14 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   const int r1 = min(a.V, r0 + a.rows_per_block);
   // first row pair of this wave, loads issued before the prologue
   int r = r0 + wave * 2 + half;
+  Vec x, wn0;
+  TailRegs T;
+  tail_load(T, a.tail, NCH);
+  vload(wn0, a.w_norm, NCH);
   u32x4 w[IT];
-  if (r < r1) load_row<32, IT>(a.embed + (size_t)r * H, l, w);
-  Vec x;
-  tail_vec(x, a.tail, NCH, H, a.eps, red);
-  const float rn = vrms(x, NCH, H, a.eps, red);
-  vscale(x, rn, a.w_norm, NCH);
+  load_row<32, IT>(a.embed + (size_t)min(r, a.V - 1) * H, l, w);
+  tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
+  vscale_w(x, vrms(x, NCH, H, a.eps, red), wn0);
   vstore(x, xs, NCH);
   __syncthreads();
   float bv = -INFINITY;
@@ -424,16 +511,13 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   const float cap = a.softcap;
   for (; r - half < r1; r += 8) {
     u32x4 wn[IT];
-    const int rn2 = r + 8;
-    if (rn2 < r1) load_row<32, IT>(a.embed + (size_t)rn2 * H, l, wn);
-    if (r < r1) {
-      const float acc = dot_row<32, IT>(w, xs, l);
-      float v = rbf(acc);
-      if (cap > 0.0f) v = tanhf(v / cap) * cap;
-      if (l == 0) {
-        a.logits[r] = v;
-        better(bv, bi, v, r);
-      }
+    load_row<32, IT>(a.embed + (size_t)min(r + 8, a.V - 1) * H, l, wn);  // next pair (clamped)
+    const float acc = dot_row<32, IT>(w, xs, l);
+    float v = rbf(acc);
+    if (cap > 0.0f) v = tanhf(v / cap) * cap;
+    if (r < r1 && l == 0) {
+      a.logits[r] = v;
+      better(bv, bi, v, r);
     }
 #pragma unroll
     for (int i = 0; i < IT; ++i) w[i] = wn[i];
@@ -488,6 +572,24 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ b
   }
 }
 
+// Work units (row pairs, row groups or tasks) per block for the row walks:
+// about gemv_blocks() blocks (one per CU by default; G4MI_GEMV_BLOCKS
+// overrides it for tuning), 4 waves each, at least one unit per wave.
+static int gemv_blocks() {
+  static const int n = [] {
+    const char* e = getenv("G4MI_GEMV_BLOCKS");
+    const int v = e ? atoi(e) : 0;
+    return (v >= 16 && v <= 65536) ? v : 256;
+  }();
+  return n;
+}
+static int row_groups_per_block(int units) {
+  const int nb = gemv_blocks();
+  int per = (units + nb - 1) / nb;
+  per = ((per + 3) / 4) * 4;
+  return per < 4 ? 4 : per;
+}
+
 static float bf16_round_host(double v) {
   float f = (float)v;
   uint32_t u;
@@ -534,10 +636,17 @@ int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64
   a.rows[0] = (int)q_rows; a.rows[1] = (int)k_rows; a.rows[2] = (int)v_rows;
   a.out = qkv_out; a.H = (int)H; a.eps = eps;
   const int total = (int)(q_rows + k_rows + v_rows);
-  dim3 grid((unsigned)((total + 7) / 8));
+  const int npairs = (total + 1) / 2;
+  a.pairs_per_block = row_groups_per_block(npairs);
+  dim3 grid((unsigned)((npairs + a.pairs_per_block - 1) / a.pairs_per_block));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {
-#define G4MI_C(I) case I: hipLaunchKernelGGL(layer_in_kernel<I>, grid, dim3(256), 0, st, a); break;
+#define G4MI_C(I)                                                                                   \
+  case I:                                                                                           \
+    if (mode == kInEmbed) hipLaunchKernelGGL((layer_in_kernel<I, kInEmbed>), grid, dim3(256), 0, st, a); \
+    else if (mode == kInTail) hipLaunchKernelGGL((layer_in_kernel<I, kInTail>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((layer_in_kernel<I, kInPlain>), grid, dim3(256), 0, st, a);            \
+    break;
     G4MI_IT16(G4MI_C)
 #undef G4MI_C
   }
@@ -548,16 +657,18 @@ int g4mi_oproj(const uint16_t* ctx, const uint16_t* w, int64_t rows, int64_t K, 
   G4MI_REQUIRE(ctx && w && out && rows >= 1, G4MI_EINVAL, "oproj: missing argument");
   hipStream_t st = as_stream(stream);
   if (K % 512 == 0 && K / 512 >= 1 && K / 512 <= 16) {
-    dim3 grid((unsigned)((rows + 3) / 4));
+    const int ng = (int)rows, gpb = row_groups_per_block(ng);
+    dim3 grid((unsigned)((ng + gpb - 1) / gpb));
     switch (K / 512) {
-#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<64, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, out); break;
+#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<64, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, gpb, out); break;
       G4MI_IT16(G4MI_C)
 #undef G4MI_C
     }
   } else if (K % 256 == 0 && K / 256 <= 16) {
-    dim3 grid((unsigned)((rows + 7) / 8));
+    const int ng = (int)((rows + 1) / 2), gpb = row_groups_per_block(ng);
+    dim3 grid((unsigned)((ng + gpb - 1) / gpb));
     switch (K / 256) {
-#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<32, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, out); break;
+#define G4MI_C(I) case I: hipLaunchKernelGGL((oproj_kernel<32, I>), grid, dim3(256), 0, st, ctx, w, (int)rows, gpb, out); break;
       G4MI_IT16(G4MI_C)
 #undef G4MI_C
     }
@@ -580,7 +691,8 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
   FfnInArgs a;
   a.x = x; a.o = o; a.w_pa = post_attn_ln; a.w_pf = pre_ff_ln; a.w_pf2 = pre_ff2_ln;
   a.x1_out = x1_out; a.xe_out = xe_out; a.gate = gate; a.up = up; a.I = (int)I; a.act_mlp = act_mlp;
-  a.dense_blocks = (int)((I + 3) / 4);
+  a.tasks_per_block = row_groups_per_block((int)I);
+  a.dense_blocks = (int)((I + a.tasks_per_block - 1) / a.tasks_per_block);
   a.r_scale = router_scale; a.r_proj = router_proj; a.E = router_proj ? (int)E : 0;
   a.r_c = bf16_round_host(1.0 / sqrt((double)H));
   a.scores = scores; a.H = (int)H; a.eps = eps;

@@ -281,14 +281,11 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
       top_i[(size_t)n * K + threadIdx.x] = L.topi[threadIdx.x];
     }
   }
-  if (task >= K * F) return;
-  const int slot = task / F, f = task - slot * F;
-  const int e = (scores != nullptr) ? L.topi[slot] : top_i[n * K + slot];
-  if (e < 0 || e >= E) {  // not an expert index: contribute nothing
-    if (lane == 0) act[((size_t)n * K + slot) * F + f] = 0;
-    return;
-  }
-  const u32x4* row = (const u32x4*)(gate_up + ((size_t)(e * 2 + half) * F + f) * H);
+  const int tc = min(task, K * F - 1);  // clamped: loads stay unconditional
+  const int slot = tc / F, f = tc - slot * F;
+  const int ei = (scores != nullptr) ? L.topi[slot] : top_i[n * K + slot];
+  const bool ok = task < K * F && ei >= 0 && ei < E;  // else: contribute nothing
+  const u32x4* row = (const u32x4*)(gate_up + ((size_t)(max(min(ei, E - 1), 0) * 2 + half) * F + f) * H);
   u32x4 w[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 32 * i);
@@ -297,11 +294,11 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   for (int i = 0; i < IT; ++i) acc = dot8(w[i], xr[i], acc);
   acc = group_sum<32>(acc);
   const float up = __shfl(acc, 32, kWave);
-  if (lane == 0) {
+  if (lane == 0 && task < K * F) {
     const float tw = (scores != nullptr) ? L.topw[slot] : top_w[n * K + slot];
     const float g = rbf(acc), u = rbf(up);
     const float a = rbf(rbf(rbf(gelu_tanh(g)) * u) * rbf(tw));
-    act[((size_t)n * K + slot) * F + f] = f2bf(a);
+    act[((size_t)n * K + slot) * F + f] = ok ? f2bf(a) : (uint16_t)0;
   }
 }
 

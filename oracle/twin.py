@@ -170,16 +170,18 @@ def init_cache(cfg, batch: int, max_len: int) -> dict:
 
 # ----------------------------------------------------------------- blocks
 def attention_core(q, k_raw, v_raw, q_norm, k_norm, cos, sin, cache_k, cache_v, write_at, mask, kv_len, eps,
-                   softcap=None, precise=True):
+                   softcap=None, precise=True, inplace=False):
     """model.py:198-213 from the raw projections on: q [B,T,KV,G,D], k_raw/v_raw
     [B,T,KV,D] bf16 (v_raw is k_raw on k==v layers).  Returns (ctx
-    [B,T,KV,G,D] bf16, cache_k, cache_v)."""
+    [B,T,KV,G,D] bf16, cache_k, cache_v).  With `inplace` the caches are
+    updated in place (the reference donates them), else copied first."""
     q = apply_rope(rms_norm(q, q_norm, eps), cos, sin)
     k = apply_rope(rms_norm(k_raw, k_norm, eps), cos, sin)
     v = rms_norm(v_raw, None, eps)
     t = q.shape[1]
-    cache_k = cache_k.clone()
-    cache_v = cache_v.clone()
+    if not inplace:
+        cache_k = cache_k.clone()
+        cache_v = cache_v.clone()
     cache_k[:, write_at : write_at + t] = k
     cache_v[:, write_at : write_at + t] = v
     kk, vv = cache_k[:, :kv_len], cache_v[:, :kv_len]
@@ -192,7 +194,8 @@ def attention_core(q, k_raw, v_raw, q_norm, k_norm, cos, sin, cache_k, cache_v, 
     return ctx, cache_k, cache_v
 
 
-def attention(cfg, lp, x, layer_type, cos, sin, cache_k, cache_v, write_at, mask, kv_len, precise=True):
+def attention(cfg, lp, x, layer_type, cos, sin, cache_k, cache_v, write_at, mask, kv_len, precise=True,
+              inplace=False):
     """model.py:195-215.  x [B,T,H] bf16 (input_layernorm output); mask bool
     broadcastable to [B,KV,G,T,kv_len].  Returns (out [B,T,H], cache_k, cache_v)."""
     q = ein("bth,kgdh->btkgd", x, lp["q_proj"], precise)
@@ -200,7 +203,7 @@ def attention(cfg, lp, x, layer_type, cos, sin, cache_k, cache_v, write_at, mask
     v_raw = k_raw if cfg.k_eq_v_for(layer_type) else ein("bth,kdh->btkd", x, lp["v_proj"], precise)
     ctx, cache_k, cache_v = attention_core(q, k_raw, v_raw, lp["q_norm"], lp["k_norm"], cos, sin, cache_k, cache_v,
                                            write_at, mask, kv_len, cfg.rms_norm_eps,
-                                           getattr(cfg, "attn_logit_softcapping", None), precise)
+                                           getattr(cfg, "attn_logit_softcapping", None), precise, inplace)
     out = ein("btkgd,hkgd->bth", ctx, lp["o_proj"], precise)
     return out, cache_k, cache_v
 
@@ -268,12 +271,13 @@ def moe(cfg, lp, flat, dense: bool, precise=True, return_route=False):
     return (out, top_w, top_i) if return_route else out
 
 
-def layer(cfg, lp, x, layer_type, cos, sin, ck, cv, write_at, mask, kv_len, dense_moe, precise=True, trace=None):
+def layer(cfg, lp, x, layer_type, cos, sin, ck, cv, write_at, mask, kv_len, dense_moe, precise=True, trace=None,
+          inplace=False):
     """model.py:297-322.  `trace`, if a list, receives this layer's (top_w, top_i)."""
     eps = cfg.rms_norm_eps
     residual = x
     h = rms_norm(x, lp["input_layernorm"], eps)
-    h, ck, cv = attention(cfg, lp, h, layer_type, cos, sin, ck, cv, write_at, mask, kv_len, precise)
+    h, ck, cv = attention(cfg, lp, h, layer_type, cos, sin, ck, cv, write_at, mask, kv_len, precise, inplace)
     h = rms_norm(h, lp["post_attention_layernorm"], eps)
     x = rb(f32(residual) + f32(h))
 
@@ -294,7 +298,7 @@ def layer(cfg, lp, x, layer_type, cos, sin, ck, cv, write_at, mask, kv_len, dens
 
 
 def forward(cfg, params, tokens, positions, cache, write_at, masks, kv_len, dense_moe, last_index=None,
-            precise=True, trace=None):
+            precise=True, trace=None, inplace=False):
     """model.py:333-386 without sharding.  tokens [B,T] int; returns
     (logits f32 [B,T or 1,V], cache).  `trace`, if a list, receives per-layer
     routing (top_w, top_i)."""
@@ -309,7 +313,7 @@ def forward(cfg, params, tokens, positions, cache, write_at, masks, kv_len, dens
     for i, lt in enumerate(cfg.layer_types):
         cos, sin = rope[lt]
         x, ks[i], vs[i] = layer(cfg, layer_params(params, i), x, lt, cos, sin, ks[i], vs[i], write_at,
-                                masks[lt], kv_len, dense_moe, precise, trace)
+                                masks[lt], kv_len, dense_moe, precise, trace, inplace)
     x = rms_norm(x, params["norm"], cfg.rms_norm_eps)
     if last_index is not None:
         x = x[:, int(last_index) : int(last_index) + 1]
