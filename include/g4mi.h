@@ -202,6 +202,35 @@ int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* mo
 int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n, int32_t* tok, int32_t* pos,
                          int32_t* hist, int64_t hist_len, void* stream);
 
+/* Prompt feeding of a token-at-a-time prefill (engine.py:57-67 runs the whole
+ * prompt through forward; here each prompt token is one captured step):
+ * pos[0] += 1, then, if pos < feed_cap, tok[0] = feed[pos] and hist[pos] =
+ * tok[0] (when within hist_len).  feed holds the prompt at its positions. */
+int g4mi_advance_feed(const int32_t* feed, int64_t feed_cap, int32_t* tok, int32_t* pos, int32_t* hist,
+                      int64_t hist_len, void* stream);
+
+/* ---------------------------------------------------------------- sampling (K7)
+ * model.py:414-424 (sample): temperature <= 0 -> greedy (first index of the
+ * maximum logit); else top_k of logits / max(T, 1e-6) (descending, ties to
+ * the lower index), softmax, nucleus cut where the exclusive prefix sum
+ * (csum - p) >= top_p, renormalise, one draw.  The uniform is Philox4x32-10
+ * under params->seed at counter (step, 0x53414D50, 0, 0) with step = pos[0]
+ * when counter_mode != 0 (decode, engine.py:80) else 0 (after a prefill,
+ * engine.py:66); it is this library's stream, not JAX's.  `params` is a
+ * device g4mi_sample_params, read when the kernels run, so a captured step
+ * picks up new settings.  Writes tok[0]; with pos != NULL also advances it
+ * and records hist as g4mi_argmax_finalize does.  logits [V] f32, top_k <= 64;
+ * params and ws 8-byte aligned. */
+typedef struct g4mi_sample_params {
+  float temperature;
+  float top_p;
+  uint64_t seed;
+} g4mi_sample_params;
+int64_t g4mi_sample_workspace_bytes(int64_t V);
+int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* params, int32_t counter_mode,
+                int32_t* tok, int32_t* pos, int32_t* hist, int64_t hist_len, void* ws, int64_t ws_bytes,
+                void* stream);
+
 #ifdef __cplusplus
 }
 #endif

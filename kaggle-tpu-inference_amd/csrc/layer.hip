@@ -572,6 +572,19 @@ __global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ b
   }
 }
 
+// Teacher forcing through a prompt: pos += 1; tok = feed[pos]; hist[pos] = tok.
+__global__ void advance_feed_kernel(const int32_t* __restrict__ feed, int feed_cap, int32_t* tok, int32_t* pos,
+                                    int32_t* hist, int hist_len) {
+  if (threadIdx.x != 0) return;
+  const int p = pos[0] + 1;
+  pos[0] = p;
+  if (p >= 0 && p < feed_cap) {
+    const int t = feed[p];
+    tok[0] = t;
+    if (hist != nullptr && p < hist_len) hist[p] = t;
+  }
+}
+
 // Work units (row pairs, row groups or tasks) per block for the row walks:
 // about gemv_blocks() blocks (one per CU by default; G4MI_GEMV_BLOCKS
 // overrides it for tuning), 4 waves each, at least one unit per wave.
@@ -768,6 +781,15 @@ int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n
   hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(256), 0, as_stream(stream), blk_val, blk_idx, (int)n, tok, pos,
                      hist, (int)hist_len);
   return check_launch("argmax_finalize");
+}
+
+int g4mi_advance_feed(const int32_t* feed, int64_t feed_cap, int32_t* tok, int32_t* pos, int32_t* hist,
+                      int64_t hist_len, void* stream) {
+  G4MI_REQUIRE(feed && tok && pos && feed_cap >= 1 && feed_cap <= INT32_MAX, G4MI_EINVAL,
+               "advance_feed: missing argument");
+  hipLaunchKernelGGL(advance_feed_kernel, dim3(1), dim3(64), 0, as_stream(stream), feed, (int)feed_cap, tok, pos,
+                     hist, (int)hist_len);
+  return check_launch("advance_feed");
 }
 
 }  // extern "C"

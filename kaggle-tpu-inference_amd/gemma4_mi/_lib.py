@@ -67,6 +67,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _f32, _f32, _p, _p, _p, _p],
     ),
     "g4mi_argmax_finalize": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p]),
+    "g4mi_advance_feed": (_int, [_p, _i64, _p, _p, _p, _i64, _p]),
+    "g4mi_sample_workspace_bytes": (_i64, [_i64]),
+    "g4mi_sample": (_int, [_p, _i64, _i64, _p, _i32, _p, _p, _p, _i64, _p, _i64, _p]),
     "g4mi_kv_append": (
         _int,
         [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p],

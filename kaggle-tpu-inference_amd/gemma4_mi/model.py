@@ -211,6 +211,7 @@ class DecodeRunner:
             self.splits[lt] = ns
             ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, cfg.num_attention_heads, d, lmax, ns))
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        self.sample_ws = torch.zeros(ops.sample_workspace_bytes(cfg.vocab_size), dtype=torch.uint8, device=dev)
 
     def _splits(self, lt: str) -> int:
         cfg = self.cfg
@@ -220,10 +221,15 @@ class DecodeRunner:
         need = self.ops.attention_min_splits(span)
         return max(need, min(want, (span + 63) // 64))
 
-    def launch(self, combine: str = "bf16_running", advance: bool = True):
-        """Enqueues one token step reading tok/pos; with `advance` the argmax
-        kernel writes the next token to tok, increments pos and records the
-        token in hist[pos]."""
+    def launch(self, combine: str = "bf16_running", advance: bool = True, sampler=None, feed=None):
+        """Enqueues one token step reading tok/pos.
+
+        With `advance` the head writes the next token to tok, increments pos
+        and records the token in hist[pos].  The head is the greedy argmax,
+        or, with `sampler` = (params, top_k, counter_mode), the top-k/top-p
+        sampler (model.py:414-424).  With `feed` (a device int32 prompt
+        buffer) the step skips the lm_head and instead feeds the next prompt
+        token: pos += 1, tok = feed[pos], hist[pos] = tok."""
         ops, cfg, p = self.ops, self.cfg, self.params
         H, eps, NH = cfg.hidden_size, cfg.rms_norm_eps, cfg.num_attention_heads
         moe = cfg.enable_moe_block
@@ -265,13 +271,21 @@ class DecodeRunner:
             ops.ffn_out(self.act_mlp, lp["mlp.down_proj"], self.mlp_out, self.act_moe if moe else None,
                         lp.get("experts.down_proj"), self.top_i[i] if moe else None, cfg.top_k_experts, combine,
                         self.moe_out if moe else None, H)
+        if feed is not None:
+            ops.advance_feed(feed, self.tok, self.pos, self.hist)
+            return
         last = self.layers[-1]
         ops.lm_head(self.x1, self.mlp_out, self.moe_out if moe else None, last.get("post_feedforward_layernorm_1"),
                     last.get("post_feedforward_layernorm_2"), last["post_feedforward_layernorm"],
                     last["layer_scalar"], p["norm"], p["embed"], cfg.final_logit_softcapping, eps, self.logits,
                     self.blk_val, self.blk_idx)
-        ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos if advance else None,
-                            self.hist if advance else None)
+        if sampler is not None:
+            params, top_k, counter_mode = sampler
+            ops.sample(self.logits, top_k, params, self.tok, counter_mode, self.pos if advance else None,
+                       self.hist if advance else None, ws=self.sample_ws)
+        else:
+            ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos if advance else None,
+                                self.hist if advance else None)
 
     def set_state(self, token: int, pos: int) -> None:
         self.tok.fill_(int(token))

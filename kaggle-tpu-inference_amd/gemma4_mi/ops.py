@@ -378,6 +378,44 @@ def lm_head(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, fin
               float(eps), _ptr(logits), _ptr(blk_val), _ptr(blk_idx), stream_handle(embed.device))
 
 
+def advance_feed(feed, tok, pos, hist=None):
+    """pos += 1; tok = feed[pos]; hist[pos] = tok (teacher forcing through a prompt)."""
+    _need(feed, torch.int32, "feed")
+    _lib.call("g4mi_advance_feed", _ptr(feed), feed.numel(), _ptr(tok), _ptr(pos), _ptr(hist),
+              0 if hist is None else hist.numel(), stream_handle(tok.device))
+
+
 def argmax_finalize(blk_val, blk_idx, tok, pos=None, hist=None):
     _lib.call("g4mi_argmax_finalize", _ptr(blk_val), _ptr(blk_idx), blk_val.numel(), _ptr(tok), _ptr(pos),
               _ptr(hist), 0 if hist is None else hist.numel(), stream_handle(tok.device))
+
+
+# ------------------------------------------------------------------------- sampling
+def sample_params(temperature: float, top_p: float, seed: int, device, out: torch.Tensor | None = None):
+    """A device g4mi_sample_params {f32 temperature, f32 top_p, u64 seed} (16 bytes).
+    With `out`, the existing buffer is overwritten (stream-ordered copy)."""
+    import struct
+
+    raw = struct.pack("<ffQ", float(temperature), float(top_p), int(seed) & (2**64 - 1))
+    host = torch.frombuffer(bytearray(raw), dtype=torch.uint8)
+    if out is None:
+        out = torch.empty(16, dtype=torch.uint8, device=device)
+    out.copy_(host)
+    return out
+
+
+def sample_workspace_bytes(V: int) -> int:
+    return int(_lib.lib().g4mi_sample_workspace_bytes(V))
+
+
+def sample(logits, top_k: int, params, tok, counter_mode: int = 1, pos=None, hist=None, ws=None):
+    """model.py:414-424 on a device logits row [V] f32 -> tok [1] int32 (and
+    pos/hist advanced when given).  `params` from sample_params()."""
+    _need(logits, torch.float32, "logits")
+    V = logits.numel()
+    need = sample_workspace_bytes(V)
+    if ws is None:
+        ws = WORKSPACE.get(logits.device, "sample", need)
+    _lib.call("g4mi_sample", _ptr(logits), V, int(top_k), _ptr(params), int(counter_mode), _ptr(tok), _ptr(pos),
+              _ptr(hist), 0 if hist is None else hist.numel(), _ptr(ws), ws.numel(), stream_handle(logits.device))
+    return tok
