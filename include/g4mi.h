@@ -125,9 +125,12 @@ int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, cons
  *   page_table [B,max_pages] int32; pos [B] int32 (device).
  * With append != 0 the new K/V are normalised, roped and written at pos.
  * ctx [B,NH,D] bf16.  D in {64,128,256,512}; NH/KV in {1,2,4,8};
- * n_split_max >= g4mi_attention_min_splits(span), span = window (when
- * 0 < window < lmax) else lmax (a split holds <= 256 positions).  A position
- * outside [0, lmax) attends to nothing (ctx = 0). */
+ * g4mi_attention_min_splits(span) <= n_split_max <= 256, span = window (when
+ * 0 < window < lmax) else lmax (a split holds <= 256 positions, so span <=
+ * 65536).  A position outside [0, lmax) attends to nothing (ctx = 0).  The
+ * workspace holds arrival counters: zero-fill it once before first use (each
+ * call leaves the counters at zero); concurrent calls need separate
+ * workspaces. */
 int64_t g4mi_attention_min_splits(int64_t lmax);
 int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max);
 int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,

@@ -6,16 +6,16 @@
 // pt[b][p / PAGE], slot p % PAGE.  One (page, kv head) is PAGE*D contiguous
 // values, so a split of consecutive positions streams contiguous memory.
 //
-// Three kernels per call, split-K over positions:
-//   scores: q = rope(rms_norm(q_raw, q_norm)) for the G query heads of a KV
-//           head; the block whose split ends at `pos` also builds
-//           k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) and appends
-//           them to the cache; s = f32(bf16(q . k)) (scale 1.0), optional
-//           softcap, causal/sliding range; per-split max and sum of exp.
-//   pv:     merges the split statistics, p = bf16(exp(s - m) / sum) -- the
-//           reference rounds the normalised probabilities to bf16 before the
-//           PV product (model.py:212) -- and accumulates p . V in f32.
-//   reduce: ctx = bf16(sum of the split partials), in split order.
+// Two kernels per call, split-K over positions (grid: splits x KV heads x B):
+//   qk: q = rope(rms_norm(q_raw, q_norm)) for the G query heads of a KV
+//       head; the block whose split ends at `pos` also builds
+//       k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) and appends
+//       them to the cache; s = f32(bf16(q . k)) (scale 1.0) on MFMA,
+//       optional softcap, causal/sliding range; per-split max and sum of exp.
+//   pv: merges the split statistics, p = bf16(exp(s - m) / sum) -- the
+//       reference rounds the normalised probabilities to bf16 before the
+//       PV product (model.py:212) -- accumulates p . V in f32, and reduces the
+//       split partials in a fixed order into ctx = bf16(sum).
 // Masked positions contribute exp(-1e30 - m) = 0 in the reference, so only the
 // attended range [lo, pos] is visited.
 //
@@ -109,18 +109,25 @@ __device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const 
 }
 
 // ------------------------------------------------------------------ scores
-// grid (n_split_max, KV, B), 256 threads.  Wave steps cover PPW positions with
-// LPP = D/8 lanes each (one 16-byte chunk per lane).
+// grid (n_split_max, KV, B), 256 threads.  The G query heads of a KV head
+// (zero-padded to 16 rows) times K^T on MFMA: v_mfma_f32_16x16x32_bf16 takes
+// A = q rows [16 x 32 dims] and B = K^T [32 dims x 16 positions]; lane l holds
+// A[l%16][8(l/16)..+7], B[8(l/16)..+7][l%16] (16 contiguous bytes of the K row
+// of position l%16) and gets C[4(l/16)+i][l%16], i < 4.  Wave w takes the
+// 16-position tiles w, w+4, ... of the split; the next tile's K loads are in
+// flight while the current one is multiplied.
 template <int D, int G>
-__global__ __launch_bounds__(256) void attn_scores_kernel(
+__global__ __launch_bounds__(256) void attn_qk_kernel(
     AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
     const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
     const uint16_t* __restrict__ rope_cos, const uint16_t* __restrict__ rope_sin, uint16_t* __restrict__ k_pages,
     uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table, const int32_t* __restrict__ pos_arr,
     int append, float* __restrict__ ws_scores, float* __restrict__ ws_stats) {
-  constexpr int LPP = D / 8;
-  constexpr int PPW = 64 / LPP;
-  __shared__ float qs[G * D];
+  constexpr int PL = D / 64;
+  constexpr int GW = (G + 3) / 4;
+  constexpr int KS = D / 32;  // MFMA steps along the head dimension
+  __shared__ __align__(16) uint16_t qa[16 * D];
+  __shared__ __align__(16) uint16_t kn16[D];
   __shared__ float knew[D];
   __shared__ float vnew[D];
   __shared__ float sc[G][kChunkMax];
@@ -138,8 +145,6 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
 
   // Prologue, all loads first: wave w owns q heads w, w+4 (G <= 8); with the
   // append, waves 2 and 3 also own the new K and V rows.
-  constexpr int PL = D / 64;
-  constexpr int GW = (G + 3) / 4;
   const int so = lane * PL;                 // this lane's slice offset
   const int jo = so % (D / 2);              // its cos/sin offset
   const bool mine = append && (end == pos + 1);
@@ -158,20 +163,25 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
     load_slice<PL>((wave == 2 ? kr : vr) + so, kvx);
     load_slice<PL>(k_norm + so, kw);
   }
+  // padding rows G..15 of the A operand are zero
+  for (int c = tid; c < (16 - G) * D / 8; c += 256) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
     const int g = wave + 4 * u;
     if (g < G) {
       norm_rope_slice<D>(qx[u], qw, cs, sn, a.eps, true);
 #pragma unroll
-      for (int i = 0; i < PL; ++i) qs[g * D + so + i] = qx[u][i];
+      for (int i = 0; i < PL; ++i) qa[g * D + so + i] = f2bf(qx[u][i]);
     }
   }
   if (mine && wave >= 2) {
     norm_rope_slice<D>(kvx, wave == 2 ? kw : nullptr, cs, sn, a.eps, wave == 2);
     float* dst = (wave == 2) ? knew : vnew;
 #pragma unroll
-    for (int i = 0; i < PL; ++i) dst[so + i] = kvx[i];
+    for (int i = 0; i < PL; ++i) {
+      dst[so + i] = kvx[i];
+      if (wave == 2) kn16[so + i] = f2bf(kvx[i]);
+    }
   }
   __syncthreads();
   if (mine) {
@@ -183,47 +193,53 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
       }
   }
 
-  const int sub = lane % LPP, slot = lane / LPP;
-  float q[G][8];
+  const int kg = lane >> 4, col = lane & 15;
+  u32x4 af[KS];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) q[g][i] = qs[g * D + sub * 8 + i];
+  for (int s = 0; s < KS; ++s) af[s] = *(const u32x4*)(qa + col * D + 32 * s + 8 * kg);
   const float cap = a.softcap;
-  constexpr int U = 4;  // position steps per batch: U K loads in flight per lane
-  for (int base = wave * PPW * U; base < npos; base += 4 * PPW * U) {
-    // branch-free: page lookups for the batch, then the K loads from clamped
-    // addresses; masking is applied to the values (see layer.hip on vmcnt)
-    long long off[U];
+  const int ntiles = (npos + 15) >> 4;
+  auto load_tile = [&](int t, u32x4* bf, long long& off) {
+    const int jc = min(t * 16 + col, npos - 1);
+    off = page_off(a, pt_row, start + jc, kv);
+    const uint16_t* kp = k_pages + max(off, 0ll) + 8 * kg;
 #pragma unroll
-    for (int u = 0; u < U; ++u) off[u] = page_off(a, pt_row, start + min(base + u * PPW + slot, npos - 1), kv);
-    float kf[U][8];
-    bool ok[U];
+    for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
+  };
+  u32x4 bcur[KS];
+  long long ocur;
+  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur);
+  for (int t = wave; t < ntiles; t += 4) {
+    u32x4 bnext[KS];
+    long long onext;
+    load_tile(min(t + 4, ntiles - 1), bnext, onext);  // clamped: always in range
+    const int j = t * 16 + col;
+    const bool isnew = mine && (start + j == pos);
+    if (mine) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = base + u * PPW + slot;
-      unpack8(ld16(k_pages + max(off[u], 0ll) + sub * 8), kf[u]);
-      ok[u] = (j < npos) && (off[u] >= 0);
-      if (mine && start + j == pos && j < npos) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) kf[u][i] = knew[sub * 8 + i];
-        ok[u] = true;
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 nv = *(const u32x4*)(kn16 + 32 * s + 8 * kg);
+        bcur[s] = isnew ? nv : bcur[s];
       }
     }
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = base + u * PPW + slot;
+    for (int s = 0; s < KS; ++s)
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[s]),
+                                                    __builtin_bit_cast(bf16x8, bcur[s]), acc, 0, 0, 0);
+    const bool ok = (ocur >= 0) || isnew;
 #pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float acc = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc = fmaf(q[g][i], kf[u][i], acc);
-        acc = group_sum<LPP>(acc);
-        float sv = rbf(acc);
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G && j < npos) {
+        float sv = rbf(acc[i]);
         if (cap > 0.0f) sv = tanhf(sv / cap) * cap;
-        if (j < npos && sub == 0) sc[g][j] = ok[u] ? sv : -INFINITY;
+        sc[h][j] = ok ? sv : -INFINITY;
       }
     }
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bcur[s] = bnext[s];
+    ocur = onext;
   }
   __syncthreads();
 #pragma unroll
@@ -258,118 +274,239 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(
   }
 }
 
-// ------------------------------------------------------------------ pv
+// ------------------------------------------------------------------ pv + reduce
 // grid (n_split_max, KV, B), 256 threads.  Wave w owns the values
-// [w*D/4, (w+1)*D/4) of every head; LPV = D/32 lanes per position, so the
-// position-partials reduce inside the wave and no cross-wave pass is needed.
+// [w*D/4, (w+1)*D/4) of every head; LPV = D/32 lanes per position.  The
+// block's V loads are issued before the split statistics are merged.  Each
+// split writes its f32 partial [G, D]; the last split of each group of
+// kGroup to finish sums the group's partials in split order, and with more
+// than one group the last group to finish sums the group sums in order, so
+// ctx is deterministic (no float atomics).  The partials pass between blocks
+// through coherent (device-scope) 16-byte stores and loads, see arrive_last().
+constexpr int kGroup = 16;
+constexpr int kMaxSplits = 256;
+constexpr int kMaxGroups = kMaxSplits / kGroup;
+
+// sum[r] = sum over i < n (n <= 16, in order) of the float4 at byte offset
+// base + i*stride + 16*e4, e4 = threadIdx.x + 256*r < N4, read with coherent
+// loads (the sources were written by other blocks of this kernel).  All loads
+// of a half (8 sources) are issued before the first add, so a half costs one
+// round trip.
+template <int E4, int N4>
+__device__ __forceinline__ void ordered_sum(__amdgpu_buffer_rsrc_t rs, uint32_t base, uint32_t stride, int n,
+                                            float4* sum) {
+#pragma unroll
+  for (int r = 0; r < E4; ++r) sum[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int h0 = 0; h0 < kGroup; h0 += 8) {
+    if (h0 < n) {
+      float4 v[8][E4];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < E4; ++r) {
+          const int e4 = min((int)threadIdx.x + 256 * r, N4 - 1);
+          v[i][r] = coherent_load4(rs, base + (uint32_t)min(h0 + i, n - 1) * stride + 16u * (uint32_t)e4);
+        }
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < E4; ++r)
+          if (h0 + i < n) {
+            sum[r].x += v[i][r].x;
+            sum[r].y += v[i][r].y;
+            sum[r].z += v[i][r].z;
+            sum[r].w += v[i][r].w;
+          }
+    }
+  }
+}
+
+template <int E4, int N4>
+__device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
+#pragma unroll
+  for (int r = 0; r < E4; ++r) {
+    const int e4 = threadIdx.x + 256 * r;
+    if (e4 < N4) {
+      uint2 w;
+      w.x = pack2(sum[r].x, sum[r].y);
+      w.y = pack2(sum[r].z, sum[r].w);
+      ((uint2*)out)[e4] = w;
+    }
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
                                                       const int32_t* __restrict__ page_table,
                                                       const int32_t* __restrict__ pos_arr,
                                                       const float* __restrict__ ws_scores,
-                                                      const float* __restrict__ ws_stats, float* __restrict__ ws_part) {
+                                                      const float* __restrict__ ws_stats, float* ws_part,
+                                                      float* ws_group, unsigned int* counters,
+                                                      uint16_t* __restrict__ ctx) {
   constexpr int LPV = D / 32;
   constexpr int PPV = 64 / LPV;
+  constexpr int UB = 8;                        // wave steps of V loads in flight
+  constexpr int RS = G * kChunkMax / 256;      // scores per thread
+  constexpr int E4 = (G * D / 4 + 255) / 256;  // reduced float4s per thread
   __shared__ float pr[G][kChunkMax];
   __shared__ float mg[G], sg[G];
+  __shared__ int flag;
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = pos_arr[b];
   const Range R = attn_range(a, pos);
-  if (split >= R.n_eff) return;
+  if (split >= R.n_eff) {
+    if (R.n_eff == 0 && split == 0)  // nothing attended: ctx = 0
+      for (int e = tid; e < G * D; e += 256) ctx[(size_t)b * a.NH * D + (size_t)kv * G * D + e] = 0;
+    return;
+  }
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
-  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
-  for (int g = wave; g < G; g += 4) {
-    const int h = kv * G + g;
-    const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
-    const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
-    float m = -INFINITY;
-    for (int i = lane; i < R.n_eff; i += 64) m = fmaxf(m, sm[i]);
-    m = wave_max_bfly(m);
-    float t = 0.0f;
-    for (int i = lane; i < R.n_eff; i += 64) t += (sm[i] == -INFINITY) ? 0.0f : expf(sm[i] - m) * sl[i];
-    t = group_sum<64>(t);
-    if (lane == 0) {
-      mg[g] = m;
-      sg[g] = t;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float* srow = ws_scores + ((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo);
-    for (int j = tid; j < npos; j += 256) {
-      const float s = srow[j];
-      pr[g][j] = (s == -INFINITY) ? 0.0f : rbf(expf(s - mg[g]) / sg[g]);
-    }
-  }
-  __syncthreads();
+  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
   const int sub = lane % LPV, slot = lane / LPV;
   const int dofs = wave * (D / 4) + sub * 8;
+
+  // loads in the order they are needed: split statistics, this split's
+  // scores, then the first batch of V rows
+  float st_m[kMaxSplits / 64], st_l[kMaxSplits / 64];
+  const int g_st = wave;  // heads wave, wave+4 merged below
+  float sreg[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int idx = tid + 256 * r, g = idx / kChunkMax, j = idx % kChunkMax;
+    sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo) + min(j, npos - 1)];
+  }
+  const int nsteps = (npos + PPV - 1) / PPV;
+  auto vload = [&](int st0, u32x4* vf, bool* okv) {
+#pragma unroll
+    for (int u = 0; u < UB; ++u) {
+      const int j = (st0 + u) * PPV + slot;
+      const long long off = page_off(a, pt_row, start + min(j, npos - 1), kv);
+      vf[u] = ld16((const u32x4*)(v_pages + max(off, 0ll) + dofs));
+      okv[u] = (j < npos) && (off >= 0);
+    }
+  };
+  u32x4 vcur[UB];
+  bool okcur[UB];
+  vload(0, vcur, okcur);
+  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
+#pragma unroll
+  for (int u = 0; u < (G + 3) / 4; ++u) {
+    const int g = g_st + 4 * u;
+    if (g < G) {
+      const int h = kv * G + g;
+      const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
+      const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) {
+        const int ic = min(lane + 64 * q, R.n_eff - 1);
+        st_m[q] = sm[ic];
+        st_l[q] = sl[ic];
+      }
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) {
+        const bool in = lane + 64 * q < R.n_eff;
+        st_m[q] = in ? st_m[q] : -INFINITY;
+        st_l[q] = in ? st_l[q] : 0.0f;
+      }
+      float m = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) m = fmaxf(m, st_m[q]);
+      m = wave_max_bfly(m);
+      float t = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) t += (st_m[q] == -INFINITY) ? 0.0f : expf(st_m[q] - m) * st_l[q];
+      t = group_sum<64>(t);
+      if (lane == 0) {
+        mg[g] = m;
+        sg[g] = t;
+      }
+    }
+  }
+  __syncthreads();
+  // normalised probabilities, rounded to bf16 as the reference does (model.py:212)
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int idx = tid + 256 * r, g = idx / kChunkMax, j = idx % kChunkMax;
+    const float s = sreg[r];
+    if (j < npos) pr[g][j] = (s == -INFINITY) ? 0.0f : rbf(expf(s - mg[g]) / sg[g]);
+  }
+  __syncthreads();
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
-  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
-  constexpr int U = 4;  // positions per batch: U V loads in flight per lane
-  for (int j0 = slot; j0 < npos; j0 += PPV * U) {
-    long long off[U];
+  for (int st0 = 0; st0 < nsteps; st0 += UB) {
+    u32x4 vnext[UB];
+    bool oknext[UB];
+    if (st0 + UB < nsteps) vload(st0 + UB, vnext, oknext);
 #pragma unroll
-    for (int u = 0; u < U; ++u) off[u] = page_off(a, pt_row, start + min(j0 + u * PPV, npos - 1), kv);
-    float vf[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u) unpack8(ld16(v_pages + max(off[u], 0ll) + dofs), vf[u]);
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int j = j0 + u * PPV;
-      const bool ok = (j < npos) && (off[u] >= 0);
+    for (int u = 0; u < UB; ++u) {
+      const int j = (st0 + u) * PPV + slot;
+      float vf[8];
+      unpack8(vcur[u], vf);
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float p = ok ? pr[g][min(j, npos - 1)] : 0.0f;
+        const float p = okcur[u] ? pr[g][min(j, npos - 1)] : 0.0f;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[u][i], acc[g][i]);
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+      }
+    }
+    if (st0 + UB < nsteps) {
+#pragma unroll
+      for (int u = 0; u < UB; ++u) {
+        vcur[u] = vnext[u];
+        okcur[u] = oknext[u];
       }
     }
   }
-  float* part = ws_part + (((size_t)b * a.n_split_max + split) * a.NH + kv * G) * D;
+  const size_t hd = (size_t)kv * G * D;  // offset of this KV head's group in [NH, D]
+  const uint32_t sstride = (uint32_t)(a.NH * D * 4);  // bytes per split partial
+  const __amdgpu_buffer_rsrc_t rpart = buffer_rsrc(ws_part, (uint32_t)(a.B * a.n_split_max) * sstride);
+  const uint32_t pbase = (uint32_t)(((size_t)b * a.n_split_max + split) * sstride + hd * 4);
 #pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[g][i];
-#pragma unroll
-      for (int m = LPV; m < 64; m <<= 1) v += __shfl_xor(v, m, kWave);
-      if (slot == 0) part[g * D + dofs + i] = v;
-    }
-}
-
-// ------------------------------------------------------------------ reduce
-__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int32_t* __restrict__ pos_arr,
-                                                          const float* __restrict__ ws_part,
-                                                          uint16_t* __restrict__ ctx) {
-  const int b = blockIdx.y;
-  const int idx = blockIdx.x * 256 + threadIdx.x;  // h*D + d
-  if (idx >= a.NH * a.D) return;
-  const Range R = attn_range(a, pos_arr[b]);
-  const size_t stride = (size_t)a.NH * a.D;
-  const float* src = ws_part + (size_t)b * a.n_split_max * stride + idx;
-  float acc[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) acc[u] = 0.0f;
-  int i = 0;
-  for (; i + 8 <= R.n_eff; i += 8) {
+  for (int g = 0; g < G; ++g) {
     float v[8];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = src[(size_t)(i + u) * stride];
+    for (int i = 0; i < 8; ++i) {
+      v[i] = acc[g][i];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc[u] += v[u];
+      for (int m = LPV; m < 64; m <<= 1) v[i] += __shfl_xor(v[i], m, kWave);
+    }
+    if (slot == 0) {
+      const uint32_t o = pbase + (uint32_t)(g * D + dofs) * 4;
+      coherent_store4(rpart, o, make_float4(v[0], v[1], v[2], v[3]));
+      coherent_store4(rpart, o + 16, make_float4(v[4], v[5], v[6], v[7]));
+    }
   }
-  for (; i < R.n_eff; ++i) acc[0] += src[(size_t)i * stride];
-  const float s = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
-  ctx[(size_t)b * stride + idx] = f2bf(s);
+
+  // two-level ordered reduction of the partials
+  const int grp = split / kGroup;
+  const int ngroups = (R.n_eff + kGroup - 1) / kGroup;
+  const int gsz = min(kGroup, R.n_eff - grp * kGroup);
+  unsigned int* cnt = counters + ((size_t)b * a.KV + kv) * (kMaxGroups + 1);
+  if (!arrive_last(cnt + 1 + grp, (unsigned)gsz, &flag)) return;
+  float4 sum[E4];
+  ordered_sum<E4, G * D / 4>(rpart, (uint32_t)(((size_t)b * a.n_split_max + grp * kGroup) * sstride + hd * 4),
+                             sstride, gsz, sum);
+  uint16_t* out = ctx + (size_t)b * a.NH * D + hd;
+  if (ngroups == 1) {
+    store_bf16x4<E4, G * D / 4>(out, sum);
+    return;
+  }
+  const __amdgpu_buffer_rsrc_t rgrp = buffer_rsrc(ws_group, (uint32_t)(a.B * kMaxGroups) * sstride);
+  const uint32_t gbase = (uint32_t)((size_t)b * kMaxGroups * sstride + hd * 4);
+#pragma unroll
+  for (int r = 0; r < E4; ++r) {
+    const int e4 = threadIdx.x + 256 * r;
+    if (e4 < G * D / 4) coherent_store4(rgrp, gbase + (uint32_t)grp * sstride + 16u * (uint32_t)e4, sum[r]);
+  }
+  if (!arrive_last(cnt, (unsigned)ngroups, &flag)) return;
+  ordered_sum<E4, G * D / 4>(rgrp, gbase, sstride, ngroups, sum);
+  store_bf16x4<E4, G * D / 4>(out, sum);
 }
 
 // ------------------------------------------------------------------ append
@@ -411,14 +548,20 @@ __global__ __launch_bounds__(128) void kv_append_kernel(AttnDims a, const uint16
 }
 
 // ------------------------------------------------------------------ launch
+struct AttnWs {
+  float *scores, *stats, *part, *group;
+  unsigned int* counters;
+};
+
 template <int D, int G>
 static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint16_t* q_raw, const uint16_t* k_raw,
                         const uint16_t* v_raw, const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* cs,
                         const uint16_t* sn, uint16_t* kp, uint16_t* vp, const int32_t* pt, const int32_t* pos,
-                        int append, float* ws_scores, float* ws_stats, float* ws_part) {
-  hipLaunchKernelGGL((attn_scores_kernel<D, G>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm, cs,
-                     sn, kp, vp, pt, pos, append, ws_scores, ws_stats);
-  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(256), 0, st, a, vp, pt, pos, ws_scores, ws_stats, ws_part);
+                        int append, const AttnWs& w, uint16_t* ctx) {
+  hipLaunchKernelGGL((attn_qk_kernel<D, G>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm, cs, sn,
+                     kp, vp, pt, pos, append, w.scores, w.stats);
+  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
+                     w.group, w.counters, ctx);
 }
 
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
@@ -430,7 +573,8 @@ using namespace g4mi;
 extern "C" {
 
 int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max) {
-  return al256(B * NH * lmax * 4) + al256(2 * B * NH * n_split_max * 4) + al256(B * n_split_max * NH * D * 4);
+  return al256(B * NH * lmax * 4) + al256(2 * B * NH * n_split_max * 4) + al256(B * n_split_max * NH * D * 4) +
+         al256(B * kMaxGroups * NH * D * 4) + al256(B * NH * (kMaxGroups + 1) * 4);
 }
 
 int64_t g4mi_attention_min_splits(int64_t lmax) { return (lmax + kChunkMax - 1) / kChunkMax; }
@@ -456,9 +600,11 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
                "decode_attention: bad page_size/max_pages/num_pages/lmax");
   G4MI_REQUIRE(window >= 0, G4MI_EINVAL, "decode_attention: negative window");
   const int64_t span = (window > 0 && window < lmax) ? window : lmax;  // most positions one query attends
-  G4MI_REQUIRE(n_split_max >= g4mi_attention_min_splits(span) && n_split_max <= 65535, G4MI_EINVAL,
+  G4MI_REQUIRE(n_split_max >= g4mi_attention_min_splits(span) && n_split_max <= kMaxSplits, G4MI_EINVAL,
                "decode_attention: n_split_max %lld < %lld (a split holds at most %d positions)",
                (long long)n_split_max, (long long)g4mi_attention_min_splits(span), kChunkMax);
+  G4MI_REQUIRE(B * n_split_max * NH * D * 4 < ((int64_t)1 << 31), G4MI_EUNSUPPORTED,
+               "decode_attention: B * n_split_max * NH * D partials exceed 2 GiB");
   G4MI_REQUIRE(((uintptr_t)k_pages & 15u) == 0 && ((uintptr_t)v_pages & 15u) == 0, G4MI_EALIGN,
                "decode_attention: cache pages must be 16-byte aligned");
   G4MI_REQUIRE(ws_bytes >= g4mi_decode_attention_workspace_bytes(B, NH, D, lmax, n_split_max), G4MI_EWORKSPACE,
@@ -467,22 +613,23 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
   a.B = (int)B; a.NH = (int)NH; a.KV = (int)KV; a.G = (int)G; a.D = (int)D; a.page = (int)page_size;
   a.max_pages = (int)max_pages; a.num_pages = (int)num_pages; a.window = (int)window;
   a.n_split_max = (int)n_split_max; a.lmax = (int)lmax; a.softcap = softcap; a.eps = eps;
-  float* ws_scores = (float*)ws;
-  float* ws_stats = (float*)((char*)ws + al256(B * NH * lmax * 4));
-  float* ws_part = (float*)((char*)ws_stats + al256(2 * B * NH * n_split_max * 4));
+  AttnWs w;
+  w.scores = (float*)ws;
+  w.stats = (float*)((char*)w.scores + al256(B * NH * lmax * 4));
+  w.part = (float*)((char*)w.stats + al256(2 * B * NH * n_split_max * 4));
+  w.group = (float*)((char*)w.part + al256(B * n_split_max * NH * D * 4));
+  w.counters = (unsigned int*)((char*)w.group + al256(B * kMaxGroups * NH * D * 4));
   hipStream_t st = as_stream(stream);
   dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
 #define G4MI_ATT(DD, GG)                                                                                         \
   if (D == DD && G == GG)                                                                                        \
     launch_attn<DD, GG>(a, grid, st, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, \
-                        page_table, pos, append, ws_scores, ws_stats, ws_part);
+                        page_table, pos, append, w, ctx);
   G4MI_ATT(64, 1) G4MI_ATT(64, 2) G4MI_ATT(64, 4) G4MI_ATT(64, 8)
   G4MI_ATT(128, 1) G4MI_ATT(128, 2) G4MI_ATT(128, 4) G4MI_ATT(128, 8)
   G4MI_ATT(256, 1) G4MI_ATT(256, 2) G4MI_ATT(256, 4) G4MI_ATT(256, 8)
   G4MI_ATT(512, 1) G4MI_ATT(512, 2) G4MI_ATT(512, 4) G4MI_ATT(512, 8)
 #undef G4MI_ATT
-  hipLaunchKernelGGL(attn_reduce_kernel, dim3((unsigned)((NH * D + 255) / 256), (unsigned)B), dim3(256), 0, st, a,
-                     pos, ws_part, ctx);
   return check_launch("decode_attention");
 }
 

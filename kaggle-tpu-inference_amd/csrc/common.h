@@ -12,6 +12,8 @@
 namespace g4mi {
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));  // MFMA bf16 operand (16 bytes)
+typedef float f32x4 __attribute__((ext_vector_type(4)));    // MFMA 16x16 accumulator per lane
 
 constexpr int kWave = 64;
 
@@ -176,24 +178,42 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * cdf;
 }
 
-// ------------------------------------------------------------------ last-block
-// Returns true in every thread of the block that arrives last at `counter`
-// (device-scope), after making the block's prior global writes visible.  The
-// last block resets the counter so the next launch (or graph replay) starts
-// from zero.
+// Cross-block hand-off inside one kernel without flushing the L2 caches.
+// On gfx950 each XCD has its own L2; a __threadfence() writes back and
+// invalidates the whole L2 of the calling XCD, which costs microseconds.
+// Data that another block will read is instead written and read with
+// device-scope (sc1) buffer stores and loads, coherent across the XCD L2s by
+// themselves (the gfx94x/gfx950 memory model emits the same sc1 accesses for
+// agent-scope atomics).  arrive_last() waits until the block's own stores
+// have completed (s_waitcnt vmcnt(0)), then counts the block in; the block
+// that brings the count to `total` gets true, resets the counter for the
+// next launch or graph replay, and may then read every block's coherent
+// stores with coherent_load4.  Buffer accesses outside the resource's range
+// read zero and write nothing.
+constexpr int kCPolSC1 = 16;  // cache-policy bit: device scope
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ void coherent_store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+  u32x4 w;
+  w.x = __float_as_uint(v.x); w.y = __float_as_uint(v.y); w.z = __float_as_uint(v.z); w.w = __float_as_uint(v.w);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, kCPolSC1);
+}
+__device__ __forceinline__ float4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCPolSC1);
+  return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
+}
 __device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int total, int* flag_lds) {
-  __threadfence();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (threadIdx.x == 0) {
-    unsigned int prev = atomicAdd(counter, 1u);
-    int last = (prev == total - 1);
+    const unsigned int prev = atomicAdd(counter, 1u);
+    const int last = (prev == total - 1);
     if (last) atomicExch(counter, 0u);
     *flag_lds = last;
   }
   __syncthreads();
-  const bool last = *flag_lds != 0;
-  if (last) __threadfence();
-  return last;
+  return *flag_lds != 0;
 }
 
 }  // namespace g4mi

@@ -78,9 +78,10 @@ def test_host_size_helpers(lib):
     assert lib.g4mi_moe_router_workspace_bytes(3, 16) == 256
     assert lib.g4mi_moe_experts_workspace_bytes(8, 704, 8) == 8 * 8 * 704 * 2
     assert lib.g4mi_moe_block_workspace_bytes(1, 128, 704, 8) == 512 + 11264
-    # scores [B,NH,lmax] f32 + stats [2,B,NH,splits] f32 + partials [B,splits,NH,D] f32, each 256-aligned
+    # scores [B,NH,lmax] f32 + stats [2,B,NH,splits] f32 + partials [B,splits,NH,D] f32 + group sums
+    # [B,16,NH,D] f32 + arrival counters [B,NH,17] u32, each 256-aligned
     assert lib.g4mi_decode_attention_workspace_bytes(1, 16, 512, 32768, 128) == (
-        16 * 32768 * 4 + 2 * 16 * 128 * 4 + 128 * 16 * 512 * 4)
+        16 * 32768 * 4 + 2 * 16 * 128 * 4 + 128 * 16 * 512 * 4 + 16 * 16 * 512 * 4 + 1280)
 
 
 def _expect(rc, code, fragment):
@@ -111,6 +112,8 @@ def test_unsupported_shapes_are_reported(lib):
     _expect(lib.g4mi_decode_attention(*([fake] * 9), 4, fake, 1, fake, 1, 16, 8, 96, 64, 0, 0.0, 1e-6, 0, 128, 1,
                                       fake, fake, 1 << 30, None), EUNSUPPORTED, "head_dim")
     _expect(lib.g4mi_decode_attention(*([fake] * 9), 4, fake, 1, fake, 1, 16, 8, 256, 64, 0, 0.0, 1e-6, 0, 32768, 8,
+                                      fake, fake, 1 << 30, None), EINVAL, "n_split_max")
+    _expect(lib.g4mi_decode_attention(*([fake] * 9), 4, fake, 1, fake, 1, 16, 8, 256, 64, 0, 0.0, 1e-6, 0, 32768, 257,
                                       fake, fake, 1 << 30, None), EINVAL, "n_split_max")
 
 
