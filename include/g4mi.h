@@ -161,7 +161,9 @@ int g4mi_kv_append(const uint16_t* k_raw, const uint16_t* v_raw, const uint16_t*
  *           rms_norm(moe_out, post_ff_2)) (hs = mlp_out when moe_out is NULL)
  *                                                              (model.py:312-322)
  *   mode 2: x_in.
- * x is also stored to x_out.  qkv_out = [q rows | k rows | v rows] bf16. */
+ *   mode 3: x_in is already rms_norm(x, input_layernorm) (as g4mi_ffn_out's
+ *           epilogue writes it); input_ln and x_out are not used.
+ * Modes 0-2 also store x to x_out.  qkv_out = [q rows | k rows | v rows] bf16. */
 int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64_t vocab, const uint16_t* x_in,
                   const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
                   const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
@@ -176,18 +178,34 @@ int g4mi_oproj(const uint16_t* ctx, const uint16_t* w, int64_t rows, int64_t K, 
  * act_mlp[I] = bf16(bf16(gelu(g)) * u) of the dense MLP on rms_norm(x1,
  * pre_feedforward_layernorm) (model.py:218-220, 310); with router_proj,
  * xe = rms_norm(x1, pre_feedforward_layernorm_2) (model.py:315) and the
- * router scores [E] on it (model.py:225-227). */
+ * router scores [E] on it (model.py:225-227).  With per_expert_scale also the
+ * expert selection of model.py:228-231 (softmax, top-k, renormalisation,
+ * per-expert scale) -> top_w [k] f32, top_i [k] int32, computed once by the
+ * last router block to finish; E <= 256, k <= 32.  The workspace holds that
+ * block's arrival counter: zero-fill it once (each call leaves it at zero). */
+int64_t g4mi_ffn_in_workspace_bytes(void);
 int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_ln, const uint16_t* pre_ff_ln,
                 const uint16_t* pre_ff2_ln, uint16_t* x1_out, uint16_t* xe_out, const uint16_t* gate,
                 const uint16_t* up, int64_t I, uint16_t* act_mlp, const uint16_t* router_scale,
-                const uint16_t* router_proj, int64_t E, float* scores, int64_t H, float eps, void* stream);
+                const uint16_t* router_proj, int64_t E, float* scores, const uint16_t* per_expert_scale, int64_t k,
+                float* top_w, int32_t* top_i, void* ws, int64_t ws_bytes, int64_t H, float eps, void* stream);
 
 /* mlp_out[H] = act_mlp . down[H, I] (model.py:221) and, with experts_down,
  * moe_out[H] = the combine of the k selected experts' down rows applied to
- * act_moe [k, F] (model.py:272-293 / model.py:250 by `combine`).  k <= 8. */
+ * act_moe [k, F] (model.py:272-293 / model.py:250 by `combine`).  k <= 8.
+ * With next_ln, the last block to finish also applies the layer tail
+ * (model.py:312-322: x_out = bf16(bf16(x1 + rms_norm(hs, post_ff)) *
+ * layer_scalar), hs as in g4mi_layer_in mode 1) and the next norm
+ * (model.py:298 or the final norm, model.py:373): xn_out = rms_norm(x_out,
+ * next_ln).  H <= 4096 then.  The workspace holds that block's arrival
+ * counter: zero-fill it once (each call leaves it at zero). */
+int64_t g4mi_ffn_out_workspace_bytes(void);
 int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint16_t* mlp_out,
                  const uint16_t* act_moe, const uint16_t* experts_down, const int32_t* top_i, int64_t E, int64_t k,
-                 int64_t F, int32_t combine, uint16_t* moe_out, int64_t H, void* stream);
+                 int64_t F, int32_t combine, uint16_t* moe_out, const uint16_t* x1, const uint16_t* post_ff1_ln,
+                 const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                 const uint16_t* next_ln, uint16_t* x_out, uint16_t* xn_out, float eps, void* ws, int64_t ws_bytes,
+                 int64_t H, void* stream);
 
 /* The last layer's tail (as g4mi_layer_in mode 1), the final norm
  * (model.py:373), logits[V] f32 = softcap(f32(bf16(x . embed[v])))
@@ -202,6 +220,11 @@ int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* mo
 /* Greedy token (model.py:416: first index of the maximum) from the per-block
  * maxima -> tok[0].  With pos != NULL also pos[0] += 1 and hist[pos[0]] = token
  * (when within hist_len), so a captured decode step advances on its own. */
+/* logits and per-block maxima as g4mi_lm_head from an input that is already
+ * rms_norm(x, final_norm) (g4mi_ffn_out's epilogue writes it). */
+int g4mi_lm_head_normed(const uint16_t* xn, const uint16_t* embed, int64_t V, int64_t H, float softcap,
+                        float* logits, float* blk_val, int32_t* blk_idx, void* stream);
+
 int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n, int32_t* tok, int32_t* pos,
                          int32_t* hist, int64_t hist_len, void* stream);
 

@@ -23,17 +23,24 @@ __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 
 __device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 
 // f32 -> bf16, round to nearest even (NaN stays NaN).
-__device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// f32 -> bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32; NaN stays
+// a quiet NaN).  One instruction converts a pair.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 // Round an f32 to the nearest bf16 and return it as f32.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+// f64 -> f32, kept opaque: the reference rounds f64 results to f32 first, and
+// without the barrier the compiler fuses f64 -> f32 -> bf16 into a single
+// f64 -> bf16 rounding, which differs in rare halfway cases.
+__device__ __forceinline__ float f32_of(double d) {
+  float f = (float)d;
+  asm volatile("" : "+v"(f));
+  return f;
+}
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) {
-  return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // 8 bf16 in a 16-byte vector -> 8 f32.
@@ -199,6 +206,12 @@ __device__ __forceinline__ void coherent_store4(__amdgpu_buffer_rsrc_t r, uint32
   w.x = __float_as_uint(v.x); w.y = __float_as_uint(v.y); w.z = __float_as_uint(v.z); w.w = __float_as_uint(v.w);
   __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, kCPolSC1);
 }
+__device__ __forceinline__ u32x4 coherent_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCPolSC1);
+}
+__device__ __forceinline__ void coherent_store_bf16(uint16_t* p, uint16_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 __device__ __forceinline__ float4 coherent_load4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCPolSC1);
   return make_float4(__uint_as_float(w.x), __uint_as_float(w.y), __uint_as_float(w.z), __uint_as_float(w.w));
@@ -214,6 +227,21 @@ __device__ __forceinline__ bool arrive_last(unsigned int* counter, unsigned int 
   }
   __syncthreads();
   return *flag_lds != 0;
+}
+
+// arrive_last for a large grid: device-scope atomics on one address
+// serialise (~20 ns each), so blocks first arrive on their group's counter
+// (kArriveGroup consecutive blocks, counters 128 bytes apart) and the last of
+// each group on the top counter.  counters: 1 + 32 * ceil(gridDim.x / 32)
+// words, zero between launches (each launch leaves them at zero).
+constexpr int kArriveGroup = 32;
+constexpr int kArriveStride = 32;  // words between group counters
+__device__ __forceinline__ bool arrive_last_grid(unsigned int* counters, int* flag_lds) {
+  const unsigned int nb = gridDim.x, grp = blockIdx.x / kArriveGroup;
+  const unsigned int ng = (nb + kArriveGroup - 1) / kArriveGroup;
+  const unsigned int gsz = min((unsigned int)kArriveGroup, nb - grp * kArriveGroup);
+  if (!arrive_last(counters + kArriveStride * (1 + grp), gsz, flag_lds)) return false;
+  return arrive_last(counters, ng, flag_lds);
 }
 
 }  // namespace g4mi

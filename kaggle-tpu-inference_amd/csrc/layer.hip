@@ -29,6 +29,7 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "select.h"
 
 namespace g4mi {
 
@@ -45,6 +46,15 @@ __device__ __forceinline__ void vload(Vec& v, const uint16_t* __restrict__ p, in
   for (int j = 0; j < kVecChunks; ++j) {
     const int c = threadIdx.x + 256 * j;
     v.c[j] = (c < nch) ? ld16((const u32x4*)p + c) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+// vload of a vector other blocks of this kernel wrote with coherent stores
+__device__ __forceinline__ void vload_coherent(Vec& v, const uint16_t* p, int nch) {
+  const __amdgpu_buffer_rsrc_t r = buffer_rsrc(p, (uint32_t)nch * 16u);
+#pragma unroll
+  for (int j = 0; j < kVecChunks; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    v.c[j] = (c < nch) ? coherent_load16(r, (uint32_t)c * 16u) : u32x4{0u, 0u, 0u, 0u};
   }
 }
 __device__ __forceinline__ double vsumsq(const Vec& v, int nch) {
@@ -175,7 +185,7 @@ __device__ __forceinline__ float dot_row(const u32x4* w, const u32x4* __restrict
 }
 
 // ------------------------------------------------------------------ layer_in
-enum { kInEmbed = 0, kInTail = 1, kInPlain = 2 };
+enum { kInEmbed = 0, kInTail = 1, kInPlain = 2, kInNormed = 3 };
 struct InArgs {
   int mode;
   const int32_t* tok;
@@ -211,6 +221,8 @@ struct PairWalk {
   }
 };
 
+constexpr int kInPrefetch = 4;  // row pairs per wave in flight in layer_in
+
 template <int IT, int MODE>
 __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   constexpr int H = IT * 256;
@@ -233,7 +245,7 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   // branch merge forces an early full wait.
   Vec x, win;
   TailRegs T;
-  vload(win, a.w_in, NCH);
+  if constexpr (MODE != kInNormed) vload(win, a.w_in, NCH);
   if constexpr (MODE == kInEmbed) {
     int t = a.tok[0];
     t = (t < 0 || t >= a.vocab) ? 0 : t;
@@ -243,23 +255,42 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   } else {
     vload(x, a.x_in, NCH);
   }
+  // The compiler may not sink the prologue loads below the row loads (their
+  // results would then wait for the rows).  One row batch per wave is
+  // requested before the prologue, the rest after it: issuing all of them
+  // first would hold the prologue's instructions behind the CU's memory queue.
+  asm volatile("" ::: "memory");
   PairWalk<IT> pw(a.pairs_per_block, (total + 1) / 2);
-  u32x4 w[IT];
-  load_row<32, IT>(rowptr(min(pw.p, pw.plast)), l, w);
+  constexpr int NPF = kInPrefetch;
+  u32x4 w[NPF][IT];
+  load_row<32, IT>(rowptr(min(pw.p, pw.plast)), l, w[0]);
   if constexpr (MODE == kInEmbed) vmul(x, a.embed_c);
   if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
-  if (blockIdx.x == 0) vstore(x, (u32x4*)a.x_out, NCH);
-  vscale_w(x, vrms(x, NCH, H, a.eps, red), win);
+  if constexpr (MODE != kInNormed) {
+    if (blockIdx.x == 0 && a.x_out != nullptr) vstore(x, (u32x4*)a.x_out, NCH);
+    vscale_w(x, vrms(x, NCH, H, a.eps, red), win);
+  }
   vstore(x, xs, NCH);
-  __syncthreads();
-  for (; pw.p < pw.pend; pw.p += 4) {
-    u32x4 wn[IT];
-    load_row<32, IT>(rowptr(min(pw.p + 4, pw.plast)), l, wn);
-    const float acc = dot_row<32, IT>(w, xs, l);
-    const int r = 2 * pw.p + half;
-    if (r < total && l == 0) a.out[r] = f2bf(acc);
 #pragma unroll
-    for (int i = 0; i < IT; ++i) w[i] = wn[i];
+  for (int d = 1; d < NPF; ++d) load_row<32, IT>(rowptr(min(pw.p + 4 * d, pw.plast)), l, w[d]);
+  __syncthreads();
+  int p = pw.p;
+  // full batches: consume pair p+4d, refill it with pair p+4d+4*NPF (clamped)
+  for (; p + 4 * NPF < pw.pend; p += 4 * NPF) {
+#pragma unroll
+    for (int d = 0; d < NPF; ++d) {
+      const float acc = dot_row<32, IT>(w[d], xs, l);
+      const int r = 2 * (p + 4 * d) + half;
+      if (r < total && l == 0) a.out[r] = f2bf(acc);
+      load_row<32, IT>(rowptr(min(p + 4 * d + 4 * NPF, pw.plast)), l, w[d]);
+    }
+  }
+  // last batch: no refills
+#pragma unroll
+  for (int d = 0; d < NPF; ++d) {
+    const float acc = dot_row<32, IT>(w[d], xs, l);
+    const int r = 2 * (p + 4 * d) + half;
+    if (p + 4 * d < pw.pend && r < total && l == 0) a.out[r] = f2bf(acc);
   }
 }
 
@@ -305,6 +336,11 @@ struct FfnInArgs {
   int E;
   float r_c;                   // bf16(H^-0.5)
   float* scores;               // [E]
+  const uint16_t* pes;         // per_expert_scale [E] (null: no selection)
+  int K;                       // experts per token
+  float* top_w;                // [K]
+  int32_t* top_i;              // [K]
+  unsigned int* counter;       // router-block arrivals (zero between launches)
   int H;
   float eps;
 };
@@ -381,7 +417,23 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
       else d0 = dot8_f64(w[i], xs[l + 32 * i], d0);
     }
     const double acc = group_sum_f64<32>(d0 + d1);
-    if (e < a.E && l == 0) a.scores[e] = rbf((float)acc);
+    if (e < a.E && l == 0)
+      __hip_atomic_store(a.scores + e, rbf(f32_of(acc)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (a.pes == nullptr) return;
+    // the last router block to finish selects the experts (model.py:228-231)
+    // once, so the expert kernel starts from the routing instead of the scores
+    __shared__ SelectLds L;
+    __shared__ int flag;
+    if (!arrive_last(a.counter, (unsigned)(gridDim.x - a.dense_blocks), &flag)) return;
+    const int t = threadIdx.x;
+    const float sv = (t < a.E) ? __hip_atomic_load(a.scores + min(t, a.E - 1), __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : -INFINITY;
+    block_select_values(sv, a.pes, a.E, a.K, L);
+    if (t < a.K) {
+      a.top_w[t] = L.topw[t];
+      a.top_i[t] = L.topi[t];
+    }
   }
 }
 
@@ -400,6 +452,13 @@ struct FfnOutArgs {
   int bf16_running;
   uint16_t* moe_out;        // [H]
   int H;
+  // optional epilogue: the layer tail and the next norm, by the last block
+  TailArgs tail;            // tail.mlp / tail.moe are mlp_out / moe_out
+  const uint16_t* w_next;   // next layer's input_layernorm (or the final norm); null: no epilogue
+  uint16_t* x_out;          // residual after this layer [H]
+  uint16_t* xn_out;         // rms_norm(x_out, w_next) [H]
+  unsigned int* counter;
+  float eps;
 };
 
 template <int FIT>
@@ -438,35 +497,62 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   for (int j = 0; j < ACT_PER; ++j)
     if (tid + 256 * j < ich) act_lds[tid + 256 * j] = av[j];
   __syncthreads();
-  if (!hv) return;
-  float acc = 0.0f;
+  if (hv) {  // wave-uniform
+    float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < DIT; ++i) {
-    const int c = lane + 64 * i;
-    if (c < ich) acc = dot8(wd[i], act_lds[c], acc);
-  }
-  acc = group_sum<64>(acc);
-  if (lane == 0) a.mlp_out[h] = f2bf(acc);
-  if (a.e_down == nullptr) return;
-  float part = 0.0f;
-  if (e >= 0) {
-    const u32x4* av = (const u32x4*)(a.act_moe + (size_t)g * F);
+    for (int i = 0; i < DIT; ++i) {
+      const int c = lane + 64 * i;
+      if (c < ich) acc = dot8(wd[i], act_lds[c], acc);
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) coherent_store_bf16(a.mlp_out + h, f2bf(acc));
+    if (a.e_down != nullptr) {
+      float part = 0.0f;
+      if (e >= 0) {
+        const u32x4* avm = (const u32x4*)(a.act_moe + (size_t)g * F);
 #pragma unroll
-    for (int i = 0; i < FIT; ++i) part = dot8(we[i], ld16(av + l8 + 8 * i), part);
+        for (int i = 0; i < FIT; ++i) part = dot8(we[i], ld16(avm + l8 + 8 * i), part);
+      }
+      part = group_sum<8>(part);
+      float run = 0.0f;
+      for (int q = 0; q < a.K && q < 8; ++q) {
+        const float pq = __shfl(part, 8 * q, kWave);
+        if (a.bf16_running) run = (q == 0) ? rbf(pq) : rbf(run + rbf(pq));
+        else run = (q == 0) ? pq : run + pq;
+      }
+      if (lane == 0) coherent_store_bf16(a.moe_out + h, f2bf(run));
+    }
   }
-  part = group_sum<8>(part);
-  float run = 0.0f;
-  for (int q = 0; q < a.K && q < 8; ++q) {
-    const float pq = __shfl(part, 8 * q, kWave);
-    if (a.bf16_running) run = (q == 0) ? rbf(pq) : rbf(run + rbf(pq));
-    else run = (q == 0) ? pq : run + pq;
+  if (a.w_next == nullptr) return;
+  // The last block to finish applies the layer tail (model.py:317-322) and
+  // the next layer's input norm (model.py:298) once, so the next kernel
+  // starts from the normalised vector instead of three dependent reductions.
+  __shared__ int flag;
+  __shared__ double red[8];
+  if (!arrive_last_grid(a.counter, &flag)) return;
+  const int nch = a.H / 8;
+  TailRegs T;
+  Vec wn, x;
+  vload_coherent(T.a, a.mlp_out, nch);
+  if (a.e_down != nullptr) vload_coherent(T.b, a.moe_out, nch);
+  vload(T.x1, a.tail.x1, nch);
+  vload(T.w3, a.tail.w_pf, nch);
+  if (a.e_down != nullptr) {
+    vload(T.w1, a.tail.w_pf1, nch);
+    vload(T.w2, a.tail.w_pf2, nch);
   }
-  if (lane == 0) a.moe_out[h] = f2bf(run);
+  vload(wn, a.w_next, nch);
+  T.ls = a.tail.ls[0];
+  tail_compute(x, T, a.e_down != nullptr, nch, a.H, a.eps, red);
+  vstore(x, (u32x4*)a.x_out, nch);
+  vscale_w(x, vrms(x, nch, a.H, a.eps, red), wn);
+  vstore(x, (u32x4*)a.xn_out, nch);
 }
 
 // ------------------------------------------------------------------ lm_head
 struct LmArgs {
   TailArgs tail;
+  const uint16_t* xn;       // already normalised input (NORMED variant)
   const uint16_t* w_norm;   // final norm
   const uint16_t* embed;    // [V, H]
   int V;
@@ -483,7 +569,7 @@ __device__ __forceinline__ void better(float& bv, int& bi, float v, int i) {
   if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
 }
 
-template <int IT>
+template <int IT, bool NORMED>
 __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
@@ -498,12 +584,19 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   int r = r0 + wave * 2 + half;
   Vec x, wn0;
   TailRegs T;
-  tail_load(T, a.tail, NCH);
-  vload(wn0, a.w_norm, NCH);
+  if constexpr (NORMED) {
+    vload(x, a.xn, NCH);
+  } else {
+    tail_load(T, a.tail, NCH);
+    vload(wn0, a.w_norm, NCH);
+  }
+  asm volatile("" ::: "memory");
   u32x4 w[IT];
   load_row<32, IT>(a.embed + (size_t)min(r, a.V - 1) * H, l, w);
-  tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
-  vscale_w(x, vrms(x, NCH, H, a.eps, red), wn0);
+  if constexpr (!NORMED) {
+    tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
+    vscale_w(x, vrms(x, NCH, H, a.eps, red), wn0);
+  }
   vstore(x, xs, NCH);
   __syncthreads();
   float bv = -INFINITY;
@@ -627,11 +720,12 @@ int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64
                   const uint16_t* input_ln, uint16_t* x_out, const uint16_t* wq, int64_t q_rows, const uint16_t* wk,
                   int64_t k_rows, const uint16_t* wv, int64_t v_rows, uint16_t* qkv_out, int64_t H, float eps,
                   void* stream) {
-  G4MI_REQUIRE(mode >= 0 && mode <= 2, G4MI_EINVAL, "layer_in: bad mode %d", mode);
+  G4MI_REQUIRE(mode >= 0 && mode <= 3, G4MI_EINVAL, "layer_in: bad mode %d", mode);
   G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
                "layer_in: H=%lld must be 256*i, i <= 16", (long long)H);
-  G4MI_REQUIRE(input_ln && x_out && qkv_out && wq && q_rows >= 1 && k_rows >= 0 && v_rows >= 0, G4MI_EINVAL,
-               "layer_in: missing argument");
+  G4MI_REQUIRE(qkv_out && wq && q_rows >= 1 && k_rows >= 0 && v_rows >= 0, G4MI_EINVAL, "layer_in: missing argument");
+  G4MI_REQUIRE(mode == kInNormed || (input_ln && x_out), G4MI_EINVAL, "layer_in: missing input norm or x_out");
+  G4MI_REQUIRE(mode != kInNormed || x_in, G4MI_EINVAL, "layer_in: normed mode needs x_in");
   G4MI_REQUIRE(mode != 0 || (tok && embed && vocab >= 1), G4MI_EINVAL, "layer_in: embed mode needs tok/embed");
   G4MI_REQUIRE(mode != 1 || (x1 && mlp_out && post_ff_ln && layer_scalar), G4MI_EINVAL,
                "layer_in: tail mode needs x1/mlp_out/post_ff_ln/layer_scalar");
@@ -658,7 +752,8 @@ int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64
   case I:                                                                                           \
     if (mode == kInEmbed) hipLaunchKernelGGL((layer_in_kernel<I, kInEmbed>), grid, dim3(256), 0, st, a); \
     else if (mode == kInTail) hipLaunchKernelGGL((layer_in_kernel<I, kInTail>), grid, dim3(256), 0, st, a); \
-    else hipLaunchKernelGGL((layer_in_kernel<I, kInPlain>), grid, dim3(256), 0, st, a);            \
+    else if (mode == kInPlain) hipLaunchKernelGGL((layer_in_kernel<I, kInPlain>), grid, dim3(256), 0, st, a); \
+    else hipLaunchKernelGGL((layer_in_kernel<I, kInNormed>), grid, dim3(256), 0, st, a);          \
     break;
     G4MI_IT16(G4MI_C)
 #undef G4MI_C
@@ -691,14 +786,20 @@ int g4mi_oproj(const uint16_t* ctx, const uint16_t* w, int64_t rows, int64_t K, 
   return check_launch("oproj");
 }
 
+int64_t g4mi_ffn_in_workspace_bytes(void) { return 256; }
+
 int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_ln, const uint16_t* pre_ff_ln,
                 const uint16_t* pre_ff2_ln, uint16_t* x1_out, uint16_t* xe_out, const uint16_t* gate,
                 const uint16_t* up, int64_t I, uint16_t* act_mlp, const uint16_t* router_scale,
-                const uint16_t* router_proj, int64_t E, float* scores, int64_t H, float eps, void* stream) {
+                const uint16_t* router_proj, int64_t E, float* scores, const uint16_t* per_expert_scale, int64_t k,
+                float* top_w, int32_t* top_i, void* ws, int64_t ws_bytes, int64_t H, float eps, void* stream) {
   G4MI_REQUIRE(x && o && post_attn_ln && pre_ff_ln && x1_out && gate && up && act_mlp && I >= 1, G4MI_EINVAL,
                "ffn_in: missing argument");
   G4MI_REQUIRE(router_proj == nullptr || (router_scale && pre_ff2_ln && xe_out && scores && E >= 1 && E <= 65536),
                G4MI_EINVAL, "ffn_in: router needs scale, pre_ff_2 norm, xe_out and scores");
+  G4MI_REQUIRE(per_expert_scale == nullptr || (router_proj && top_w && top_i && k >= 1 && k <= 32 && k <= E &&
+                                               E <= 256 && ws && ws_bytes >= g4mi_ffn_in_workspace_bytes()),
+               G4MI_EINVAL, "ffn_in: selection needs the router, top_w/top_i, 1 <= k <= 32, E <= 256, workspace");
   G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
                "ffn_in: H=%lld must be 256*i, i <= 16", (long long)H);
   FfnInArgs a;
@@ -709,6 +810,7 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
   a.r_scale = router_scale; a.r_proj = router_proj; a.E = router_proj ? (int)E : 0;
   a.r_c = bf16_round_host(1.0 / sqrt((double)H));
   a.scores = scores; a.H = (int)H; a.eps = eps;
+  a.pes = per_expert_scale; a.K = (int)k; a.top_w = top_w; a.top_i = top_i; a.counter = (unsigned int*)ws;
   const int rblocks = router_proj ? (int)((E + 7) / 8) : 0;
   dim3 grid((unsigned)(a.dense_blocks + rblocks));
   hipStream_t st = as_stream(stream);
@@ -720,10 +822,24 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
   return check_launch("ffn_in");
 }
 
+int64_t g4mi_ffn_out_workspace_bytes(void) {
+  return 4 * kArriveStride * (1 + (1024 + kArriveGroup - 1) / kArriveGroup);  // grid <= 1024 blocks (H <= 4096)
+}
+
 int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint16_t* mlp_out,
                  const uint16_t* act_moe, const uint16_t* experts_down, const int32_t* top_i, int64_t E, int64_t k,
-                 int64_t F, int32_t combine, uint16_t* moe_out, int64_t H, void* stream) {
+                 int64_t F, int32_t combine, uint16_t* moe_out, const uint16_t* x1, const uint16_t* post_ff1_ln,
+                 const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
+                 const uint16_t* next_ln, uint16_t* x_out, uint16_t* xn_out, float eps, void* ws, int64_t ws_bytes,
+                 int64_t H, void* stream) {
   G4MI_REQUIRE(act_mlp && down && mlp_out && H >= 1, G4MI_EINVAL, "ffn_out: missing argument");
+  G4MI_REQUIRE(next_ln == nullptr || (x1 && post_ff_ln && layer_scalar && x_out && xn_out && ws &&
+                                      ws_bytes >= g4mi_ffn_out_workspace_bytes()),
+               G4MI_EINVAL, "ffn_out: the tail epilogue needs x1, post_ff norm, layer_scalar, x_out, xn_out, ws");
+  G4MI_REQUIRE(next_ln == nullptr || experts_down == nullptr || (post_ff1_ln && post_ff2_ln), G4MI_EINVAL,
+               "ffn_out: the tail epilogue with experts needs post_ff_1/post_ff_2 norms");
+  G4MI_REQUIRE(next_ln == nullptr || (H % 8 == 0 && H <= 4096), G4MI_EUNSUPPORTED,
+               "ffn_out: the tail epilogue needs H = 8*i <= 4096");
   G4MI_REQUIRE(I % 8 == 0 && I >= 8 && I <= 4096, G4MI_EUNSUPPORTED, "ffn_out: I=%lld must be 8*i <= 4096",
                (long long)I);
   G4MI_REQUIRE(experts_down == nullptr || (act_moe && top_i && moe_out && k >= 1 && k <= 8 && E >= 1), G4MI_EINVAL,
@@ -736,6 +852,8 @@ int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint1
   a.act_mlp = act_mlp; a.down = down; a.I = (int)I; a.mlp_out = mlp_out;
   a.act_moe = act_moe; a.e_down = experts_down; a.top_i = top_i; a.E = (int)E; a.K = (int)k;
   a.bf16_running = combine == G4MI_COMBINE_BF16_RUNNING; a.moe_out = moe_out; a.H = (int)H;
+  a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
+  a.w_next = next_ln; a.x_out = x_out; a.xn_out = xn_out; a.counter = (unsigned int*)ws; a.eps = eps;
   dim3 grid((unsigned)((H + 3) / 4));
   const size_t lds = (size_t)(I / 8) * 16;
   hipStream_t st = as_stream(stream);
@@ -768,11 +886,30 @@ int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* mo
   dim3 grid((unsigned)g4mi_lm_head_blocks(V));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {
-#define G4MI_C(I) case I: hipLaunchKernelGGL(lmhead_kernel<I>, grid, dim3(256), 0, st, a); break;
+#define G4MI_C(I) case I: hipLaunchKernelGGL((lmhead_kernel<I, false>), grid, dim3(256), 0, st, a); break;
     G4MI_IT16(G4MI_C)
 #undef G4MI_C
   }
   return check_launch("lm_head");
+}
+
+int g4mi_lm_head_normed(const uint16_t* xn, const uint16_t* embed, int64_t V, int64_t H, float softcap,
+                        float* logits, float* blk_val, int32_t* blk_idx, void* stream) {
+  G4MI_REQUIRE(xn && embed && logits && blk_val && blk_idx, G4MI_EINVAL, "lm_head_normed: missing argument");
+  G4MI_REQUIRE(V >= 1 && V <= (int64_t)1 << 30, G4MI_EINVAL, "lm_head_normed: bad vocab");
+  G4MI_REQUIRE(H % 256 == 0 && H / 256 >= 1 && H / 256 <= 16, G4MI_EUNSUPPORTED,
+               "lm_head_normed: H=%lld must be 256*i, i <= 16", (long long)H);
+  LmArgs a = {};
+  a.xn = xn; a.embed = embed; a.V = (int)V; a.softcap = softcap; a.logits = logits;
+  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = 256; a.H = (int)H;
+  dim3 grid((unsigned)g4mi_lm_head_blocks(V));
+  hipStream_t st = as_stream(stream);
+  switch (H / 256) {
+#define G4MI_C(I) case I: hipLaunchKernelGGL((lmhead_kernel<I, true>), grid, dim3(256), 0, st, a); break;
+    G4MI_IT16(G4MI_C)
+#undef G4MI_C
+  }
+  return check_launch("lm_head_normed");
 }
 
 int g4mi_argmax_finalize(const float* blk_val, const int32_t* blk_idx, int64_t n, int32_t* tok, int32_t* pos,

@@ -24,8 +24,8 @@ __global__ __launch_bounds__(256) void fill_normal_bf16_kernel(uint16_t* __restr
     const double rad = sqrt(-2.0 * log(u1));
     const double ang = 6.283185307179586476925286766559 * u2;
     const double z0 = rad * cos(ang), z1 = rad * sin(ang);
-    const uint16_t b0 = f2bf((float)(stdv * z0));
-    const uint16_t b1 = f2bf((float)(stdv * z1));
+    const uint16_t b0 = f2bf(f32_of(stdv * z0));
+    const uint16_t b1 = f2bf(f32_of(stdv * z1));
     const int64_t i = 2 * j;
     if (i + 1 < n) {
       // i is even: the pair is 4-byte aligned when `out` is.

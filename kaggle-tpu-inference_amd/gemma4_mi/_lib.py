@@ -56,11 +56,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _p],
     ),
     "g4mi_oproj": (_int, [_p, _p, _i64, _i64, _p, _p]),
+    "g4mi_ffn_in_workspace_bytes": (_i64, []),
     "g4mi_ffn_in": (
         _int,
-        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _i64, _f32, _p],
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _i64, _p, _p, _i64, _p, _p, _p, _i64, _i64, _f32, _p],
     ),
-    "g4mi_ffn_out": (_int, [_p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _i64, _p]),
+    "g4mi_ffn_out_workspace_bytes": (_i64, []),
+    "g4mi_ffn_out": (
+        _int,
+        [_p, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _p, _f32, _p, _i64,
+         _i64, _p],
+    ),
+    "g4mi_lm_head_normed": (_int, [_p, _p, _i64, _i64, _f32, _p, _p, _p, _p]),
     "g4mi_lm_head_blocks": (_i64, [_i64]),
     "g4mi_lm_head": (
         _int,

@@ -154,11 +154,12 @@ def decode_masks(cfg: TextConfig, max_len: int, pos) -> dict:
 class DecodeRunner:
     """Launches one batch-1 token step of the model on the current stream.
 
-    Per layer: layer_in (tail of the previous layer + input norm + q/k/v),
-    decode attention (append + scores + pv + reduce), o_proj, ffn_in
-    (post-attention norm + dense gate/up + router scores), routed expert
-    gate/up, ffn_out (dense and expert down + combine); then lm_head and the
-    greedy argmax.  All buffers are allocated once, so a step can be captured
+    Per layer: layer_in (q/k/v of the normalised input; the first layer
+    embeds the token), decode attention (append + scores, then PV + the
+    ordered split reduce), o_proj, ffn_in (post-attention norm, dense
+    gate/up, router scores and the expert selection), routed expert gate/up,
+    ffn_out (dense and expert down + combine, then the layer tail and the
+    next layer's input norm once); then lm_head and the greedy argmax.  All buffers are allocated once, so a step can be captured
     in a HIP graph and replayed; the token and position live in device
     memory (`tok`, `pos`)."""
 
@@ -179,7 +180,7 @@ class DecodeRunner:
                       for lt in cfg.layer_types)
         ctx_max = max(cfg.num_attention_heads * cfg.head_dim_for(lt) for lt in cfg.layer_types)
         z = lambda n, dt=bf: torch.zeros(n, dtype=dt, device=dev)  # noqa: E731
-        self.x, self.x1, self.xe, self.o = z(H), z(H), z(H), z(H)
+        self.x, self.x1, self.xe, self.o, self.xn = z(H), z(H), z(H), z(H), z(H)
         self.mlp_out, self.moe_out = z(H), z(H)
         self.qkv, self.ctx = z(qkv_max), z(ctx_max)
         self.act_mlp = z(cfg.intermediate_size)
@@ -212,6 +213,9 @@ class DecodeRunner:
             ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, cfg.num_attention_heads, d, lmax, ns))
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.sample_ws = torch.zeros(ops.sample_workspace_bytes(cfg.vocab_size), dtype=torch.uint8, device=dev)
+        self.ffn_ws = torch.zeros(int(ops._lib.lib().g4mi_ffn_in_workspace_bytes()), dtype=torch.uint8, device=dev)
+        self.ffn_out_ws = torch.zeros(int(ops._lib.lib().g4mi_ffn_out_workspace_bytes()), dtype=torch.uint8,
+                                      device=dev)
 
     def _splits(self, lt: str) -> int:
         cfg = self.cfg
@@ -241,14 +245,9 @@ class DecodeRunner:
             if i == 0:
                 ops.layer_in(0, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
                              q_rows, k_rows, v_rows, self.qkv, tok=self.tok, embed=p["embed"])
-            else:
-                prev = self.layers[i - 1]
-                ops.layer_in(1, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
-                             q_rows, k_rows, v_rows, self.qkv, x1=self.x1, mlp_out=self.mlp_out,
-                             moe_out=self.moe_out if moe else None,
-                             post_ff1=prev.get("post_feedforward_layernorm_1"),
-                             post_ff2=prev.get("post_feedforward_layernorm_2"),
-                             post_ff=prev["post_feedforward_layernorm"], layer_scalar=prev["layer_scalar"])
+            else:  # the previous ffn_out already applied the tail and this layer's input norm
+                ops.layer_in(3, H, eps, None, None, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
+                             q_rows, k_rows, v_rows, self.qkv, x_in=self.xn)
             q = self.qkv[:q_rows].view(1, NH, d)
             k = self.qkv[q_rows:q_rows + k_rows].view(1, kv, d)
             v = self.qkv[q_rows + k_rows:q_rows + k_rows + v_rows].view(1, kv, d) if v_rows else None
@@ -262,23 +261,24 @@ class DecodeRunner:
             ops.ffn_in(self.x, self.o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
                        lp.get("pre_feedforward_layernorm_2"), self.x1, self.xe, lp["mlp.gate_proj"],
                        lp["mlp.up_proj"], self.act_mlp, lp.get("router.scale"), lp.get("router.proj"),
-                       self.scores if moe else None, H, eps)
+                       self.scores if moe else None, H, eps,
+                       per_expert_scale=lp["router.per_expert_scale"] if moe else None, k=cfg.top_k_experts,
+                       route=(self.top_w[i], self.top_i[i]) if moe else None, ws=self.ffn_ws)
             if moe:
-                ops.moe_gateup_routed(self.xe.view(1, H), self.scores.view(1, -1), lp["router.per_expert_scale"],
-                                      lp["experts.gate_up_proj"], cfg.top_k_experts,
-                                      act=self.act_moe.view(1, cfg.top_k_experts, -1),
-                                      route=(self.top_w[i:i + 1], self.top_i[i:i + 1]))
+                ops.moe_gateup(self.xe.view(1, H), lp["experts.gate_up_proj"], self.top_w[i:i + 1],
+                               self.top_i[i:i + 1], act=self.act_moe.view(1, cfg.top_k_experts, -1))
+            nxt = self.layers[i + 1]["input_layernorm"] if i + 1 < cfg.num_hidden_layers else p["norm"]
+            tail = {"x1": self.x1, "post_ff1": lp.get("post_feedforward_layernorm_1"),
+                    "post_ff2": lp.get("post_feedforward_layernorm_2"), "post_ff": lp["post_feedforward_layernorm"],
+                    "layer_scalar": lp["layer_scalar"], "next_ln": nxt, "x_out": self.x, "xn_out": self.xn}
             ops.ffn_out(self.act_mlp, lp["mlp.down_proj"], self.mlp_out, self.act_moe if moe else None,
                         lp.get("experts.down_proj"), self.top_i[i] if moe else None, cfg.top_k_experts, combine,
-                        self.moe_out if moe else None, H)
+                        self.moe_out if moe else None, H, tail=tail, eps=eps, ws=self.ffn_out_ws)
         if feed is not None:
             ops.advance_feed(feed, self.tok, self.pos, self.hist)
             return
-        last = self.layers[-1]
-        ops.lm_head(self.x1, self.mlp_out, self.moe_out if moe else None, last.get("post_feedforward_layernorm_1"),
-                    last.get("post_feedforward_layernorm_2"), last["post_feedforward_layernorm"],
-                    last["layer_scalar"], p["norm"], p["embed"], cfg.final_logit_softcapping, eps, self.logits,
-                    self.blk_val, self.blk_idx)
+        ops.lm_head_normed(self.xn, p["embed"], cfg.final_logit_softcapping, self.logits, self.blk_val,
+                           self.blk_idx)
         if sampler is not None:
             params, top_k, counter_mode = sampler
             ops.sample(self.logits, top_k, params, self.tok, counter_mode, self.pos if advance else None,

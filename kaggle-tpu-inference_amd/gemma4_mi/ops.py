@@ -336,12 +336,13 @@ def layer_in(mode, H, eps, input_ln, x_out, wq, wk, wv, q_rows, k_rows, v_rows, 
              x_in=None, x1=None, mlp_out=None, moe_out=None, post_ff1=None, post_ff2=None, post_ff=None,
              layer_scalar=None):
     """q/k/v projection of rms_norm(x, input_ln) with x from the embedding
-    (mode 0), the previous layer's tail (mode 1) or x_in (mode 2)."""
+    (mode 0), the previous layer's tail (mode 1) or x_in (mode 2); mode 3
+    takes x_in as the already-normalised input."""
     vocab = embed.shape[0] if embed is not None else 0
     _lib.call("g4mi_layer_in", int(mode), _ptr(tok), _ptr(embed), vocab, _ptr(x_in), _ptr(x1), _ptr(mlp_out),
               _ptr(moe_out), _ptr(post_ff1), _ptr(post_ff2), _ptr(post_ff), _ptr(layer_scalar), _ptr(input_ln),
               _ptr(x_out), _ptr(wq), q_rows, _ptr(wk), k_rows, _ptr(wv), v_rows, _ptr(qkv_out), H, float(eps),
-              stream_handle(x_out.device))
+              stream_handle(qkv_out.device))
 
 
 def oproj(ctx, w, rows, K, out):
@@ -349,21 +350,45 @@ def oproj(ctx, w, rows, K, out):
 
 
 def ffn_in(x, o, post_attn_ln, pre_ff_ln, pre_ff2_ln, x1_out, xe_out, gate, up, act_mlp, router_scale, router_proj,
-           scores, H, eps):
+           scores, H, eps, per_expert_scale=None, k=0, route=None, ws=None):
+    """Post-attention residual, pre-FFN norms, dense gate/up and router scores
+    (model.py:218-227, 301-315); with per_expert_scale and route = (top_w [k],
+    top_i [k]) also the expert selection (model.py:228-231)."""
     I = gate.shape[0]
     E = router_proj.shape[0] if router_proj is not None else 0
+    top_w, top_i = route if route is not None else (None, None)
+    if per_expert_scale is not None and ws is None:
+        ws = WORKSPACE.get(x.device, "ffn_in", int(_lib.lib().g4mi_ffn_in_workspace_bytes()))
     _lib.call("g4mi_ffn_in", _ptr(x), _ptr(o), _ptr(post_attn_ln), _ptr(pre_ff_ln), _ptr(pre_ff2_ln), _ptr(x1_out),
               _ptr(xe_out), _ptr(gate), _ptr(up), I, _ptr(act_mlp), _ptr(router_scale), _ptr(router_proj), E,
-              _ptr(scores), H, float(eps), stream_handle(x.device))
+              _ptr(scores), _ptr(per_expert_scale), int(k), _ptr(top_w), _ptr(top_i), _ptr(ws),
+              0 if ws is None else ws.numel(), H, float(eps), stream_handle(x.device))
 
 
-def ffn_out(act_mlp, down, mlp_out, act_moe, experts_down, top_i, k, combine, moe_out, H):
+def ffn_out(act_mlp, down, mlp_out, act_moe, experts_down, top_i, k, combine, moe_out, H, tail=None, eps=1e-6,
+            ws=None):
+    """Dense and expert down projections + combine (model.py:221, 272-294).
+    With tail = dict(x1, post_ff1, post_ff2, post_ff, layer_scalar, next_ln,
+    x_out, xn_out) the last block also applies the layer tail and the next
+    norm (model.py:312-322, 298)."""
     I = down.shape[1]
     E = experts_down.shape[0] if experts_down is not None else 0
     F = experts_down.shape[2] if experts_down is not None else 0
     mode = {"bf16_running": _lib.COMBINE_BF16_RUNNING, "f32": _lib.COMBINE_F32}[combine]
+    t = tail or {}
+    if tail is not None and ws is None:
+        ws = WORKSPACE.get(mlp_out.device, "ffn_out", int(_lib.lib().g4mi_ffn_out_workspace_bytes()))
     _lib.call("g4mi_ffn_out", _ptr(act_mlp), _ptr(down), I, _ptr(mlp_out), _ptr(act_moe), _ptr(experts_down),
-              _ptr(top_i), E, k, F, mode, _ptr(moe_out), H, stream_handle(mlp_out.device))
+              _ptr(top_i), E, k, F, mode, _ptr(moe_out), _ptr(t.get("x1")), _ptr(t.get("post_ff1")),
+              _ptr(t.get("post_ff2")), _ptr(t.get("post_ff")), _ptr(t.get("layer_scalar")), _ptr(t.get("next_ln")),
+              _ptr(t.get("x_out")), _ptr(t.get("xn_out")), float(eps), _ptr(ws), 0 if ws is None else ws.numel(), H,
+              stream_handle(mlp_out.device))
+
+
+def lm_head_normed(xn, embed, softcap, logits, blk_val, blk_idx):
+    V, H = embed.shape
+    _lib.call("g4mi_lm_head_normed", _ptr(xn), _ptr(embed), V, H, float(softcap or 0.0), _ptr(logits),
+              _ptr(blk_val), _ptr(blk_idx), stream_handle(embed.device))
 
 
 def lm_head_blocks(V: int) -> int:
