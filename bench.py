@@ -251,64 +251,58 @@ def run_copy(args) -> dict:
 
 # ------------------------------------------------------------------ full-model decode
 def _e2e_decode(args) -> dict:
-    """Batch-1 greedy decode of the 26B-A4B-shaped model with a 32K cache."""
+    """Batch-1 greedy decode of the 26B-A4B-shaped model with a 32K cache,
+    through the Engine API (engine.py's compile_all / prefill_fn / decode_fn)."""
     import numpy as np
     import torch
 
-    from gemma4_mi import model as gm
-    from gemma4_mi import ops
     from gemma4_mi.config import gemma4_26b_a4b_config
-    from gemma4_mi.weights import decode_bytes, init_random_params, param_bytes
+    from gemma4_mi.engine import PREFILL_BUCKET, Engine
+    from gemma4_mi.weights import decode_bytes, param_bytes
 
     cfg = gemma4_26b_a4b_config()
     seed, prompt_len = 3, args.prompt_len
     t0 = time.perf_counter()
-    params = init_random_params(cfg, seed, device="cuda:0")
-    torch.cuda.synchronize()
-    _log(f"weights: {param_bytes(cfg) / 2**30:.1f} GiB generated in {time.perf_counter() - t0:.1f}s")
-    cache = gm.init_cache(cfg, None, 1, args.max_len, device="cuda:0")
-    r = gm.DecodeRunner(cfg, params, cache, device="cuda:0")
+    eng = Engine.random(cfg, seed=seed, max_len=args.max_len)
+    _log(f"weights: {param_bytes(cfg) / 2**30:.1f} GiB generated, engine ready in {time.perf_counter() - t0:.1f}s")
+    comp = eng.compile_all(PREFILL_BUCKET)
+    _log("step graphs captured: " + ", ".join(f"{k}={v:.3f}" for k, v in comp.items()))
     prompt = np.random.default_rng(seed).integers(0, cfg.vocab_size, size=prompt_len).tolist()
+    bucket = max(PREFILL_BUCKET, ((prompt_len + PREFILL_BUCKET - 1) // PREFILL_BUCKET) * PREFILL_BUCKET)
 
-    g_pre = _capture_step(r, "f32")
-    g_dec = _capture_step(r, "bf16_running")
-    _log("decode step captured (%d kernels per token)" % (8 * cfg.num_hidden_layers + 2))
-
-    # prefill (TTFT): one dense-MoE step per prompt token, first token on the host
+    # TTFT: the prompt through the prefill graphs (dense-MoE combine), first token to the host
+    toks_in = torch.tensor(prompt, dtype=torch.int32)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for t, tok in enumerate(prompt):
-        r.set_state(tok, t)
-        g_pre.replay()
-    first = int(r.tok.item())
+    tok, cache, pos = eng.prefill_fn(bucket)(eng.params, toks_in, eng.cache, prompt_len, seed, 0.0, 1.0)
+    first = int(tok.item())
     ttft = time.perf_counter() - t0
-    # decode: W warm-up steps, then exactly K timed steps
+    dec = eng.decode_fn()
     for _ in range(args.warmup):
-        g_dec.replay()
+        tok, cache, pos = dec(eng.params, tok, cache, pos, seed, 0.0, 1.0)
     torch.cuda.synchronize()
-    p0 = int(r.pos.item())
+    p0 = int(pos)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(args.steps):
-        g_dec.replay()
+        tok, cache, pos = dec(eng.params, tok, cache, pos, seed, 0.0, 1.0)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / args.steps
-    p1 = int(r.pos.item())
-    toks = r.hist[prompt_len: p1 + 1].cpu().tolist()
+    p1 = int(pos)
+    toks = eng._runner.hist[prompt_len: p1 + 1].cpu().tolist()
     bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
-    return {"cfg": cfg, "params": params, "cache": cache, "runner": r, "ms": ms, "ttft": ttft, "first": first,
-            "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt}
-
-
-def _capture_step(r, combine):
-    return _capture(lambda: r.launch(combine, advance=True))
+    return {"cfg": cfg, "params": eng.params, "cache": eng.cache, "engine": eng, "ms": ms, "ttft": ttft,
+            "first": first, "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt}
 
 
 def _gateup_timing(cfg, params, n: int, steps: int) -> tuple[float, float]:
-    """Average duration (us) of the routed expert gate/up kernel over `n`
+    """Average duration (us) of the decode path's expert gate/up kernel
+    (moe_gateup_kernel with the routing that ffn_in selected) over `n`
     launches per graph cycling through the layers (different experts each
-    launch), and its algorithmic bytes per launch."""
+    launch, so the 1.5 GB expert tables defeat the MALL), and its algorithmic
+    bytes per launch: the 8 experts' gate and up rows, the hidden state, the
+    routing and the activations written."""
     import torch
 
     from gemma4_mi import ops
@@ -318,20 +312,18 @@ def _gateup_timing(cfg, params, n: int, steps: int) -> tuple[float, float]:
     L = cfg.num_hidden_layers
     xe = torch.empty((n, 1, H), dtype=torch.bfloat16, device="cuda:0")
     ops.fill_normal_(xe, tensor_key(7, "bench.xe"), 1.0)
-    scores = torch.empty((n, 1, E), dtype=torch.float32, device="cuda:0")
     act = torch.empty((n, 1, K, F), dtype=torch.bfloat16, device="cuda:0")
-    tw = torch.empty((n, 1, K), dtype=torch.float32, device="cuda:0")
-    ti = torch.empty((n, 1, K), dtype=torch.int32, device="cuda:0")
+    route = []
     lp = lambda i, k: params[f"layers.{i % L}.{k}"]  # noqa: E731
     for i in range(n):
-        ops.moe_router_scores(xe[i], lp(i, "router.scale"), lp(i, "router.proj"), cfg.rms_norm_eps, out=scores[i])
-    g = _capture(lambda: [ops.moe_gateup_routed(xe[i], scores[i], lp(i, "router.per_expert_scale"),
-                                                lp(i, "experts.gate_up_proj"), K, act=act[i], route=(tw[i], ti[i]))
+        route.append(ops.moe_router_topk(xe[i], lp(i, "router.scale"), lp(i, "router.proj"),
+                                         lp(i, "router.per_expert_scale"), K, cfg.rms_norm_eps))
+    g = _capture(lambda: [ops.moe_gateup(xe[i], lp(i, "experts.gate_up_proj"), route[i][0], route[i][1], act=act[i])
                           for i in range(n)])
     _time_graph(g, 2)
     reps = max(1, steps // n)
     us = _time_graph(g, reps) / (reps * n) * 1e3
-    nbytes = K * 2 * F * H * 2 + H * 2 + E * 4 + K * F * 2
+    nbytes = K * 2 * F * H * 2 + H * 2 + K * 8 + K * F * 2
     return us, nbytes
 
 
@@ -385,6 +377,19 @@ def _cpu_decode_baseline(res, budget_s: float, max_steps: int) -> dict:
     }
 
 
+def _measured_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
+    summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated), or None."""
+    path = os.path.join(ROOT, "profiles", "moe_gateup_26b_a4b_traffic.txt")
+    try:
+        kv = dict(line.split(":", 1) for line in open(path) if ":" in line and not line.startswith("#"))
+    except OSError:
+        return None
+    if kv.get("kernel", "").strip() != kernel:
+        return None
+    return float(kv["traffic_bytes_per_launch"])
+
+
 def run_decode(args) -> dict:
     import numpy as np
 
@@ -409,14 +414,15 @@ def run_decode(args) -> dict:
             "ttft_s": res["ttft"], "itl_ms": ms,
             "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
             "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS,
-            "kernels_per_token": 8 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token",
-            "prefill": "token-by-token decode kernels with the dense-MoE combine",
+            "kernels_per_token": 7 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token (Engine.decode_fn)",
+            "prefill": "Engine.prefill_fn: token-by-token decode kernels with the dense-MoE combine",
             "first_tokens": res["tokens"][:8],
         },
         "roofline": {
-            "kernel": "moe_gateup_kernel (routed, 8 experts x 1408 rows x 2816)", "bound": "hbm",
+            "kernel": "moe_gateup_kernel (8 selected experts x 1408 gate/up rows x 2816)", "bound": "hbm",
             "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None, "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
+            "traffic": _measured_traffic("moe_gateup_kernel"), "bytes_per_launch": gu_bytes, "avg_launch_us": gu_us,
+            "traffic_source": "profiles/moe_gateup_26b_a4b_traffic.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
         },
     }
     if not args.no_cpu_baseline:
@@ -424,7 +430,27 @@ def run_decode(args) -> dict:
     return out
 
 
-WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy}
+def run_gateup(args) -> dict:
+    """The decode path's expert gate/up kernel alone on the 26B-A4B expert
+    tables (the roofline kernel of the decode workload; short, for rocprofv3
+    counter runs)."""
+    from gemma4_mi.config import gemma4_26b_a4b_config
+    from gemma4_mi.weights import init_random_params
+
+    cfg = gemma4_26b_a4b_config()
+    params = init_random_params(cfg, 3, device="cuda:0")
+    us, nbytes = _gateup_timing(cfg, params, 60, args.steps)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {
+        "metric": "expert gate/up kernel GB/s (algorithmic bytes)", "value": gbs, "unit": "GB/s",
+        "ms_per_step": us * 1e-3, "dtype": "bf16",
+        "config": {"workload": "moe_gateup_26b_a4b", "launches_per_graph": 60, "bytes_per_launch": nbytes},
+        "roofline": {"kernel": "moe_gateup_kernel", "bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
+WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup}
 
 
 def main() -> int:
