@@ -257,6 +257,36 @@ int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* param
                 int32_t* tok, int32_t* pos, int32_t* hist, int64_t hist_len, void* ws, int64_t ws_bytes,
                 void* stream);
 
+/* ---------------------------------------------------------------- prefill (K8, K9)
+ * bf16 GEMM on MFMA: C[m, n] = sum_k A[a_rows ? a_rows[m] : m, k] * B[n, k],
+ * A [*, K] (row stride lda), B [N, K] (row stride ldb), f32 accumulation.
+ * epilogue 0: C bf16 [M, N] (ldc); 1: C f32; 2 (gated): N gate rows from B
+ * and the up rows at B + pair_offset, C[m, n] = bf16(bf16(bf16(gelu(bf16(g)))
+ * * bf16(u)) * bf16(row_scale[m])) (model.py:220, 246-247; row_scale may be
+ * NULL).  With tiles (device int32 triples (group, m0, m1), count *ntiles <=
+ * max_tiles, m1 - m0 <= 64) each tile uses B + group * b_group_stride: the
+ * grouped per-expert GEMM.  k_slices > 1 splits K over blocks (plain
+ * epilogues 0/1 only) with a workspace of g4mi_gemm_workspace_bytes.
+ * K % 32 == 0; rows 16-byte aligned.  No reference counterpart: XLA's dot. */
+int64_t g4mi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t k_slices);
+int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                   int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                   const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
+                   int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes,
+                   void* stream);
+
+/* The dense-MoE prefill of model.py:241-250 for n tokens: xn [n, H] (the
+ * pre_feedforward_layernorm_2 output), routing top_w [n, K] f32 / top_i
+ * [n, K] int32, gate_up [E, 2, F, H], down [E, H, F] -> out [n, H] bf16 = bf16
+ * of one f32 sum over the selected experts.  Unselected experts contribute
+ * exact zeros in the reference (masked weights), so only the selected
+ * (token, expert) pairs are computed, as grouped MFMA GEMMs.  n <= 65535,
+ * E <= 256, K <= 32, H and F multiples of 32. */
+int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_t F, int64_t H);
+int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
+                     const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
+                     void* ws, int64_t ws_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

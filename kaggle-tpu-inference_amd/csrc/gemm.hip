@@ -1,0 +1,312 @@
+// Prefill GEMMs on MFMA (gfx950 v_mfma_f32_16x16x32_bf16).
+//
+// C[m, n] = sum_k A[m, k] * B[n, k]: activations A [M, K] and weights B [N, K]
+// are both row-major with K contiguous, as every projection of the model is
+// stored (model.py:84-117), so both operands stream 16-byte rows.  bf16 in,
+// f32 accumulate.  One block computes a BM x BN tile with 4 waves (2 x 2);
+// a wave holds (BM/2) x (BN/2) of f32 accumulators as 16 x 16 MFMA tiles.
+// K advances 32 at a time through double-buffered LDS tiles: the next step's
+// global loads are in flight while the current step multiplies.
+//
+// MFMA operand layout (16x16x32 bf16): lane l holds A[l%16][8(l/16)..+7] and
+// B[l%16][8(l/16)..+7] (both rows of their K-contiguous tiles) and receives
+// C[4(l/16)+i][l%16], i < 4.
+//
+// Options, used by the batched prefill:
+//  * a_rows: A row of output row m is a_rows[m] (token gather for the MoE);
+//  * grouped tiles: a device list of (group, m0, m1) M-tiles, each using the
+//    group's B (b + group * b_group_stride) -- one expert per tile;
+//  * split-K: blockIdx.z takes K slice z and writes f32 partials, summed in
+//    slice order by gemm_reduce_kernel (deterministic);
+//  * epilogues: bf16 store, f32 store, or the gated activation of a (gate, up)
+//    pair: the tile's first BN/2 B rows come from b, the last BN/2 from
+//    b + pair_offset at the same row index, and output column n0/2 + j gets
+//    bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w_row)) (model.py:220,
+//    model.py:246-247 and 269-271 with the routing weight w_row of the row).
+#include <stdlib.h>
+
+#include "capi_util.h"
+#include "common.h"
+
+namespace g4mi {
+
+enum { kEpBf16 = 0, kEpF32 = 1, kEpGated = 2 };
+
+struct GemmTile {
+  int32_t group, m0, m1;
+};
+
+struct GemmArgs {
+  const uint16_t* a;
+  int64_t lda;
+  const int32_t* a_rows;    // null: identity
+  const uint16_t* b;
+  int64_t ldb;
+  int64_t b_group_stride;   // elements between groups (grouped tiles)
+  int64_t pair_offset;      // gated: element offset of the up rows
+  int M, N, K;              // N: output columns (gated: gate rows)
+  const GemmTile* tiles;    // null: plain M tiling
+  const int32_t* ntiles;    // device count of `tiles`
+  void* c;
+  int64_t ldc;
+  const float* row_scale;   // gated: per output row weight (null: 1)
+  int k_slices;             // split-K slices (f32 partials when > 1)
+  float* partial;           // [k_slices, M, N] f32
+};
+
+constexpr int kBK = 32;
+constexpr int kPad = 8;  // LDS row padding (elements): rows of 80 bytes
+
+template <int BM, int BN, int EP>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
+  constexpr int FM = WM / 16, FN = WN / 16; // MFMA fragments per wave
+  constexpr int LDT = kBK + kPad;
+  constexpr int ACH = BM * kBK / 8 / 256;   // 16-byte A chunks per thread per step
+  constexpr int BCH = BN * kBK / 8 / 256;
+  static_assert(ACH >= 1 && BCH >= 1, "tile too small for 256 threads");
+  // one LDS block: the double-buffered A and B tiles, reused by the gated
+  // epilogue's exchange
+  __shared__ __align__(16) uint16_t smem[2 * BM * LDT + 2 * BN * LDT];
+  // A tile of buffer `buf` at smem + buf*BM*LDT, B tile at smem + 2*BM*LDT + buf*BN*LDT
+  constexpr int SB0 = 2 * BM * LDT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // ---- this block's tile
+  int group = 0, m0, m1;
+  if (g.tiles != nullptr) {
+    if ((int)blockIdx.x >= g.ntiles[0]) return;
+    const GemmTile t = g.tiles[blockIdx.x];
+    group = t.group;
+    m0 = t.m0;
+    m1 = t.m1;
+  } else {
+    m0 = blockIdx.x * BM;
+    m1 = min(g.M, m0 + BM);
+  }
+  const int n0 = blockIdx.y * (EP == kEpGated ? BN / 2 : BN);  // first output column
+  const uint16_t* bbase = g.b + (size_t)group * g.b_group_stride;
+  const int kslices = g.k_slices;
+  const int ksteps_all = g.K / kBK;
+  const int ks0 = (ksteps_all * (int)blockIdx.z) / kslices;
+  const int ks1 = (ksteps_all * ((int)blockIdx.z + 1)) / kslices;
+
+  // ---- global source rows of the chunks this thread copies (fixed over K)
+  const u32x4* asrc[ACH];
+  const u32x4* bsrc[BCH];
+  int adst[ACH], bdst[BCH];
+#pragma unroll
+  for (int q = 0; q < ACH; ++q) {
+    const int c = tid + 256 * q;  // chunk: row c/4, 8 elements at (c%4)*8
+    const int r = c >> 2, kc = (c & 3) * 8;
+    const int m = min(m0 + r, max(m1 - 1, m0));
+    const int src = (g.a_rows != nullptr) ? g.a_rows[m] : m;
+    asrc[q] = (const u32x4*)(g.a + (size_t)src * g.lda + kc);
+    adst[q] = r * LDT + kc;
+  }
+#pragma unroll
+  for (int q = 0; q < BCH; ++q) {
+    const int c = tid + 256 * q;
+    const int r = c >> 2, kc = (c & 3) * 8;
+    const uint16_t* row;
+    if constexpr (EP == kEpGated) {
+      const int half = r >= BN / 2;
+      const int n = min(n0 + (r - half * (BN / 2)), g.N - 1);
+      row = bbase + (half ? g.pair_offset : 0) + (size_t)n * g.ldb;
+    } else {
+      const int n = min(n0 + r, g.N - 1);
+      row = bbase + (size_t)n * g.ldb;
+    }
+    bsrc[q] = (const u32x4*)(row + kc);
+    bdst[q] = r * LDT + kc;
+  }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  u32x4 ra[ACH], rb[BCH];
+  auto gload = [&](int ks) {
+#pragma unroll
+    for (int q = 0; q < ACH; ++q) ra[q] = ld16(asrc[q] + ks * (kBK / 8));
+#pragma unroll
+    for (int q = 0; q < BCH; ++q) rb[q] = ld_stream(bsrc[q] + ks * (kBK / 8));
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int q = 0; q < ACH; ++q) *(u32x4*)(smem + buf * BM * LDT + adst[q]) = ra[q];
+#pragma unroll
+    for (int q = 0; q < BCH; ++q) *(u32x4*)(smem + SB0 + buf * BN * LDT + bdst[q]) = rb[q];
+  };
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  if (ks0 < ks1) {
+    gload(ks0);
+    lstore(0);
+    __syncthreads();
+    int buf = 0;
+    for (int ks = ks0; ks < ks1; ++ks) {
+      const bool more = ks + 1 < ks1;
+      if (more) gload(ks + 1);
+      u32x4 af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = *(const u32x4*)(smem + buf * BM * LDT + (wm * WM + i * 16 + fr) * LDT + fk);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bf[j] = *(const u32x4*)(smem + SB0 + buf * BN * LDT + (wn * WN + j * 16 + fr) * LDT + fk);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
+                                                              __builtin_bit_cast(bf16x8, bf[j]), acc[i][j], 0, 0,
+                                                              0);
+      if (more) {
+        lstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
+      }
+    }
+  }
+
+  // ---- epilogue.  Fragment (i, j), register q: row wm*WM + 16i + 4(l/16) + q,
+  // column wn*WN + 16j + (l%16) of the tile.
+  const int er = 4 * (lane >> 4), ec = lane & 15;
+  if (kslices > 1) {
+    float* p = g.partial + (size_t)blockIdx.z * g.M * g.N;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = m0 + wm * WM + 16 * i + er + q, n = n0 + wn * WN + 16 * j + ec;
+          if (m < m1 && n < g.N) p[(size_t)m * g.N + n] = acc[i][j][q];
+        }
+    return;
+  }
+  if constexpr (EP == kEpGated) {
+    // up (wn = 1) to LDS, then the gate waves combine
+    __syncthreads();
+    float* su = (float*)smem;  // BM x WN f32
+    static_assert((size_t)BM * (BN / 2) * 4 <= sizeof(smem), "exchange buffer too small");
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) su[(wm * WM + 16 * i + er + q) * WN + 16 * j + ec] = acc[i][j][q];
+    }
+    __syncthreads();
+    if (wn == 0) {
+      uint16_t* c = (uint16_t*)g.c;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int r = wm * WM + 16 * i + er + q, col = 16 * j + ec;
+            const int m = m0 + r, n = n0 + col;
+            if (m < m1 && n < g.N) {
+              const float gt = rbf(acc[i][j][q]), up = rbf(su[r * WN + col]);
+              float a = rbf(rbf(gelu_tanh(gt)) * up);
+              if (g.row_scale != nullptr) a = rbf(a * rbf(g.row_scale[m]));
+              c[(size_t)m * g.ldc + n] = f2bf(a);
+            }
+          }
+    }
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = m0 + wm * WM + 16 * i + er + q, n = n0 + wn * WN + 16 * j + ec;
+        if (m < m1 && n < g.N) {
+          if constexpr (EP == kEpF32) ((float*)g.c)[(size_t)m * g.ldc + n] = acc[i][j][q];
+          else ((uint16_t*)g.c)[(size_t)m * g.ldc + n] = f2bf(acc[i][j][q]);
+        }
+      }
+}
+
+// C = sum over the k_slices f32 partials, in slice order.
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ partial, int slices, int64_t mn,
+                                                          int N, void* c, int64_t ldc, int f32_out) {
+  const int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= mn) return;
+  float s = 0.0f;
+  for (int z = 0; z < slices; ++z) s += partial[(size_t)z * mn + e];
+  const int64_t m = e / N, n = e - m * N;
+  if (f32_out) ((float*)c)[m * ldc + n] = s;
+  else ((uint16_t*)c)[m * ldc + n] = f2bf(s);
+}
+
+template <int BM, int BN, int EP>
+static void launch(const GemmArgs& g, int mtiles, hipStream_t st) {
+  const int ncols = (EP == kEpGated) ? BN / 2 : BN;
+  dim3 grid((unsigned)mtiles, (unsigned)((g.N + ncols - 1) / ncols), (unsigned)g.k_slices);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, EP>), grid, dim3(256), 0, st, g);
+}
+
+}  // namespace g4mi
+
+using namespace g4mi;
+
+extern "C" {
+
+int64_t g4mi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t k_slices) {
+  return k_slices > 1 ? k_slices * M * N * 4 : 0;
+}
+
+int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                   int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                   const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
+                   int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes,
+                   void* stream) {
+  G4MI_REQUIRE(a && b && c && M >= 1 && N >= 1 && K >= 1, G4MI_EINVAL, "gemm: missing argument");
+  G4MI_REQUIRE(K % kBK == 0, G4MI_EUNSUPPORTED, "gemm: K=%lld must be a multiple of %d", (long long)K, kBK);
+  G4MI_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ((uintptr_t)a & 15u) == 0 && ((uintptr_t)b & 15u) == 0, G4MI_EALIGN,
+               "gemm: operand rows must be 16-byte aligned");
+  G4MI_REQUIRE(epilogue >= kEpBf16 && epilogue <= kEpGated, G4MI_EINVAL, "gemm: bad epilogue %d", epilogue);
+  G4MI_REQUIRE(epilogue != kEpGated || (pair_offset % 8 == 0 && pair_offset != 0), G4MI_EINVAL,
+               "gemm: the gated epilogue needs the up rows' offset");
+  G4MI_REQUIRE(tiles == nullptr || (ntiles && max_tiles >= 1), G4MI_EINVAL, "gemm: grouped tiles need a count");
+  G4MI_REQUIRE(k_slices >= 1 && k_slices <= K / kBK && k_slices <= 64, G4MI_EINVAL, "gemm: bad k_slices");
+  G4MI_REQUIRE(k_slices == 1 || (tiles == nullptr && epilogue != kEpGated), G4MI_EUNSUPPORTED,
+               "gemm: split-K is for plain bf16/f32 outputs");
+  G4MI_REQUIRE(k_slices == 1 || (ws && ws_bytes >= g4mi_gemm_workspace_bytes(M, N, k_slices)), G4MI_EWORKSPACE,
+               "gemm: workspace too small for split-K");
+  GemmArgs g;
+  g.a = a; g.lda = lda; g.a_rows = a_rows; g.b = b; g.ldb = ldb; g.b_group_stride = b_group_stride;
+  g.pair_offset = pair_offset; g.M = (int)M; g.N = (int)N; g.K = (int)K; g.tiles = (const GemmTile*)tiles;
+  g.ntiles = ntiles; g.c = c; g.ldc = ldc; g.row_scale = row_scale; g.k_slices = (int)k_slices;
+  g.partial = (float*)ws;
+  hipStream_t st = as_stream(stream);
+  // grouped tiles are 64 rows; small plain M takes 64-row tiles too
+  const bool small = tiles != nullptr || M <= 64;
+  const int64_t mtiles = tiles ? max_tiles : (M + (small ? 63 : 127)) / (small ? 64 : 128);
+  G4MI_REQUIRE(mtiles <= 2147483647, G4MI_EINVAL, "gemm: too many tiles");
+  if (small) {
+    if (epilogue == kEpGated) launch<64, 128, kEpGated>(g, (int)mtiles, st);
+    else if (k_slices > 1 || epilogue == kEpF32) launch<64, 64, kEpF32>(g, (int)mtiles, st);
+    else launch<64, 64, kEpBf16>(g, (int)mtiles, st);
+  } else {
+    if (epilogue == kEpGated) launch<128, 128, kEpGated>(g, (int)mtiles, st);
+    else if (k_slices > 1 || epilogue == kEpF32) launch<128, 128, kEpF32>(g, (int)mtiles, st);
+    else launch<128, 128, kEpBf16>(g, (int)mtiles, st);
+  }
+  if (k_slices > 1) {
+    const int64_t mn = M * N;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, (const float*)ws,
+                       (int)k_slices, mn, (int)N, c, ldc, epilogue == kEpF32 ? 1 : 0);
+  }
+  return check_launch("gemm_bf16");
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+// Batched prefill pieces: the dense-MoE prefill on MFMA (model.py:241-250)
+// and the row-wise glue between the prefill GEMMs (model.py:297-322, 355-357).
+//
+// MoE prefill (K8).  The reference evaluates all E experts for every token
+// and masks the result with the routing weights (w_full = 0 for experts a
+// token did not select), so an unselected expert contributes act = bf16(x * 0)
+// = 0 to the down contraction: exact zeros.  This path therefore runs only
+// the selected (token, expert) pairs as grouped GEMMs, 16x fewer FLOPs at
+// E = 128, k = 8, with the same rounding points:
+//   1. moe_sort_kernel: tokens grouped by expert (counts, offsets, a gather
+//      list, the per-slot routing weight) and 64-row GEMM tiles per expert;
+//   2. gate/up GEMM over the gathered rows with the gated epilogue:
+//      act = bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w))   (model.py:246-247);
+//   3. down GEMM, f32 output per (token, expert);
+//   4. moe_combine_kernel: out[t] = bf16(sum over the token's slots in order)
+//      -- one f32 sum over (expert, f) as the dense einsum (model.py:250).
+#include "capi_util.h"
+#include "common.h"
+
+extern "C" int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                              int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                              const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue,
+                              void* c, int64_t ldc, const float* row_scale, int64_t k_slices, void* ws,
+                              int64_t ws_bytes, void* stream);
+
+namespace g4mi {
+
+constexpr int kTileRows = 64;  // grouped GEMM tile height (gemm.hip's small tiles)
+constexpr int kMaxExperts = 256;
+
+// One block.  entries i = t*K + s (token t, slot s) of the routing.
+//   sorted position p of entry i: offsets[e] + (rank among entries of expert e)
+//   a_rows[p] = t, w_sorted[p] = top_w[i], slot_pos[i] = p (-1: invalid expert)
+//   tiles: (e, m0, m1) for every 64 rows of every expert, ntiles[0] = count.
+__global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ top_i,
+                                                        const float* __restrict__ top_w, int n, int K, int E,
+                                                        int32_t* __restrict__ a_rows, float* __restrict__ w_sorted,
+                                                        int32_t* __restrict__ slot_pos, int32_t* __restrict__ tiles,
+                                                        int32_t* __restrict__ ntiles) {
+  __shared__ int cnt[kMaxExperts], off[kMaxExperts], cur[kMaxExperts], toff[kMaxExperts];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += blockDim.x) cnt[e] = 0;
+  __syncthreads();
+  const int total = n * K;
+  for (int i = tid; i < total; i += blockDim.x) {
+    const int e = top_i[i];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int o = 0, to = 0;
+    for (int e = 0; e < E; ++e) {
+      off[e] = o;
+      cur[e] = 0;
+      toff[e] = to;
+      o += cnt[e];
+      to += (cnt[e] + kTileRows - 1) / kTileRows;
+    }
+    ntiles[0] = to;
+  }
+  __syncthreads();
+  for (int i = tid; i < total; i += blockDim.x) {
+    const int e = top_i[i];
+    if (e >= 0 && e < E) {
+      const int p = off[e] + atomicAdd(&cur[e], 1);
+      a_rows[p] = i / K;
+      w_sorted[p] = top_w[i];
+      slot_pos[i] = p;
+    } else {
+      slot_pos[i] = -1;
+    }
+  }
+  for (int e = tid; e < E; e += blockDim.x) {
+    const int nt = (cnt[e] + kTileRows - 1) / kTileRows;
+    for (int j = 0; j < nt; ++j) {
+      int32_t* t = tiles + 3 * (toff[e] + j);
+      t[0] = e;
+      t[1] = off[e] + j * kTileRows;
+      t[2] = min(off[e] + (j + 1) * kTileRows, off[e] + cnt[e]);
+    }
+  }
+}
+
+// out[t, h] = bf16(sum over s < K, in order, of part[slot_pos[t*K + s], h]) (f32)
+__global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ part,
+                                                          const int32_t* __restrict__ slot_pos, int n, int K, int H,
+                                                          uint16_t* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int h = blockIdx.x * 256 + threadIdx.x;
+  if (t >= n || h >= H) return;
+  float s = 0.0f;
+  for (int q = 0; q < K; ++q) {
+    const int p = slot_pos[t * K + q];
+    if (p >= 0) s += part[(size_t)p * H + h];
+  }
+  out[(size_t)t * H + h] = f2bf(s);
+}
+
+static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
+
+struct MoePrefillWs {
+  int32_t *a_rows, *slot_pos, *tiles, *ntiles;
+  float *w_sorted, *part;
+  uint16_t* act;
+};
+
+static MoePrefillWs moe_prefill_ws(void* ws, int64_t n, int64_t K, int64_t E, int64_t F, int64_t H) {
+  const int64_t nk = n * K, max_tiles = (nk + kTileRows - 1) / kTileRows + E;
+  char* p = (char*)ws;
+  MoePrefillWs w;
+  w.a_rows = (int32_t*)p; p += al256(nk * 4);
+  w.slot_pos = (int32_t*)p; p += al256(nk * 4);
+  w.tiles = (int32_t*)p; p += al256(max_tiles * 12);
+  w.ntiles = (int32_t*)p; p += 256;
+  w.w_sorted = (float*)p; p += al256(nk * 4);
+  w.act = (uint16_t*)p; p += al256(nk * F * 2);
+  w.part = (float*)p;
+  return w;
+}
+
+}  // namespace g4mi
+
+using namespace g4mi;
+
+extern "C" {
+
+int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_t F, int64_t H) {
+  const int64_t nk = n * K, max_tiles = (nk + kTileRows - 1) / kTileRows + E;
+  return 3 * al256(nk * 4) + al256(max_tiles * 12) + 256 + al256(nk * F * 2) + al256(nk * H * 4);
+}
+
+int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
+                     const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
+                     void* ws, int64_t ws_bytes, void* stream) {
+  G4MI_REQUIRE(xn && top_w && top_i && gate_up && down && out && ws, G4MI_EINVAL, "moe_prefill: missing argument");
+  G4MI_REQUIRE(n >= 1 && n <= 65535 && K >= 1 && K <= 32 && E >= 1 && E <= kMaxExperts, G4MI_EINVAL,
+               "moe_prefill: bad n/K/E");
+  G4MI_REQUIRE(H % 32 == 0 && F % 32 == 0, G4MI_EUNSUPPORTED, "moe_prefill: H and F must be multiples of 32");
+  G4MI_REQUIRE(ws_bytes >= g4mi_moe_prefill_workspace_bytes(n, K, E, F, H), G4MI_EWORKSPACE,
+               "moe_prefill: workspace too small");
+  hipStream_t st = as_stream(stream);
+  const MoePrefillWs w = moe_prefill_ws(ws, n, K, E, F, H);
+  const int64_t max_tiles = (n * K + kTileRows - 1) / kTileRows + E;
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, (int)n, (int)K, (int)E, w.a_rows,
+                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles);
+  int rc = check_launch("moe_prefill sort");
+  if (rc) return rc;
+  // gate/up: gathered token rows x the expert's (gate, up) rows -> act [n*K, F]
+  rc = g4mi_gemm_bf16(xn, H, w.a_rows, gate_up, H, 2 * F * H, F * H, n * K, F, H, w.tiles, w.ntiles, max_tiles,
+                      2, w.act, F, w.w_sorted, 1, nullptr, 0, stream);
+  if (rc) return rc;
+  // down: act rows x the expert's down rows -> f32 partial [n*K, H]
+  rc = g4mi_gemm_bf16(w.act, F, nullptr, down, F, H * F, 0, n * K, H, F, w.tiles, w.ntiles, max_tiles, 1, w.part,
+                      H, nullptr, 1, nullptr, 0, stream);
+  if (rc) return rc;
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
+                     w.slot_pos, (int)n, (int)K, (int)H, out);
+  return check_launch("moe_prefill combine");
+}
+
+}  // extern "C"

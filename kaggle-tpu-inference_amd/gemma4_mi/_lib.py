@@ -76,6 +76,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g4mi_argmax_finalize": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _p]),
     "g4mi_advance_feed": (_int, [_p, _i64, _p, _p, _p, _i64, _p]),
     "g4mi_sample_workspace_bytes": (_i64, [_i64]),
+    "g4mi_gemm_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "g4mi_gemm_bf16": (
+        _int,
+        [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _i32, _p, _i64, _p, _i64, _p, _i64, _p],
+    ),
+    "g4mi_moe_prefill_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "g4mi_moe_prefill": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p]),
     "g4mi_sample": (_int, [_p, _i64, _i64, _p, _i32, _p, _p, _p, _i64, _p, _i64, _p]),
     "g4mi_kv_append": (
         _int,

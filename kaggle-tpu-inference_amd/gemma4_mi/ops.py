@@ -444,3 +444,57 @@ def sample(logits, top_k: int, params, tok, counter_mode: int = 1, pos=None, his
     _lib.call("g4mi_sample", _ptr(logits), V, int(top_k), _ptr(params), int(counter_mode), _ptr(tok), _ptr(pos),
               _ptr(hist), 0 if hist is None else hist.numel(), _ptr(ws), ws.numel(), stream_handle(logits.device))
     return tok
+
+
+# ------------------------------------------------------------------------- prefill GEMMs
+EP_BF16, EP_F32, EP_GATED = 0, 1, 2
+
+
+def gemm(a, b, out=None, a_rows=None, epilogue=EP_BF16, pair_offset=0, n=None, row_scale=None, k_slices=1,
+         lda=None, ldc=None, tiles=None, ntiles=None, m=None):
+    """C = A[a_rows] . B^T on MFMA (bf16 in, f32 accumulate).
+
+    a [*, K] bf16; b [N, K] bf16, or [G, ..., N, K] groups selected per
+    64-row tile by `tiles` (int32 [T, 3] of (group, m0, m1), live count in
+    `ntiles`, int32 [1]).  epilogue EP_BF16, EP_F32, or EP_GATED with the up
+    rows at b + pair_offset elements and row_scale [M] f32 (n = gate rows).
+    out [M, N] (row stride ldc)."""
+    K = a.shape[-1]
+    M = m if m is not None else (a_rows.numel() if a_rows is not None else a.shape[0])
+    N = n if n is not None else b.shape[-2]
+    _need(a, BF16, "a")
+    _need(b, BF16, "b")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32 if epilogue == EP_F32 else BF16, device=a.device)
+    ws = None
+    nbytes = int(_lib.lib().g4mi_gemm_workspace_bytes(M, N, k_slices))
+    if nbytes:
+        ws = WORKSPACE.get(a.device, "gemm", nbytes)
+    group_stride = b.stride(0) if (tiles is not None and b.dim() >= 3) else 0
+    _lib.call("g4mi_gemm_bf16", _ptr(a), a.stride(0) if lda is None else lda, _ptr(a_rows), _ptr(b), b.stride(-2),
+              group_stride, int(pair_offset), M, N, K, _ptr(tiles), _ptr(ntiles),
+              0 if tiles is None else tiles.shape[0], int(epilogue), _ptr(out),
+              out.stride(0) if ldc is None else ldc, _ptr(row_scale), int(k_slices), _ptr(ws),
+              0 if ws is None else ws.numel(), stream_handle(a.device))
+    return out
+
+
+def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
+    """model.py:241-250 for xn [n, H]: out [n, H] bf16 (selected experts only,
+    grouped MFMA GEMMs)."""
+    n, H = xn.shape
+    E, _, F, _ = gate_up.shape
+    K = top_i.shape[1]
+    _need(xn, BF16, "xn")
+    _need(top_w, torch.float32, "top_w", (n, K))
+    _need(top_i, torch.int32, "top_i", (n, K))
+    _need(gate_up, BF16, "gate_up", (E, 2, F, H))
+    _need(down, BF16, "down", (E, H, F))
+    if out is None:
+        out = torch.empty((n, H), dtype=BF16, device=xn.device)
+    nbytes = int(_lib.lib().g4mi_moe_prefill_workspace_bytes(n, K, E, F, H))
+    if ws is None:
+        ws = WORKSPACE.get(xn.device, "moe_prefill", nbytes)
+    _lib.call("g4mi_moe_prefill", _ptr(xn), _ptr(top_w), _ptr(top_i), _ptr(gate_up), _ptr(down), n, H, F, E, K,
+              _ptr(out), _ptr(ws), ws.numel(), stream_handle(xn.device))
+    return out
