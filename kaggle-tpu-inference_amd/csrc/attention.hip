@@ -143,8 +143,23 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   const int npos = end - start;
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
 
-  // Prologue, all loads first: wave w owns q heads w, w+4 (G <= 8); with the
-  // append, waves 2 and 3 also own the new K and V rows.
+  // The first K tile of this wave is requested before anything else: it
+  // does not depend on q, so its HBM latency overlaps the q prologue.
+  const int kg = lane >> 4, col = lane & 15;
+  const int ntiles = (npos + 15) >> 4;
+  auto load_tile = [&](int t, u32x4* bf, long long& off) {
+    const int jc = min(t * 16 + col, npos - 1);
+    off = page_off(a, pt_row, start + jc, kv);
+    const uint16_t* kp = k_pages + max(off, 0ll) + 8 * kg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
+  };
+  u32x4 bcur[KS];
+  long long ocur;
+  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur);
+
+  // Prologue: wave w owns q heads w, w+4 (G <= 8); with the append, waves 2
+  // and 3 also own the new K and V rows.
   const int so = lane * PL;                 // this lane's slice offset
   const int jo = so % (D / 2);              // its cos/sin offset
   const bool mine = append && (end == pos + 1);
@@ -193,22 +208,10 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
       }
   }
 
-  const int kg = lane >> 4, col = lane & 15;
   u32x4 af[KS];
 #pragma unroll
   for (int s = 0; s < KS; ++s) af[s] = *(const u32x4*)(qa + col * D + 32 * s + 8 * kg);
   const float cap = a.softcap;
-  const int ntiles = (npos + 15) >> 4;
-  auto load_tile = [&](int t, u32x4* bf, long long& off) {
-    const int jc = min(t * 16 + col, npos - 1);
-    off = page_off(a, pt_row, start + jc, kv);
-    const uint16_t* kp = k_pages + max(off, 0ll) + 8 * kg;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
-  };
-  u32x4 bcur[KS];
-  long long ocur;
-  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur);
   for (int t = wave; t < ntiles; t += 4) {
     u32x4 bnext[KS];
     long long onext;

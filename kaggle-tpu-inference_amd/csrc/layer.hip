@@ -25,6 +25,8 @@
 // under the HBM latency of its own rows.  RMSNorm scales use exact f64 sums.
 #include <string.h>
 
+#include <algorithm>
+
 #include "capi_util.h"
 #include <cstdlib>
 
@@ -33,56 +35,69 @@
 
 namespace g4mi {
 
-constexpr int kVecChunks = 2;  // 16-byte chunks per thread: H <= 256*8*2 = 4096
-
-// A length-H bf16 vector spread over a 256-thread block: thread t owns the
-// 16-byte chunks t and t+256.
-struct Vec {
-  u32x4 c[kVecChunks];
+// A length-H bf16 vector spread over an NT-thread block (H <= 4096): thread
+// t owns the 16-byte chunks t + NT*j, j < NC.  Chunks past H/8 are zero, so
+// the arithmetic helpers need no bounds checks (a zero chunk stays zero and
+// adds nothing to a sum of squares); only stores are masked.
+template <int NT>
+struct VecT {
+  static constexpr int NC = 512 / NT;
+  u32x4 c[NC];
 };
+using Vec = VecT<256>;
 
-__device__ __forceinline__ void vload(Vec& v, const uint16_t* __restrict__ p, int nch) {
+template <int NT>
+__device__ __forceinline__ void vload(VecT<NT>& v, const uint16_t* __restrict__ p, int nch) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) {
-    const int c = threadIdx.x + 256 * j;
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
+    const int c = threadIdx.x + NT * j;
     v.c[j] = (c < nch) ? ld16((const u32x4*)p + c) : u32x4{0u, 0u, 0u, 0u};
   }
 }
 // vload of a vector other blocks of this kernel wrote with coherent stores
-__device__ __forceinline__ void vload_coherent(Vec& v, const uint16_t* p, int nch) {
+template <int NT>
+__device__ __forceinline__ void vload_coherent(VecT<NT>& v, const uint16_t* p, int nch) {
   const __amdgpu_buffer_rsrc_t r = buffer_rsrc(p, (uint32_t)nch * 16u);
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) {
-    const int c = threadIdx.x + 256 * j;
-    v.c[j] = (c < nch) ? coherent_load16(r, (uint32_t)c * 16u) : u32x4{0u, 0u, 0u, 0u};
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
+    const int c = threadIdx.x + NT * j;
+    v.c[j] = coherent_load16(r, (uint32_t)c * 16u);  // out of range reads zero
   }
 }
-__device__ __forceinline__ double vsumsq(const Vec& v, int nch) {
-  double s = 0.0;
+template <int NT>
+__device__ __forceinline__ double vsumsq(const VecT<NT>& v) {
+  // two accumulators per chunk halve the dependent f64 chain
+  double s0 = 0.0, s1 = 0.0;
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j)
-    if ((int)threadIdx.x + 256 * j < nch) s = sumsq8_f64(v.c[j], s);
-  return s;
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
+    float f[8];
+    unpack8(v.c[j], f);
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      s0 = fma((double)f[i], (double)f[i], s0);
+      s1 = fma((double)f[i + 1], (double)f[i + 1], s1);
+    }
+  }
+  return s0 + s1;
 }
 // v = bf16(v * r * w)  (w may be null)
-__device__ __forceinline__ void vscale(Vec& v, float r, const uint16_t* __restrict__ w, int nch) {
+template <int NT>
+__device__ __forceinline__ void vscale(VecT<NT>& v, float r, const uint16_t* __restrict__ w, int nch) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) {
-    const int c = threadIdx.x + 256 * j;
-    if (c < nch) {
-      if (w != nullptr) {
-        const u32x4 wc = ld16((const u32x4*)w + c);
-        v.c[j] = scale8(v.c[j], r, &wc);
-      } else {
-        v.c[j] = scale8(v.c[j], r, nullptr);
-      }
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
+    if (w != nullptr) {
+      const u32x4 wc = ld16((const u32x4*)w + min((int)threadIdx.x + NT * j, nch - 1));
+      v.c[j] = scale8(v.c[j], r, &wc);
+    } else {
+      v.c[j] = scale8(v.c[j], r, nullptr);
     }
   }
 }
 // a = bf16(a + b)
-__device__ __forceinline__ void vadd(Vec& a, const Vec& b, int nch) {
+template <int NT>
+__device__ __forceinline__ void vadd(VecT<NT>& a, const VecT<NT>& b) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) {
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
     float x[8], y[8];
     unpack8(a.c[j], x);
     unpack8(b.c[j], y);
@@ -93,41 +108,61 @@ __device__ __forceinline__ void vadd(Vec& a, const Vec& b, int nch) {
   }
 }
 // a = bf16(a * s)
-__device__ __forceinline__ void vmul(Vec& a, float s) {
+template <int NT>
+__device__ __forceinline__ void vmul(VecT<NT>& a, float s) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) a.c[j] = scale8(a.c[j], s, nullptr);
+  for (int j = 0; j < VecT<NT>::NC; ++j) a.c[j] = scale8(a.c[j], s, nullptr);
 }
-__device__ __forceinline__ void vstore(const Vec& v, u32x4* dst, int nch) {
+template <int NT>
+__device__ __forceinline__ void vstore(const VecT<NT>& v, u32x4* dst, int nch) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) {
-    const int c = threadIdx.x + 256 * j;
+  for (int j = 0; j < VecT<NT>::NC; ++j) {
+    const int c = threadIdx.x + NT * j;
     if (c < nch) dst[c] = v.c[j];
   }
 }
-__device__ __forceinline__ float vrms(const Vec& v, int nch, int H, float eps, double* red) {
-  return rms_scale(block_sum_f64(vsumsq(v, nch), red), H, eps);
+// `red` holds 2*NT/64 doubles (block_sum2_f64 uses both halves)
+template <int NT>
+__device__ __forceinline__ double block_sum_nt(double v, double* red) {
+  constexpr int NW = NT / 64;
+  v = group_sum_f64<kWave>(v);
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  double t = red[0];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) t += red[i];
+  return t;
+}
+template <int NT>
+__device__ __forceinline__ float vrms(const VecT<NT>& v, int H, float eps, double* red) {
+  return rms_scale(block_sum_nt<NT>(vsumsq(v), red), H, eps);
 }
 
 // v = bf16(v * r * w) with the weight already in registers
-__device__ __forceinline__ void vscale_w(Vec& v, float r, const Vec& w) {
+template <int NT>
+__device__ __forceinline__ void vscale_w(VecT<NT>& v, float r, const VecT<NT>& w) {
 #pragma unroll
-  for (int j = 0; j < kVecChunks; ++j) v.c[j] = scale8(v.c[j], r, &w.c[j]);
+  for (int j = 0; j < VecT<NT>::NC; ++j) v.c[j] = scale8(v.c[j], r, &w.c[j]);
 }
-// Two block sums in one reduction round (exact f64 inputs).
+// Two block sums in one reduction round.
+template <int NT>
 __device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red) {
+  constexpr int NW = NT / 64;
   a = group_sum_f64<kWave>(a);
   b = group_sum_f64<kWave>(b);
-  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  const int w = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) {
     red[w] = a;
-    red[4 + w] = b;
+    red[NW + w] = b;
   }
   __syncthreads();
-  double ta = 0.0, tb = 0.0;
-  for (int i = 0; i < nw; ++i) {
+  double ta = red[0], tb = red[NW];
+#pragma unroll
+  for (int i = 1; i < NW; ++i) {
     ta += red[i];
-    tb += red[4 + i];
+    tb += red[NW + i];
   }
   a = ta;
   b = tb;
@@ -140,11 +175,13 @@ __device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red
 struct TailArgs {
   const uint16_t *x1, *mlp, *moe, *w_pf1, *w_pf2, *w_pf, *ls;
 };
+template <int NT>
 struct TailRegs {
-  Vec a, b, x1, w1, w2, w3;
+  VecT<NT> a, b, x1, w1, w2, w3;
   uint16_t ls;
 };
-__device__ __forceinline__ void tail_load(TailRegs& T, const TailArgs& t, int nch) {
+template <int NT>
+__device__ __forceinline__ void tail_load(TailRegs<NT>& T, const TailArgs& t, int nch) {
   vload(T.a, t.mlp, nch);
   vload(T.x1, t.x1, nch);
   vload(T.w3, t.w_pf, nch);
@@ -155,17 +192,18 @@ __device__ __forceinline__ void tail_load(TailRegs& T, const TailArgs& t, int nc
   }
   T.ls = t.ls[0];
 }
-__device__ __forceinline__ void tail_compute(Vec& x, TailRegs& T, bool moe, int nch, int H, float eps, double* red) {
+template <int NT>
+__device__ __forceinline__ void tail_compute(VecT<NT>& x, TailRegs<NT>& T, bool moe, int H, float eps, double* red) {
   if (moe) {
-    double s1 = vsumsq(T.a, nch), s2 = vsumsq(T.b, nch);
-    block_sum2_f64(s1, s2, red);
+    double s1 = vsumsq(T.a), s2 = vsumsq(T.b);
+    block_sum2_f64<NT>(s1, s2, red);
     vscale_w(T.a, rms_scale(s1, H, eps), T.w1);
     vscale_w(T.b, rms_scale(s2, H, eps), T.w2);
-    vadd(T.a, T.b, nch);
+    vadd(T.a, T.b);
   }
-  vscale_w(T.a, vrms(T.a, nch, H, eps, red), T.w3);
+  vscale_w(T.a, vrms(T.a, H, eps, red), T.w3);
   x = T.x1;
-  vadd(x, T.a, nch);
+  vadd(x, T.a);
   vmul(x, bf2f(T.ls));
 }
 
@@ -228,7 +266,7 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[8];
+  __shared__ double red[16];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31;
   const int q_rows = a.rows[0], k_rows = a.rows[1];
   const int total = q_rows + k_rows + a.rows[2];
@@ -244,7 +282,7 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   // parameter and the row loads are unconditional (clamped addresses), so no
   // branch merge forces an early full wait.
   Vec x, win;
-  TailRegs T;
+  TailRegs<256> T;
   if constexpr (MODE != kInNormed) vload(win, a.w_in, NCH);
   if constexpr (MODE == kInEmbed) {
     int t = a.tok[0];
@@ -256,23 +294,25 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
     vload(x, a.x_in, NCH);
   }
   // The compiler may not sink the prologue loads below the row loads (their
-  // results would then wait for the rows).  One row batch per wave is
-  // requested before the prologue, the rest after it: issuing all of them
-  // first would hold the prologue's instructions behind the CU's memory queue.
+  // results would then wait for the rows).  All NPF row batches of the wave
+  // are requested before the prologue, so the prologue's latency (the layer
+  // tail is three dependent block reductions) hides under the weight stream.
   asm volatile("" ::: "memory");
   PairWalk<IT> pw(a.pairs_per_block, (total + 1) / 2);
   constexpr int NPF = kInPrefetch;
   u32x4 w[NPF][IT];
-  load_row<32, IT>(rowptr(min(pw.p, pw.plast)), l, w[0]);
+#pragma unroll
+  for (int d = 0; d < NPF; ++d) load_row<32, IT>(rowptr(min(pw.p + 4 * d, pw.plast)), l, w[d]);
   if constexpr (MODE == kInEmbed) vmul(x, a.embed_c);
-  if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
+  if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, H, a.eps, red);
   if constexpr (MODE != kInNormed) {
+    // the residual store is issued after the last reduction, so no barrier
+    // waits for it
+    const float r = vrms(x, H, a.eps, red);
     if (blockIdx.x == 0 && a.x_out != nullptr) vstore(x, (u32x4*)a.x_out, NCH);
-    vscale_w(x, vrms(x, NCH, H, a.eps, red), win);
+    vscale_w(x, r, win);
   }
   vstore(x, xs, NCH);
-#pragma unroll
-  for (int d = 1; d < NPF; ++d) load_row<32, IT>(rowptr(min(pw.p + 4 * d, pw.plast)), l, w[d]);
   __syncthreads();
   int p = pw.p;
   // full batches: consume pair p+4d, refill it with pair p+4d+4*NPF (clamped)
@@ -331,7 +371,7 @@ struct FfnInArgs {
   int I;
   uint16_t* act_mlp;           // [I]
   int dense_blocks;            // blocks [0, dense_blocks) do dense rows
-  int tasks_per_block;         // dense (gate, up) pairs per dense block (multiple of 4)
+  int tasks_per_block;         // dense (gate, up) row pairs per dense block
   const uint16_t *r_scale, *r_proj;  // router (null: no MoE)
   int E;
   float r_c;                   // bf16(H^-0.5)
@@ -345,12 +385,14 @@ struct FfnInArgs {
   float eps;
 };
 
+constexpr int kFfnInTasks = 3;  // dense (gate, up) row pairs per wave requested up front
+
 template <int IT>
 __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[8];
+  __shared__ double red[16];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
   const bool dense = (int)blockIdx.x < a.dense_blocks;
   // prologue operands first (see layer_in), then the weight rows
@@ -364,16 +406,20 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   // wave w takes t0+w, t0+w+4, ...; router blocks own 8 expert rows each.
   const int t0 = blockIdx.x * a.tasks_per_block;
   const int tend = min(t0 + a.tasks_per_block, a.I), tlast = max(tend - 1, 0);
-  int t = t0 + wave;
   const int e = (blockIdx.x - a.dense_blocks) * 8 + wave * 2 + half;
   auto dense_row = [&](int f) { return (half ? a.up : a.gate) + (size_t)f * H; };
-  u32x4 w[IT];
-  load_row<32, IT>(dense ? dense_row(min(t, tlast)) : a.r_proj + (size_t)min(e, a.E - 1) * H, l, w);
+  // every task of this wave (t0 + wave + 4j, j < kFfnInTasks) is requested
+  // before the prologue; router blocks request their one row
+  u32x4 w[kFfnInTasks][IT];
+  load_row<32, IT>(dense ? dense_row(min(t0 + wave, tlast)) : a.r_proj + (size_t)min(e, a.E - 1) * H, l, w[0]);
+#pragma unroll
+  for (int j = 1; j < kFfnInTasks; ++j)
+    if (dense) load_row<32, IT>(dense_row(min(t0 + wave + 4 * j, tlast)), l, w[j]);
   // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
-  vscale_w(o, vrms(o, NCH, H, a.eps, red), wpa);
-  vadd(x, o, NCH);
+  vscale_w(o, vrms(o, H, a.eps, red), wpa);
+  vadd(x, o);
   if (blockIdx.x == 0) vstore(x, (u32x4*)a.x1_out, NCH);
-  const float r1 = vrms(x, NCH, H, a.eps, red);
+  const float r1 = vrms(x, H, a.eps, red);
   if (dense) {
     vscale_w(x, r1, wf);
     vstore(x, xs, NCH);
@@ -382,9 +428,9 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     vscale_w(xe, r1, wf);
     if (blockIdx.x == a.dense_blocks) vstore(xe, (u32x4*)a.xe_out, NCH);
     // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
-    const float r2 = vrms(xe, NCH, H, a.eps, red);
+    const float r2 = vrms(xe, H, a.eps, red);
 #pragma unroll
-    for (int j = 0; j < kVecChunks; ++j) {
+    for (int j = 0; j < Vec::NC; ++j) {
       const int c = tid + 256 * j;
       if (c < NCH) {
         float f[8], g[8];
@@ -400,21 +446,28 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   }
   __syncthreads();
   if (dense) {
-    for (; t < tend; t += 4) {
-      u32x4 wn[IT];
-      load_row<32, IT>(dense_row(min(t + 4, tlast)), l, wn);
-      const float acc = dot_row<32, IT>(w, xs, l);
+#pragma unroll
+    for (int j = 0; j < kFfnInTasks; ++j) {
+      const int t = t0 + wave + 4 * j;
+      const float acc = dot_row<32, IT>(w[j], xs, l);
+      const float up = __shfl(acc, 32, kWave);
+      if (t < tend && lane == 0) a.act_mlp[t] = f2bf(rbf(gelu_tanh(rbf(acc))) * rbf(up));
+    }
+    // tasks beyond kFfnInTasks per wave (small grids), one pair at a time
+    for (int t = t0 + wave + 4 * kFfnInTasks; t < tend; t += 4) {
+      u32x4 wr[IT];
+      load_row<32, IT>(dense_row(t), l, wr);
+      const float acc = dot_row<32, IT>(wr, xs, l);
       const float up = __shfl(acc, 32, kWave);
       if (lane == 0) a.act_mlp[t] = f2bf(rbf(gelu_tanh(rbf(acc))) * rbf(up));
-#pragma unroll
-      for (int i = 0; i < IT; ++i) w[i] = wn[i];
     }
   } else {
+    const u32x4* w0 = w[0];
     double d0 = 0.0, d1 = 0.0;
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
-      if (i & 1) d1 = dot8_f64(w[i], xs[l + 32 * i], d1);
-      else d0 = dot8_f64(w[i], xs[l + 32 * i], d0);
+      if (i & 1) d1 = dot8_f64(w0[i], xs[l + 32 * i], d1);
+      else d0 = dot8_f64(w0[i], xs[l + 32 * i], d0);
     }
     const double acc = group_sum_f64<32>(d0 + d1);
     if (e < a.E && l == 0)
@@ -438,8 +491,11 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
 }
 
 // ------------------------------------------------------------------ ffn_out
-// One wave per output row h: the dense down row (I values, 64 lanes) and the
-// k selected experts' down rows (8 lanes per expert slot, FIT = F/64 chunks).
+// One wave per output row h (kOutRows rows per block): the dense down row
+// (I values, 64 lanes) and the k selected experts' down rows (8 lanes per
+// expert slot, FIT = F/64 chunks).
+constexpr int kOutThreads = 256;
+constexpr int kOutRows = kOutThreads / 64;
 struct FfnOutArgs {
   const uint16_t* act_mlp;  // [I]
   const uint16_t* down;     // [H, I]
@@ -462,11 +518,12 @@ struct FfnOutArgs {
 };
 
 template <int FIT>
-__global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
+__global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
   constexpr int F = FIT * 64;
+  constexpr int NT = kOutThreads;
   extern __shared__ u32x4 act_lds[];  // I/8 chunks
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int h = blockIdx.x * 4 + wave;
+  const int h = blockIdx.x * kOutRows + wave;
   const int ich = a.I / 8;
   constexpr int DIT = 8;  // dense chunks per lane, at most (I <= 4096)
   const bool hv = h < a.H;
@@ -475,10 +532,10 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   // small operands first (issue order = completion order for vmcnt): the
   // routed expert of this lane group and this thread's share of act_mlp
   const int ei = (a.e_down != nullptr) ? a.top_i[min(g, a.K - 1)] : -1;
-  constexpr int ACT_PER = 2;  // act_mlp chunks per thread: I <= 8 * 256 * 2
+  constexpr int ACT_PER = 4096 / 8 / NT;  // act_mlp chunks per thread: I <= 4096
   u32x4 av[ACT_PER];
 #pragma unroll
-  for (int j = 0; j < ACT_PER; ++j) av[j] = ld16((const u32x4*)a.act_mlp + min(tid + 256 * j, ich - 1));
+  for (int j = 0; j < ACT_PER; ++j) av[j] = ld16((const u32x4*)a.act_mlp + min(tid + NT * j, ich - 1));
   // weight rows, unconditional with clamped addresses
   u32x4 wd[DIT];
   {
@@ -495,7 +552,7 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < ACT_PER; ++j)
-    if (tid + 256 * j < ich) act_lds[tid + 256 * j] = av[j];
+    if (tid + NT * j < ich) act_lds[tid + NT * j] = av[j];
   __syncthreads();
   if (hv) {  // wave-uniform
     float acc = 0.0f;
@@ -528,11 +585,11 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   // the next layer's input norm (model.py:298) once, so the next kernel
   // starts from the normalised vector instead of three dependent reductions.
   __shared__ int flag;
-  __shared__ double red[8];
+  __shared__ double red[2 * NT / 64];
   if (!arrive_last_grid(a.counter, &flag)) return;
   const int nch = a.H / 8;
-  TailRegs T;
-  Vec wn, x;
+  TailRegs<NT> T;
+  VecT<NT> wn, x;
   vload_coherent(T.a, a.mlp_out, nch);
   if (a.e_down != nullptr) vload_coherent(T.b, a.moe_out, nch);
   vload(T.x1, a.tail.x1, nch);
@@ -543,9 +600,10 @@ __global__ __launch_bounds__(256) void ffn_out_kernel(FfnOutArgs a) {
   }
   vload(wn, a.w_next, nch);
   T.ls = a.tail.ls[0];
-  tail_compute(x, T, a.e_down != nullptr, nch, a.H, a.eps, red);
+  tail_compute(x, T, a.e_down != nullptr, a.H, a.eps, red);
+  const float r = vrms(x, a.H, a.eps, red);
   vstore(x, (u32x4*)a.x_out, nch);
-  vscale_w(x, vrms(x, nch, a.H, a.eps, red), wn);
+  vscale_w(x, r, wn);
   vstore(x, (u32x4*)a.xn_out, nch);
 }
 
@@ -574,7 +632,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   constexpr int H = IT * 256;
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
-  __shared__ double red[8];
+  __shared__ double red[16];
   __shared__ float bvs[8];
   __shared__ int bis[8];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
@@ -583,7 +641,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   // first row pair of this wave, loads issued before the prologue
   int r = r0 + wave * 2 + half;
   Vec x, wn0;
-  TailRegs T;
+  TailRegs<256> T;
   if constexpr (NORMED) {
     vload(x, a.xn, NCH);
   } else {
@@ -594,8 +652,8 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   u32x4 w[IT];
   load_row<32, IT>(a.embed + (size_t)min(r, a.V - 1) * H, l, w);
   if constexpr (!NORMED) {
-    tail_compute(x, T, a.tail.moe != nullptr, NCH, H, a.eps, red);
-    vscale_w(x, vrms(x, NCH, H, a.eps, red), wn0);
+    tail_compute(x, T, a.tail.moe != nullptr, H, a.eps, red);
+    vscale_w(x, vrms(x, H, a.eps, red), wn0);
   }
   vstore(x, xs, NCH);
   __syncthreads();
@@ -805,7 +863,11 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
   FfnInArgs a;
   a.x = x; a.o = o; a.w_pa = post_attn_ln; a.w_pf = pre_ff_ln; a.w_pf2 = pre_ff2_ln;
   a.x1_out = x1_out; a.xe_out = xe_out; a.gate = gate; a.up = up; a.I = (int)I; a.act_mlp = act_mlp;
-  a.tasks_per_block = row_groups_per_block((int)I);
+  // dense blocks fill the CUs the router blocks leave, with at most
+  // 4 * kFfnInTasks tasks per block when that covers I
+  const int rblocks_host = router_proj ? (int)((E + 7) / 8) : 0;
+  const int dense_target = std::max(16, gemv_blocks() - rblocks_host);
+  a.tasks_per_block = (int)std::max<int64_t>(1, (I + dense_target - 1) / dense_target);
   a.dense_blocks = (int)((I + a.tasks_per_block - 1) / a.tasks_per_block);
   a.r_scale = router_scale; a.r_proj = router_proj; a.E = router_proj ? (int)E : 0;
   a.r_c = bf16_round_host(1.0 / sqrt((double)H));
@@ -854,12 +916,12 @@ int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint1
   a.bf16_running = combine == G4MI_COMBINE_BF16_RUNNING; a.moe_out = moe_out; a.H = (int)H;
   a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
   a.w_next = next_ln; a.x_out = x_out; a.xn_out = xn_out; a.counter = (unsigned int*)ws; a.eps = eps;
-  dim3 grid((unsigned)((H + 3) / 4));
+  dim3 grid((unsigned)((H + kOutRows - 1) / kOutRows));
   const size_t lds = (size_t)(I / 8) * 16;
   hipStream_t st = as_stream(stream);
   const int fit = experts_down ? (int)(F / 64) : 1;
   switch (fit) {
-#define G4MI_C(I) case I: hipLaunchKernelGGL(ffn_out_kernel<I>, grid, dim3(256), lds, st, a); break;
+#define G4MI_C(I) case I: hipLaunchKernelGGL(ffn_out_kernel<I>, grid, dim3(kOutThreads), lds, st, a); break;
     G4MI_IT16(G4MI_C)
 #undef G4MI_C
   }

@@ -154,14 +154,16 @@ def decode_masks(cfg: TextConfig, max_len: int, pos) -> dict:
 class DecodeRunner:
     """Launches one batch-1 token step of the model on the current stream.
 
-    Per layer: layer_in (q/k/v of the normalised input; the first layer
-    embeds the token), decode attention (append + scores, then PV + the
-    ordered split reduce), o_proj, ffn_in (post-attention norm, dense
+    Per layer: layer_in (the previous layer's tail and this layer's input
+    norm in every block's prologue, under its q/k/v row loads; the first
+    layer embeds the token), decode attention (append + scores, then PV +
+    the ordered split reduce), o_proj, ffn_in (post-attention norm, dense
     gate/up, router scores and the expert selection), routed expert gate/up,
-    ffn_out (dense and expert down + combine, then the layer tail and the
-    next layer's input norm once); then lm_head and the greedy argmax.  All buffers are allocated once, so a step can be captured
-    in a HIP graph and replayed; the token and position live in device
-    memory (`tok`, `pos`)."""
+    ffn_out (dense and expert down + combine); then lm_head (the last
+    layer's tail and the final norm in its prologue) and the greedy argmax.
+    All buffers are allocated once, so a step can be captured in a HIP graph
+    and replayed; the token and position live in device memory (`tok`,
+    `pos`)."""
 
     def __init__(self, cfg: TextConfig, params: dict, cache: dict, device="cuda", hist_len: int | None = None):
         from . import ops
@@ -245,9 +247,13 @@ class DecodeRunner:
             if i == 0:
                 ops.layer_in(0, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
                              q_rows, k_rows, v_rows, self.qkv, tok=self.tok, embed=p["embed"])
-            else:  # the previous ffn_out already applied the tail and this layer's input norm
-                ops.layer_in(3, H, eps, None, None, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
-                             q_rows, k_rows, v_rows, self.qkv, x_in=self.xn)
+            else:  # every block applies the previous layer's tail while its q/k/v rows stream in
+                pl = self.layers[i - 1]
+                ops.layer_in(1, H, eps, lp["input_layernorm"], self.x, lp["q_proj"], lp["k_proj"], lp.get("v_proj"),
+                             q_rows, k_rows, v_rows, self.qkv, x1=self.x1, mlp_out=self.mlp_out,
+                             moe_out=self.moe_out if moe else None, post_ff1=pl.get("post_feedforward_layernorm_1"),
+                             post_ff2=pl.get("post_feedforward_layernorm_2"), post_ff=pl["post_feedforward_layernorm"],
+                             layer_scalar=pl["layer_scalar"])
             q = self.qkv[:q_rows].view(1, NH, d)
             k = self.qkv[q_rows:q_rows + k_rows].view(1, kv, d)
             v = self.qkv[q_rows + k_rows:q_rows + k_rows + v_rows].view(1, kv, d) if v_rows else None
@@ -267,18 +273,17 @@ class DecodeRunner:
             if moe:
                 ops.moe_gateup(self.xe.view(1, H), lp["experts.gate_up_proj"], self.top_w[i:i + 1],
                                self.top_i[i:i + 1], act=self.act_moe.view(1, cfg.top_k_experts, -1))
-            nxt = self.layers[i + 1]["input_layernorm"] if i + 1 < cfg.num_hidden_layers else p["norm"]
-            tail = {"x1": self.x1, "post_ff1": lp.get("post_feedforward_layernorm_1"),
-                    "post_ff2": lp.get("post_feedforward_layernorm_2"), "post_ff": lp["post_feedforward_layernorm"],
-                    "layer_scalar": lp["layer_scalar"], "next_ln": nxt, "x_out": self.x, "xn_out": self.xn}
             ops.ffn_out(self.act_mlp, lp["mlp.down_proj"], self.mlp_out, self.act_moe if moe else None,
                         lp.get("experts.down_proj"), self.top_i[i] if moe else None, cfg.top_k_experts, combine,
-                        self.moe_out if moe else None, H, tail=tail, eps=eps, ws=self.ffn_out_ws)
+                        self.moe_out if moe else None, H)
         if feed is not None:
             ops.advance_feed(feed, self.tok, self.pos, self.hist)
             return
-        ops.lm_head_normed(self.xn, p["embed"], cfg.final_logit_softcapping, self.logits, self.blk_val,
-                           self.blk_idx)
+        # the last layer's tail and the final norm run in the lm_head prologue
+        pl = self.layers[-1]
+        ops.lm_head(self.x1, self.mlp_out, self.moe_out if moe else None, pl.get("post_feedforward_layernorm_1"),
+                    pl.get("post_feedforward_layernorm_2"), pl["post_feedforward_layernorm"], pl["layer_scalar"],
+                    p["norm"], p["embed"], cfg.final_logit_softcapping, eps, self.logits, self.blk_val, self.blk_idx)
         if sampler is not None:
             params, top_k, counter_mode = sampler
             ops.sample(self.logits, top_k, params, self.tok, counter_mode, self.pos if advance else None,
