@@ -14,8 +14,11 @@
 //       optional softcap, causal/sliding range; per-split max and sum of exp.
 //   pv: merges the split statistics, p = bf16(exp(s - m) / sum) -- the
 //       reference rounds the normalised probabilities to bf16 before the
-//       PV product (model.py:212) -- accumulates p . V in f32, and reduces the
-//       split partials in a fixed order into ctx = bf16(sum).
+//       PV product (model.py:212) -- and accumulates p . V in f32.  Up to
+//       kShortLen attended positions a block owns a kSliceD-wide slice of
+//       the head dims over all positions and writes ctx = bf16(sum)
+//       directly; longer ranges take split partials reduced in a fixed
+//       order by the last split to finish.
 // Masked positions contribute exp(-1e30 - m) = 0 in the reference, so only the
 // attended range [lo, pos] is visited.
 //
@@ -339,6 +342,131 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
   }
 }
 
+// Short ranges (len <= kShortLen): block x of a KV head owns head dims
+// [x*kSliceD, (x+1)*kSliceD) of its G query heads over every attended
+// position, so no partials cross blocks.  LPS lanes (8 dims each) cover a
+// position's slice, a wave takes PPW positions per step and the block PPB.
+// Each lane sums its positions in increasing order, then lanes with the same
+// dims are combined by a butterfly and the four waves in wave order.
+constexpr int kShortLen = 512;
+constexpr int kSliceD = 32;
+
+template <int D, int G>
+__device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int kv, int b,
+                                         const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
+                                         const float* __restrict__ ws_scores, const float* __restrict__ ws_stats,
+                                         uint16_t* __restrict__ ctx, float* pr, float* red, float* mg, float* sg) {
+  constexpr int LPS = kSliceD / 8;
+  constexpr int PPW = 64 / LPS;
+  constexpr int PPB = 4 * PPW;
+  constexpr int NST = kShortLen / PPB;       // V steps per lane at most
+  constexpr int SPT = G * kShortLen / 256;   // scores per thread at most
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int sub = lane % LPS, slot = lane / LPS;
+  const int d0 = blockIdx.x * kSliceD + sub * 8;
+  const int len = R.len;
+  const int nst = (len + PPB - 1) / PPB;
+  // loads first: this block's V slice at every position, then the scores
+  u32x4 vv[NST];
+  bool ok[NST];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    ok[st] = false;
+    if (st < nst) {  // block-uniform
+      const int j = st * PPB + wave * PPW + slot;
+      const long long off = page_off(a, pt_row, R.lo + min(j, len - 1), kv);
+      vv[st] = ld16((const u32x4*)(v_pages + max(off, 0ll) + d0));
+      ok[st] = (j < len) && (off >= 0);
+    }
+  }
+  float sreg[SPT];
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
+    sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + min(j, len - 1)];
+  }
+  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
+#pragma unroll
+  for (int u = 0; u < (G + 3) / 4; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      const int h = kv * G + g;
+      const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
+      const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
+      float st_m[kMaxSplits / 64], st_l[kMaxSplits / 64];
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) {
+        const int ic = min(lane + 64 * q, R.n_eff - 1);
+        const bool in = lane + 64 * q < R.n_eff;
+        st_m[q] = in ? sm[ic] : -INFINITY;
+        st_l[q] = in ? sl[ic] : 0.0f;
+      }
+      float m = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) m = fmaxf(m, st_m[q]);
+      m = wave_max_bfly(m);
+      float t = 0.0f;
+#pragma unroll
+      for (int q = 0; q < kMaxSplits / 64; ++q) t += (st_m[q] == -INFINITY) ? 0.0f : expf(st_m[q] - m) * st_l[q];
+      t = group_sum<64>(t);
+      if (lane == 0) {
+        mg[g] = m;
+        sg[g] = t;
+      }
+    }
+  }
+  __syncthreads();
+  // normalised probabilities, rounded to bf16 (model.py:212), zero past len
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
+    const float sv = sreg[r];
+    pr[g * kShortLen + j] = (j >= len || sv == -INFINITY) ? 0.0f : rbf(expf(sv - mg[g]) / sg[g]);
+  }
+  __syncthreads();
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+#pragma unroll
+  for (int st = 0; st < NST; ++st) {
+    if (st < nst) {
+      const int j = min(st * PPB + wave * PPW + slot, kShortLen - 1);
+      float vf[8];
+      unpack8(vv[st], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const float p = ok[st] ? pr[g * kShortLen + j] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = acc[g][i];
+#pragma unroll
+      for (int m = LPS; m < 64; m <<= 1) v += __shfl_xor(v, m, kWave);
+      acc[g][i] = v;
+    }
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red[(wave * G + g) * kSliceD + sub * 8 + i] = acc[g][i];
+  }
+  __syncthreads();
+  for (int e = tid; e < G * kSliceD; e += 256) {
+    const int g = e / kSliceD, dd = e % kSliceD;
+    const float v = ((red[g * kSliceD + dd] + red[(G + g) * kSliceD + dd]) + red[(2 * G + g) * kSliceD + dd]) +
+                    red[(3 * G + g) * kSliceD + dd];
+    ctx[((size_t)b * a.NH + kv * G + g) * D + blockIdx.x * kSliceD + dd] = f2bf(v);
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
                                                       const int32_t* __restrict__ page_table,
@@ -352,13 +480,22 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   constexpr int UB = 8;                        // wave steps of V loads in flight
   constexpr int RS = G * kChunkMax / 256;      // scores per thread
   constexpr int E4 = (G * D / 4 + 255) / 256;  // reduced float4s per thread
-  __shared__ float pr[G][kChunkMax];
+  constexpr int kLdsF = (G * kShortLen + 4 * G * kSliceD > G * kChunkMax) ? G * kShortLen + 4 * G * kSliceD
+                                                                          : G * kChunkMax;
+  __shared__ float lds_f[kLdsF];
+  float(*pr)[kChunkMax] = reinterpret_cast<float(*)[kChunkMax]>(lds_f);
   __shared__ float mg[G], sg[G];
   __shared__ int flag;
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = pos_arr[b];
   const Range R = attn_range(a, pos);
+  if (R.n_eff > 0 && R.len <= kShortLen) {  // grid.x >= D / kSliceD (see launch_attn)
+    if (split < D / kSliceD)
+      pv_short<D, G>(a, R, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, ctx, lds_f,
+                     lds_f + G * kShortLen, mg, sg);
+    return;
+  }
   if (split >= R.n_eff) {
     if (R.n_eff == 0 && split == 0)  // nothing attended: ctx = 0
       for (int e = tid; e < G * D; e += 256) ctx[(size_t)b * a.NH * D + (size_t)kv * G * D + e] = 0;
@@ -563,7 +700,8 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
                         int append, const AttnWs& w, uint16_t* ctx) {
   hipLaunchKernelGGL((attn_qk_kernel<D, G>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm, cs, sn,
                      kp, vp, pt, pos, append, w.scores, w.stats);
-  hipLaunchKernelGGL((attn_pv_kernel<D, G>), grid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
+  const dim3 pgrid(max(grid.x, (unsigned)(D / kSliceD)), grid.y, grid.z);  // short ranges use D / kSliceD blocks
+  hipLaunchKernelGGL((attn_pv_kernel<D, G>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
                      w.group, w.counters, ctx);
 }
 

@@ -2,7 +2,9 @@
 CPU oracle (model.py:197-213 restated in oracle/twin.py).
 
 Cases: small shapes with shuffled page tables, full and sliding masks, two
-sequences at different positions; k==v with softcap; and the two isolated
+sequences at different positions; k==v with softcap; the 26B layer shapes at
+decode positions on both sides of the 512-position limit between the
+per-slice PV path and the split partials; and the two isolated
 attention workloads at 32K positions (sliding window 1024 with 16 q / 8 KV
 heads at head_dim 256; full k==v with 16 q / 2 KV heads at head_dim 512;
 RoPE applied, softcap 50, seed 2).
@@ -139,6 +141,19 @@ def test_small_position_zero_and_page_boundary():
 
 def test_k_eq_v_softcap_eight_heads_per_kv():
     _run_case(1, 8, 1, 128, 520, 64, [519], 0, 50.0, True, 1e6, 0.25, 24)
+
+
+def test_full_layer_shape_both_sides_of_the_short_range_limit():
+    """26B full-layer shape (16 q / 2 KV heads, head_dim 512, k==v): attended
+    lengths 301, 511 and 512 take the per-slice path, 513 and 1501 the split
+    partials."""
+    _run_case(5, 16, 2, 512, 2048, 64, [300, 510, 511, 512, 1500], 0, 0.0, True, 1e6, 0.25, 31)
+
+
+def test_sliding_layer_shape_decode_positions():
+    """26B sliding-layer shape (16 q / 8 KV heads, head_dim 256, window
+    1024) at decode positions from the first token to a full window."""
+    _run_case(4, 16, 8, 256, 4096, 64, [5, 600, 1023, 3000], 1024, 0.0, False, 1e4, 1.0, 32)
 
 
 def test_isolated_sliding_attention_32k():
