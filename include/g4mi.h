@@ -287,6 +287,26 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
                      const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
                      void* ws, int64_t ws_bytes, void* stream);
 
+/* Row kernels between the batched prefill GEMMs, one token row of H <= 4096
+ * per block, with the decode kernels' rounding recipe:
+ *  rows_embed:     x = bf16(embed[tok] * bf16(sqrt(H))) (model.py:355-357),
+ *                  xn = rms_norm(x, input_layernorm) (model.py:298);
+ *  rows_post_attn: x1 = bf16(x + rms_norm(o, post_attention_layernorm)),
+ *                  xm = rms_norm(x1, pre_feedforward_layernorm), xe =
+ *                  rms_norm(x1, pre_feedforward_layernorm_2) (model.py:301-315;
+ *                  xe_out NULL without the MoE block);
+ *  rows_tail:      x = the layer tail (model.py:312-322), xn = rms_norm(x,
+ *                  next_ln) (the next layer's input norm). */
+int g4mi_rows_embed(const int32_t* tok, int64_t n, const uint16_t* embed, int64_t vocab, const uint16_t* input_ln,
+                    int64_t H, float eps, uint16_t* x_out, uint16_t* xn_out, void* stream);
+int g4mi_rows_post_attn(const uint16_t* x, const uint16_t* o, int64_t n, const uint16_t* post_attn_ln,
+                        const uint16_t* pre_ff_ln, const uint16_t* pre_ff2_ln, int64_t H, float eps, uint16_t* x1_out,
+                        uint16_t* xm_out, uint16_t* xe_out, void* stream);
+int g4mi_rows_tail(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, int64_t n,
+                   const uint16_t* post_ff1_ln, const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln,
+                   const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps, uint16_t* x_out,
+                   uint16_t* xn_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -14,8 +14,12 @@
 //   3. down GEMM, f32 output per (token, expert);
 //   4. moe_combine_kernel: out[t] = bf16(sum over the token's slots in order)
 //      -- one f32 sum over (expert, f) as the dense einsum (model.py:250).
+#include <math.h>
+#include <string.h>
+
 #include "capi_util.h"
 #include "common.h"
+#include "rowvec.h"
 
 extern "C" int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
                               int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
@@ -96,7 +100,98 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restric
   out[(size_t)t * H + h] = f2bf(s);
 }
 
+// ------------------------------------------------------------------ row kernels
+// One block per token row, the row held as a VecT<256> (H <= 4096).  The
+// arithmetic is the decode kernels' prologue arithmetic (rowvec.h), so the
+// prefill and the decode steps round identically.
+
+// x[t] = bf16(embed[tok[t]] * bf16(sqrt(H))) (model.py:355-357); xn[t] =
+// rms_norm(x[t], input_layernorm) (model.py:298).
+__global__ __launch_bounds__(256) void rows_embed_kernel(const int32_t* __restrict__ tok,
+                                                         const uint16_t* __restrict__ embed, int vocab, float c,
+                                                         const uint16_t* __restrict__ w_in, int H, float eps,
+                                                         uint16_t* __restrict__ x_out, uint16_t* __restrict__ xn_out) {
+  __shared__ double red[8];
+  const int t = blockIdx.x, nch = H / 8;
+  int id = tok[t];
+  id = (id < 0 || id >= vocab) ? 0 : id;
+  Vec x, w;
+  vload(x, embed + (size_t)id * H, nch);
+  vload(w, w_in, nch);
+  vmul(x, c);
+  const float r = vrms(x, H, eps, red);
+  vstore(x, (u32x4*)(x_out + (size_t)t * H), nch);
+  vscale_w(x, r, w);
+  vstore(x, (u32x4*)(xn_out + (size_t)t * H), nch);
+}
+
+// x1 = bf16(x + rms_norm(o, post_attention_layernorm)); xm = rms_norm(x1,
+// pre_feedforward_layernorm); xe = rms_norm(x1, pre_feedforward_layernorm_2)
+// (model.py:301-315; xe only with the MoE block).
+__global__ __launch_bounds__(256) void rows_post_attn_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ o,
+                                                             const uint16_t* __restrict__ w_pa,
+                                                             const uint16_t* __restrict__ w_pf,
+                                                             const uint16_t* __restrict__ w_pf2, int H, float eps,
+                                                             uint16_t* __restrict__ x1_out,
+                                                             uint16_t* __restrict__ xm_out,
+                                                             uint16_t* __restrict__ xe_out) {
+  __shared__ double red[8];
+  const int t = blockIdx.x, nch = H / 8;
+  const size_t ro = (size_t)t * H;
+  Vec xv, ov, wpa, wf, wf2;
+  vload(ov, o + ro, nch);
+  vload(xv, x + ro, nch);
+  vload(wpa, w_pa, nch);
+  vload(wf, w_pf, nch);
+  if (xe_out != nullptr) vload(wf2, w_pf2, nch);
+  vscale_w(ov, vrms(ov, H, eps, red), wpa);
+  vadd(xv, ov);
+  vstore(xv, (u32x4*)(x1_out + ro), nch);
+  const float r1 = vrms(xv, H, eps, red);
+  Vec xm = xv;
+  vscale_w(xm, r1, wf);
+  vstore(xm, (u32x4*)(xm_out + ro), nch);
+  if (xe_out != nullptr) {
+    vscale_w(xv, r1, wf2);
+    vstore(xv, (u32x4*)(xe_out + ro), nch);
+  }
+}
+
+// x = the layer tail of (x1, mlp, moe) (model.py:312-322); xn =
+// rms_norm(x, next input_layernorm) (model.py:298).
+__global__ __launch_bounds__(256) void rows_tail_kernel(TailArgs ta, const uint16_t* __restrict__ w_next, int H,
+                                                        float eps, uint16_t* __restrict__ x_out,
+                                                        uint16_t* __restrict__ xn_out) {
+  __shared__ double red[8];
+  const int t = blockIdx.x, nch = H / 8;
+  const size_t ro = (size_t)t * H;
+  TailArgs tr = ta;
+  tr.x1 += ro;
+  tr.mlp += ro;
+  if (tr.moe != nullptr) tr.moe += ro;
+  TailRegs<256> T;
+  Vec x, wn;
+  tail_load(T, tr, nch);
+  vload(wn, w_next, nch);
+  tail_compute(x, T, tr.moe != nullptr, H, eps, red);
+  const float r = vrms(x, H, eps, red);
+  vstore(x, (u32x4*)(x_out + ro), nch);
+  vscale_w(x, r, wn);
+  vstore(x, (u32x4*)(xn_out + ro), nch);
+}
+
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
+
+static float bf16_round_host(double v) {
+  float f = (float)v;
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  u &= 0xffff0000u;
+  memcpy(&f, &u, 4);
+  return f;
+}
 
 struct MoePrefillWs {
   int32_t *a_rows, *slot_pos, *tiles, *ntiles;
@@ -156,6 +251,45 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
                      w.slot_pos, (int)n, (int)K, (int)H, out);
   return check_launch("moe_prefill combine");
+}
+
+int g4mi_rows_embed(const int32_t* tok, int64_t n, const uint16_t* embed, int64_t vocab, const uint16_t* input_ln,
+                    int64_t H, float eps, uint16_t* x_out, uint16_t* xn_out, void* stream) {
+  G4MI_REQUIRE(tok && embed && input_ln && x_out && xn_out && vocab >= 1, G4MI_EINVAL, "rows_embed: missing argument");
+  G4MI_REQUIRE(n >= 1 && n <= 2147483647 && H % 8 == 0 && H >= 8 && H <= 4096, G4MI_EUNSUPPORTED,
+               "rows_embed: n=%lld H=%lld (H = 8*i <= 4096)", (long long)n, (long long)H);
+  const float c = bf16_round_host((double)(float)sqrt((double)H));
+  hipLaunchKernelGGL(rows_embed_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), tok, embed, (int)vocab,
+                     c, input_ln, (int)H, eps, x_out, xn_out);
+  return check_launch("rows_embed");
+}
+
+int g4mi_rows_post_attn(const uint16_t* x, const uint16_t* o, int64_t n, const uint16_t* post_attn_ln,
+                        const uint16_t* pre_ff_ln, const uint16_t* pre_ff2_ln, int64_t H, float eps, uint16_t* x1_out,
+                        uint16_t* xm_out, uint16_t* xe_out, void* stream) {
+  G4MI_REQUIRE(x && o && post_attn_ln && pre_ff_ln && x1_out && xm_out, G4MI_EINVAL, "rows_post_attn: missing argument");
+  G4MI_REQUIRE(xe_out == nullptr || pre_ff2_ln, G4MI_EINVAL, "rows_post_attn: xe needs pre_feedforward_layernorm_2");
+  G4MI_REQUIRE(n >= 1 && n <= 2147483647 && H % 8 == 0 && H >= 8 && H <= 4096, G4MI_EUNSUPPORTED,
+               "rows_post_attn: n=%lld H=%lld (H = 8*i <= 4096)", (long long)n, (long long)H);
+  hipLaunchKernelGGL(rows_post_attn_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), x, o, post_attn_ln,
+                     pre_ff_ln, pre_ff2_ln, (int)H, eps, x1_out, xm_out, xe_out);
+  return check_launch("rows_post_attn");
+}
+
+int g4mi_rows_tail(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, int64_t n,
+                   const uint16_t* post_ff1_ln, const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln,
+                   const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps, uint16_t* x_out,
+                   uint16_t* xn_out, void* stream) {
+  G4MI_REQUIRE(x1 && mlp_out && post_ff_ln && layer_scalar && next_ln && x_out && xn_out, G4MI_EINVAL,
+               "rows_tail: missing argument");
+  G4MI_REQUIRE(moe_out == nullptr || (post_ff1_ln && post_ff2_ln), G4MI_EINVAL,
+               "rows_tail: the MoE tail needs post_feedforward_layernorm_1/2");
+  G4MI_REQUIRE(n >= 1 && n <= 2147483647 && H % 8 == 0 && H >= 8 && H <= 4096, G4MI_EUNSUPPORTED,
+               "rows_tail: n=%lld H=%lld (H = 8*i <= 4096)", (long long)n, (long long)H);
+  const TailArgs ta{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
+  hipLaunchKernelGGL(rows_tail_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), ta, next_ln, (int)H, eps,
+                     x_out, xn_out);
+  return check_launch("rows_tail");
 }
 
 }  // extern "C"

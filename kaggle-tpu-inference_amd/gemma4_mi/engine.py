@@ -19,10 +19,15 @@ The token, position and the whole token history stay on the device; the
 host only replays graphs and copies each produced token into pinned memory,
 so `lookahead` steps stay queued while it reads the oldest one.
 
-Prefill runs the prompt one position at a time through the decode kernels
-(each row of the reference's causal prefill attends exactly the cached
-positions <= its own, so the result is the same); the prefill bucket is
-reported for compatibility but nothing is padded.
+Prefill (the default, prefill="batched") runs every prompt row through the
+layers at once (model.PrefillRunner: MFMA GEMMs for the projections and the
+dense-MoE experts, the decode attention kernels with one query row per
+sequence), then the head on the last row.  prefill="stepwise" instead feeds
+the prompt one position at a time through the decode kernels with the
+dense-MoE combine ("feed" graph, then "head").  Either way each prompt row
+attends exactly the cached positions <= its own, the reference's causal
+prefill; the prefill bucket is reported for compatibility but nothing is
+padded.
 """
 
 from __future__ import annotations
@@ -51,11 +56,15 @@ def _scalar(v) -> float:
 
 class Engine:
     def __init__(self, model_dir: str | None, max_len: int = 4096, batch: int = 1, top_k: int = 64, progress=None,
-                 *, cfg: TextConfig | None = None, params: dict | None = None, device: str = "cuda:0"):
+                 *, cfg: TextConfig | None = None, params: dict | None = None, device: str = "cuda:0",
+                 prefill: str = "batched"):
         if batch != 1:
             raise ValueError("this engine decodes one sequence (batch=1)")
         if not 1 <= top_k <= 64:
             raise ValueError("top_k must be in [1, 64]")
+        if prefill not in ("batched", "stepwise"):
+            raise ValueError("prefill must be 'batched' or 'stepwise'")
+        self.prefill_mode = prefill
         self.model_dir = model_dir
         self.cfg: TextConfig = cfg if cfg is not None else load_text_config(model_dir)
         self.max_len = int(max_len)
@@ -83,12 +92,14 @@ class Engine:
         self._stream = torch.cuda.Stream(self.device)
         self._pos_host = 0
         self._host_tok = torch.zeros(self.max_len + 1, dtype=torch.int32, pin_memory=True)
+        self._prefill_runner: M.PrefillRunner | None = None
 
     @classmethod
-    def random(cls, cfg: TextConfig, seed: int = 3, max_len: int = 4096, top_k: int = 64, device: str = "cuda:0"):
+    def random(cls, cfg: TextConfig, seed: int = 3, max_len: int = 4096, top_k: int = 64, device: str = "cuda:0",
+               prefill: str = "batched"):
         """An engine over seeded N(0, 0.02) random-init weights (no checkpoint)."""
         params = init_random_params(cfg, seed, device=device)
-        return cls(None, max_len, 1, top_k, cfg=cfg, params=params, device=device)
+        return cls(None, max_len, 1, top_k, cfg=cfg, params=params, device=device, prefill=prefill)
 
     # ---------------------------------------------------------------- graphs
     def _graph(self, kind: str, greedy: bool) -> torch.cuda.CUDAGraph:
@@ -137,6 +148,17 @@ class Engine:
         return t <= 0.0
 
     # ---------------------------------------------------------------- steps
+    def _prefill_for(self, n: int) -> M.PrefillRunner:
+        """The batched prefill runner, grown to a multiple of the bucket >= n."""
+        pr = self._prefill_runner
+        if pr is None or pr.capacity < n:
+            cap = min(self.max_len, _round_up(n, PREFILL_BUCKET))
+            self._prefill_runner = pr = None
+            pr = M.PrefillRunner(self.cfg, self.params, self.cache, cap, device=self.device,
+                                 rope=self._runner.rope)
+            self._prefill_runner = pr
+        return pr
+
     def _build_prefill(self, t: int):
         r = self._runner
 
@@ -150,12 +172,19 @@ class Engine:
             self._prompt[:n].copy_(toks)
             greedy = self._set_sampling(key, temperature, top_p)
             r.hist[:n].copy_(self._prompt[:n])
-            r.tok.copy_(self._prompt[:1])
-            r.pos.zero_()
-            feed = self._graph("feed", True)
-            for _ in range(n - 1):
-                feed.replay()
-            self._graph("head", greedy).replay()
+            if self.prefill_mode == "batched":
+                # every prompt row through the layers at once, then the head on row n-1
+                pr = self._prefill_for(n)
+                pr.run(self._prompt, n)
+                r.pos.fill_(n - 1)
+                r.head(*pr.last_row(n), sampler=None if greedy else (self._sp, self.top_k, 0))
+            else:
+                r.tok.copy_(self._prompt[:1])
+                r.pos.zero_()
+                feed = self._graph("feed", True)
+                for _ in range(n - 1):
+                    feed.replay()
+                self._graph("head", greedy).replay()
             self._pos_host = n
             return r.hist[n:n + 1].view(1, 1), cache, torch.tensor(n, dtype=torch.int32)
 
@@ -213,7 +242,8 @@ class Engine:
         toks = torch.zeros((1, bucket), dtype=torch.int32)
         t0 = time.perf_counter()
         tok, self.cache, pos = self.prefill_fn(bucket)(self.params, toks, self.cache, 4, 0, 0.0, 1.0)
-        self._graph("head", False)
+        if self.prefill_mode == "stepwise":
+            self._graph("head", False)
         torch.cuda.synchronize(self.device)
         out["prefill_compile_s"] = time.perf_counter() - t0
         t0 = time.perf_counter()

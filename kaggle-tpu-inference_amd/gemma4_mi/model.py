@@ -292,9 +292,153 @@ class DecodeRunner:
             ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos if advance else None,
                                 self.hist if advance else None)
 
+    def head(self, x1, mlp_out, moe_out, sampler=None) -> None:
+        """lm_head with the last layer's tail on (x1, mlp_out, moe_out) [H]
+        (model.py:317-322, 373-385), then the argmax or the sampler: the
+        token after position `pos` goes to tok and hist[pos + 1], pos += 1."""
+        ops, cfg, p = self.ops, self.cfg, self.params
+        pl = self.layers[-1]
+        ops.lm_head(x1, mlp_out, moe_out, pl.get("post_feedforward_layernorm_1"),
+                    pl.get("post_feedforward_layernorm_2"), pl["post_feedforward_layernorm"], pl["layer_scalar"],
+                    p["norm"], p["embed"], cfg.final_logit_softcapping, cfg.rms_norm_eps, self.logits, self.blk_val,
+                    self.blk_idx)
+        if sampler is not None:
+            params, top_k, counter_mode = sampler
+            ops.sample(self.logits, top_k, params, self.tok, counter_mode, self.pos, self.hist, ws=self.sample_ws)
+        else:
+            ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos, self.hist)
+
     def set_state(self, token: int, pos: int) -> None:
         self.tok.fill_(int(token))
         self.pos.fill_(int(pos))
+
+
+class PrefillRunner:
+    """Batched prefill of n prompt tokens at positions 0..n-1 (model.py:333-386
+    over T = n rows, dense-MoE path), leaving the last row's layer-tail inputs
+    for the head.  Per layer:
+
+      q/k/v = xn . W^T                  MFMA GEMMs (model.py:197-201)
+      kv_append                         k = rope(rms(k_raw)), v = rms(v_raw)
+                                        written at positions 0..n-1 (model.py:202-206)
+      decode_attention, append off      query row t attends [max(0, t+1-W), t]:
+                                        the causal / sliding prefill mask of
+                                        model.py:392-399 restricted to real rows
+      o = ctx . o_proj^T                MFMA GEMM (model.py:214)
+      rows_post_attn                    x1, xm, xe (model.py:301-315)
+      act = gelu(xm.g) * (xm.u)         MFMA GEMM, gated epilogue (model.py:218-220)
+      mlp = act . down^T                MFMA GEMM (model.py:221)
+      router top-k + moe_prefill        model.py:224-250 (selected experts only)
+      rows_tail                         tail + next input norm (model.py:312-322)
+
+    The first layer starts from rows_embed.  Rows beyond the prompt (the
+    reference's bucket padding) are not computed: the reference never attends
+    them and reads back only the last prompt row.  Attention runs in chunks
+    of `qchunk` query rows so its workspace stays bounded."""
+
+    def __init__(self, cfg: TextConfig, params: dict, cache: dict, capacity: int, device="cuda", qchunk: int = 256,
+                 rope=None):
+        from . import ops
+
+        self.ops, self.cfg, self.params, self.cache = ops, cfg, params, cache
+        self.device = dev = torch.device(device)
+        self.capacity = cap = int(capacity)
+        self.max_len = cache["max_len"]
+        if not 1 <= cap <= self.max_len:
+            raise ValueError(f"prefill capacity {cap} outside [1, {self.max_len}]")
+        self.qchunk = qchunk
+        self.layers = [{k[len(f"layers.{i}."):]: v for k, v in params.items() if k.startswith(f"layers.{i}.")}
+                       for i in range(cfg.num_hidden_layers)]
+        H, bf = cfg.hidden_size, torch.bfloat16
+        z = lambda *shape, dt=bf: torch.zeros(shape, dtype=dt, device=dev)  # noqa: E731
+        self.x, self.x1, self.xn, self.xm, self.o = z(cap, H), z(cap, H), z(cap, H), z(cap, H), z(cap, H)
+        self.mlp_out = z(cap, H)
+        moe = cfg.enable_moe_block
+        self.xe = z(cap, H) if moe else None
+        self.moe_out = z(cap, H) if moe else None
+        q_max = max(cfg.num_attention_heads * cfg.head_dim_for(lt) for lt in cfg.layer_types)
+        kv_max = max(cfg.kv_heads_for(lt) * cfg.head_dim_for(lt) for lt in cfg.layer_types)
+        self.q, self.ctx = z(cap * q_max), z(cap * q_max)
+        self.k, self.v = z(cap * kv_max), z(cap * kv_max)
+        self.act = z(cap, cfg.intermediate_size)
+        if moe:
+            self.top_w = z(cap, cfg.top_k_experts, dt=torch.float32)
+            self.top_i = z(cap, cfg.top_k_experts, dt=torch.int32)
+        self.pos = torch.arange(cap, dtype=torch.int32, device=dev)
+        self.page_row = cache["page_table"][0].contiguous()
+        self.pt_rep = cache["page_table"][0:1].expand(qchunk, -1).contiguous()
+        self.rope = rope if rope is not None else {
+            SLIDING: rope_table(cfg.head_dim, cfg.rope_theta_sliding, 1.0, self.max_len, dev),
+            FULL: rope_table(cfg.global_head_dim, cfg.rope_theta_full, cfg.rope_partial_rotary_factor_full,
+                             self.max_len, dev),
+        }
+        # attention over positions < capacity: lmax = capacity (rounded to pages)
+        page = cache["k"][0].shape[2]
+        self.lmax = min(self.max_len, ((cap + page - 1) // page) * page)
+        self.splits = max(1, ops.attention_min_splits(self.lmax))
+        ws = 0
+        for lt in set(cfg.layer_types):
+            ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(
+                qchunk, cfg.num_attention_heads, cfg.head_dim_for(lt), self.lmax, self.splits))
+        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+
+    def run(self, tokens: torch.Tensor, n: int) -> None:
+        """Runs the layers for tokens[:n] (device int32) on the current stream."""
+        ops, cfg, p = self.ops, self.cfg, self.params
+        if not 1 <= n <= self.capacity:
+            raise ValueError(f"{n} prompt tokens outside [1, {self.capacity}]")
+        H, eps, NH = cfg.hidden_size, cfg.rms_norm_eps, cfg.num_attention_heads
+        moe = cfg.enable_moe_block
+        L = cfg.num_hidden_layers
+        x, x1, xn, xm, o = self.x[:n], self.x1[:n], self.xn[:n], self.xm[:n], self.o[:n]
+        mlp_out = self.mlp_out[:n]
+        xe = self.xe[:n] if moe else None
+        moe_out = self.moe_out[:n] if moe else None
+        pos = self.pos[:n]
+        ops.rows_embed(tokens[:n], p["embed"], self.layers[0]["input_layernorm"], eps, x, xn)
+        for i, lt in enumerate(cfg.layer_types):
+            lp = self.layers[i]
+            d, kv = cfg.head_dim_for(lt), cfg.kv_heads_for(lt)
+            q = self.q[: n * NH * d].view(n, NH * d)
+            k = self.k[: n * kv * d].view(n, kv * d)
+            v = None if cfg.k_eq_v_for(lt) else self.v[: n * kv * d].view(n, kv * d)
+            ops.prefill_gemm(xn, lp["q_proj"].reshape(NH * d, H), q)
+            ops.prefill_gemm(xn, lp["k_proj"].reshape(kv * d, H), k)
+            if v is not None:
+                ops.prefill_gemm(xn, lp["v_proj"].reshape(kv * d, H), v)
+            cos, sin = self.rope[lt]
+            ops.kv_append(k.view(n, kv, d), None if v is None else v.view(n, kv, d), lp["k_norm"], cos, sin,
+                          self.cache["k"][i], self.cache["v"][i], self.page_row, pos, self.max_len, eps)
+            ctx = self.ctx[: n * NH * d].view(n, NH, d)
+            window = cfg.sliding_window if lt == SLIDING else 0
+            for c0 in range(0, n, self.qchunk):
+                c1 = min(n, c0 + self.qchunk)
+                b = c1 - c0
+                ops.decode_attention(q.view(n, NH, d)[c0:c1], k.view(n, kv, d)[c0:c1], None, lp["q_norm"],
+                                     lp["k_norm"], cos, sin, self.cache["k"][i], self.cache["v"][i],
+                                     self.pt_rep[:b], self.pos[c0:c1], window, cfg.attn_logit_softcapping, eps,
+                                     self.lmax, self.splits, append=False, ctx=ctx[c0:c1], ws=self.attn_ws)
+            ops.prefill_gemm(ctx.view(n, NH * d), lp["o_proj"].reshape(H, NH * d), o)
+            ops.rows_post_attn(x, o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
+                               lp.get("pre_feedforward_layernorm_2"), eps, x1, xm, xe)
+            gate, up = lp["mlp.gate_proj"], lp["mlp.up_proj"]
+            act = self.act[:n]
+            ops.prefill_gemm(xm, gate, act, epilogue=ops.EP_GATED,
+                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0])
+            ops.prefill_gemm(act, lp["mlp.down_proj"], mlp_out)
+            if moe:
+                tw, ti = self.top_w[:n], self.top_i[:n]
+                ops.moe_router_topk(xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],
+                                    cfg.top_k_experts, eps, out=(tw, ti))
+                ops.moe_prefill(xe, tw, ti, lp["experts.gate_up_proj"], lp["experts.down_proj"], out=moe_out)
+            if i + 1 < L:
+                ops.rows_tail(x1, mlp_out, moe_out, lp.get("post_feedforward_layernorm_1"),
+                              lp.get("post_feedforward_layernorm_2"), lp["post_feedforward_layernorm"],
+                              lp["layer_scalar"], self.layers[i + 1]["input_layernorm"], eps, x, xn)
+
+    def last_row(self, n: int) -> tuple:
+        """(x1, mlp_out, moe_out) of prompt row n-1: the last layer's tail inputs."""
+        return (self.x1[n - 1], self.mlp_out[n - 1], None if self.moe_out is None else self.moe_out[n - 1])
 
 
 _RUNNERS: dict = {}

@@ -498,3 +498,44 @@ def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
     _lib.call("g4mi_moe_prefill", _ptr(xn), _ptr(top_w), _ptr(top_i), _ptr(gate_up), _ptr(down), n, H, F, E, K,
               _ptr(out), _ptr(ws), ws.numel(), stream_handle(xn.device))
     return out
+
+
+# ------------------------------------------------------------------ prefill rows
+def rows_embed(tok, embed, input_ln, eps, x_out, xn_out):
+    """x = bf16(embed[tok] * bf16(sqrt(H))), xn = rms_norm(x, input_ln) for
+    n token rows (model.py:355-357, 298)."""
+    n = tok.numel()
+    V, H = embed.shape
+    _lib.call("g4mi_rows_embed", _ptr(tok), n, _ptr(embed), V, _ptr(input_ln), H, float(eps), _ptr(x_out),
+              _ptr(xn_out), stream_handle(embed.device))
+
+
+def rows_post_attn(x, o, post_attn_ln, pre_ff_ln, pre_ff2_ln, eps, x1_out, xm_out, xe_out=None):
+    """x1 = bf16(x + rms_norm(o, post_attn_ln)), xm = rms_norm(x1, pre_ff_ln),
+    xe = rms_norm(x1, pre_ff2_ln) for n rows (model.py:301-315)."""
+    n, H = x.shape
+    _lib.call("g4mi_rows_post_attn", _ptr(x), _ptr(o), n, _ptr(post_attn_ln), _ptr(pre_ff_ln), _ptr(pre_ff2_ln), H,
+              float(eps), _ptr(x1_out), _ptr(xm_out), _ptr(xe_out), stream_handle(x.device))
+
+
+def rows_tail(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, next_ln, eps, x_out, xn_out):
+    """The layer tail of n rows (model.py:312-322) and the next input norm."""
+    n, H = x1.shape
+    _lib.call("g4mi_rows_tail", _ptr(x1), _ptr(mlp_out), _ptr(moe_out), n, _ptr(post_ff1), _ptr(post_ff2),
+              _ptr(post_ff), _ptr(layer_scalar), _ptr(next_ln), H, float(eps), _ptr(x_out), _ptr(xn_out),
+              stream_handle(x1.device))
+
+
+def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256):
+    """gemm() for the batched prefill: activations a [M, K] times the weight
+    rows w [N, K]; small M takes split-K so that about `blocks` blocks run
+    (plain epilogues only)."""
+    M, K = a.shape
+    N = n if n is not None else w.shape[0]
+    k_slices = 1
+    if epilogue != EP_GATED:
+        tm = 64 if M <= 64 else 128
+        tiles = ((M + tm - 1) // tm) * ((N + tm - 1) // tm)
+        if tiles < blocks:
+            k_slices = max(1, min((blocks + tiles - 1) // tiles, K // 128, 16))
+    return gemm(a, w, out=out, epilogue=epilogue, pair_offset=pair_offset, n=N, k_slices=k_slices)

@@ -51,6 +51,15 @@ def test_generate_greedy_matches_oracle(setup):
     assert toks == list(gen_o[: N_DEC + 1])
 
 
+def test_stepwise_prefill_engine_matches_oracle(setup):
+    """prefill="stepwise" (the prompt fed one position at a time through the
+    decode kernels, "feed" then "head" graphs) gives the same greedy tokens."""
+    cfg, eng, prompt, gen_o = setup
+    eng2 = Engine(None, MAX_LEN, 1, 64, cfg=cfg, params=eng.params, device=DEV, prefill="stepwise")
+    toks = [e["token"] for e in eng2.generate(prompt.tolist(), max_new_tokens=9, temperature=0.0, stop_ids=())]
+    assert toks == list(gen_o[:9])
+
+
 def test_step_functions_calling_convention(setup):
     cfg, eng, prompt, gen_o = setup
     eng.reset_cache()
