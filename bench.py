@@ -23,6 +23,11 @@ Workloads (--workload):
              step (the 1.5 GB expert table is 6x the 256 MB Infinity Cache).
   copy       a 1 GiB device-to-device copy of known size: the calibration run
              for the HBM byte counters (FETCH_SIZE / WRITE_SIZE).
+  prefill    the batched prefill of the 26B-A4B-shaped model (seed 4) over
+             --prompt-len uniform-random tokens (2048 for the prefill +
+             batched-decode configuration); value = prompt tok/s, roofline =
+             the dense-MoE prefill block's useful TFLOP/s against 2.5 PFLOP/s.
+  gateup     the decode expert gate/up kernel alone (rocprofv3 counter runs).
 """
 
 from __future__ import annotations
@@ -415,7 +420,7 @@ def run_decode(args) -> dict:
             "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
             "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS,
             "kernels_per_token": 7 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token (Engine.decode_fn)",
-            "prefill": "Engine.prefill_fn: token-by-token decode kernels with the dense-MoE combine",
+            "prefill": "Engine.prefill_fn: batched (MFMA GEMMs, dense-MoE prefill, per-row attention)",
             "first_tokens": res["tokens"][:8],
         },
         "roofline": {
@@ -450,7 +455,101 @@ def run_gateup(args) -> dict:
     }
 
 
-WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup}
+def _prefill_flops(cfg, n: int) -> dict:
+    """Useful FLOPs of an n-token prefill (model.py:333-386 over n rows): the
+    projections, the dense MLP, the router, the selected experts' gate/up and
+    down, and causal attention (QK^T and PV over each row's attended range)."""
+    H, NH, I, F = cfg.hidden_size, cfg.num_attention_heads, cfg.intermediate_size, cfg.moe_intermediate_size
+    out = {"proj": 0.0, "dense_mlp": 0.0, "router": 0.0, "experts": 0.0, "attention": 0.0}
+    for lt in cfg.layer_types:
+        d, kv = cfg.head_dim_for(lt), cfg.kv_heads_for(lt)
+        rows = NH * d + kv * d * (1 if cfg.k_eq_v_for(lt) else 2)
+        out["proj"] += 2.0 * n * H * rows + 2.0 * n * NH * d * H
+        out["dense_mlp"] += 2.0 * n * H * 3 * I
+        if cfg.enable_moe_block:
+            out["router"] += 2.0 * n * H * cfg.num_experts
+            out["experts"] += 2.0 * n * cfg.top_k_experts * 3 * F * H
+        w = cfg.sliding_window if lt == "sliding_attention" else n
+        attended = sum(min(t + 1, w) for t in range(n))
+        out["attention"] += 2.0 * 2.0 * attended * NH * d
+    out["total"] = sum(out.values())
+    return out
+
+
+def run_prefill(args) -> dict:
+    """Prefill of the 26B-A4B-shaped model: --prompt-len uniform-random tokens
+    (seed 4) through Engine.prefill_fn (batched: MFMA GEMMs, the dense-MoE
+    prefill on the selected experts, per-row attention), first token sampled
+    greedily.  value = prompt tok/s."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi import ops
+    from gemma4_mi.config import gemma4_26b_a4b_config
+    from gemma4_mi.engine import PREFILL_BUCKET, Engine
+
+    cfg = gemma4_26b_a4b_config()
+    seed, n = 4, args.prompt_len
+    eng = Engine.random(cfg, seed=seed, max_len=args.max_len)
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab_size, size=n)
+    toks = torch.tensor(prompt, dtype=torch.int32)
+    bucket = max(PREFILL_BUCKET, ((n + PREFILL_BUCKET - 1) // PREFILL_BUCKET) * PREFILL_BUCKET)
+    fn = eng.prefill_fn(bucket)
+    for _ in range(max(1, args.warmup)):
+        tok, _, _ = fn(eng.params, toks, eng.cache, n, seed, 0.0, 1.0)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        tok, _, _ = fn(eng.params, toks, eng.cache, n, seed, 0.0, 1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    first = int(tok.item())
+    # the dense-MoE prefill block of one layer, HIP events around its launches
+    pr = eng._prefill_runner
+    lp = pr.layers[0]
+    xe, tw, ti = pr.xe[:n], pr.top_w[:n], pr.top_i[:n]
+    ops.moe_router_topk(xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],
+                        cfg.top_k_experts, cfg.rms_norm_eps, out=(tw, ti))
+    reps = 10
+    ops.moe_prefill(xe, tw, ti, lp["experts.gate_up_proj"], lp["experts.down_proj"], out=pr.moe_out[:n])
+    torch.cuda.synchronize()
+    e0.record()
+    for i in range(reps):
+        lq = pr.layers[i % cfg.num_hidden_layers]
+        ops.moe_prefill(xe, tw, ti, lq["experts.gate_up_proj"], lq["experts.down_proj"], out=pr.moe_out[:n])
+    e1.record()
+    torch.cuda.synchronize()
+    moe_us = e0.elapsed_time(e1) / reps * 1e3
+    fl = _prefill_flops(cfg, n)
+    moe_flops = fl["experts"] / cfg.num_hidden_layers
+    moe_tf = moe_flops / (moe_us * 1e-6) / 1e12
+    tfs = fl["total"] / (ms * 1e-3) / 1e12
+    return {
+        "metric": "prefill tok/s (batched prefill, MFMA GEMMs)",
+        "value": n / (ms * 1e-3),
+        "unit": "tok/s",
+        "ms_per_step": ms,
+        "dtype": "bf16",
+        "config": {
+            "workload": f"gemma4-26B-A4B-shaped random-init prefill of {n} tokens", "seed": seed,
+            "prompt_len": n, "bucket": bucket, "max_len": args.max_len, "first_token": first,
+            "useful_tflop": fl["total"] / 1e12, "useful_tflop_by_part": {k: v / 1e12 for k, v in fl.items()},
+            "useful_tflops_per_s": tfs, "useful_frac_of_bf16_peak": tfs / 2500.0,
+            "dense_moe_reference_tflop": 2.0 * n * cfg.num_experts * 3 * cfg.moe_intermediate_size
+            * cfg.hidden_size * cfg.num_hidden_layers / 1e12,
+        },
+        "roofline": {
+            "kernel": "moe_prefill (routing sort + grouped gate/up GEMM + grouped down GEMM + combine), one layer",
+            "bound": "mfma", "achieved": moe_tf, "peak": 2500.0, "unit": "TFLOP/s", "frac": moe_tf / 2500.0,
+            "traffic": None, "flops_per_launch": moe_flops, "avg_launch_us": moe_us,
+        },
+    }
+
+
+WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup,
+             "prefill": run_prefill}
 
 
 def main() -> int:
@@ -466,9 +565,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = 704 if args.workload == "decode" else 1000
+        args.steps = {"decode": 704, "prefill": 5}.get(args.workload, 1000)
     if args.warmup is None:
-        args.warmup = 64 if args.workload == "decode" else 100
+        args.warmup = {"decode": 64, "prefill": 1}.get(args.workload, 100)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (--gpus {args.gpus} refused)",
               file=sys.stderr)
