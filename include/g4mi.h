@@ -307,6 +307,23 @@ int g4mi_rows_tail(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* 
                    const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps, uint16_t* x_out,
                    uint16_t* xn_out, void* stream);
 
+/* Prefill attention (model.py:195-215 at T > 1).  q_norm_rope: q = rope(
+ * rms_norm(q, q_norm)) in place for T rows x NH heads at positions p0 + t
+ * (model.py:198-199; rope tables [rope_len, D/2] as for decode attention).
+ * prefill_attention: query row t (position p0 + t, q already normed and
+ * rotated) attends the cached keys [max(0, p0 + t + 1 - window), p0 + t]
+ * (window 0: all of [0, p0 + t]) -- the causal / sliding prefill mask of
+ * model.py:392-399 -- with scale 1.0, optional softcap, probabilities rounded
+ * to bf16 after normalisation; ctx [T, NH, D] bf16.  Two passes over the
+ * keys on MFMA; page_size a multiple of 64; K/V of the T rows must already
+ * be in the cache (g4mi_kv_append). */
+int g4mi_q_norm_rope(uint16_t* q, const uint16_t* q_norm, const uint16_t* rope_cos, const uint16_t* rope_sin,
+                     int64_t T, int64_t NH, int64_t D, int64_t p0, int64_t rope_len, float eps, void* stream);
+int g4mi_prefill_attention(const uint16_t* q, const uint16_t* k_pages, const uint16_t* v_pages, int64_t num_pages,
+                           const int32_t* page_table, int64_t max_pages, int64_t page_size, int64_t T, int64_t p0,
+                           int64_t NH, int64_t KV, int64_t D, int64_t window, float softcap, uint16_t* ctx,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

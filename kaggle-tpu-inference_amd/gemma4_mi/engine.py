@@ -21,8 +21,8 @@ so `lookahead` steps stay queued while it reads the oldest one.
 
 Prefill (the default, prefill="batched") runs every prompt row through the
 layers at once (model.PrefillRunner: MFMA GEMMs for the projections and the
-dense-MoE experts, the decode attention kernels with one query row per
-sequence), then the head on the last row.  prefill="stepwise" instead feeds
+dense-MoE experts, MFMA flash attention over the prompt rows), then the
+head on the last row.  prefill="stepwise" instead feeds
 the prompt one position at a time through the decode kernels with the
 dense-MoE combine ("feed" graph, then "head").  Either way each prompt row
 attends exactly the cached positions <= its own, the reference's causal

@@ -321,9 +321,10 @@ class PrefillRunner:
       q/k/v = xn . W^T                  MFMA GEMMs (model.py:197-201)
       kv_append                         k = rope(rms(k_raw)), v = rms(v_raw)
                                         written at positions 0..n-1 (model.py:202-206)
-      decode_attention, append off      query row t attends [max(0, t+1-W), t]:
-                                        the causal / sliding prefill mask of
-                                        model.py:392-399 restricted to real rows
+      q_norm_rope + prefill_attention   MFMA flash attention, query row t attends
+                                        [max(0, t+1-W), t]: the causal / sliding
+                                        prefill mask of model.py:392-399 on the
+                                        real rows
       o = ctx . o_proj^T                MFMA GEMM (model.py:214)
       rows_post_attn                    x1, xm, xe (model.py:301-315)
       act = gelu(xm.g) * (xm.u)         MFMA GEMM, gated epilogue (model.py:218-220)
@@ -333,11 +334,9 @@ class PrefillRunner:
 
     The first layer starts from rows_embed.  Rows beyond the prompt (the
     reference's bucket padding) are not computed: the reference never attends
-    them and reads back only the last prompt row.  Attention runs in chunks
-    of `qchunk` query rows so its workspace stays bounded."""
+    them and reads back only the last prompt row."""
 
-    def __init__(self, cfg: TextConfig, params: dict, cache: dict, capacity: int, device="cuda", qchunk: int = 256,
-                 rope=None):
+    def __init__(self, cfg: TextConfig, params: dict, cache: dict, capacity: int, device="cuda", rope=None):
         from . import ops
 
         self.ops, self.cfg, self.params, self.cache = ops, cfg, params, cache
@@ -346,7 +345,6 @@ class PrefillRunner:
         self.max_len = cache["max_len"]
         if not 1 <= cap <= self.max_len:
             raise ValueError(f"prefill capacity {cap} outside [1, {self.max_len}]")
-        self.qchunk = qchunk
         self.layers = [{k[len(f"layers.{i}."):]: v for k, v in params.items() if k.startswith(f"layers.{i}.")}
                        for i in range(cfg.num_hidden_layers)]
         H, bf = cfg.hidden_size, torch.bfloat16
@@ -366,21 +364,11 @@ class PrefillRunner:
             self.top_i = z(cap, cfg.top_k_experts, dt=torch.int32)
         self.pos = torch.arange(cap, dtype=torch.int32, device=dev)
         self.page_row = cache["page_table"][0].contiguous()
-        self.pt_rep = cache["page_table"][0:1].expand(qchunk, -1).contiguous()
         self.rope = rope if rope is not None else {
             SLIDING: rope_table(cfg.head_dim, cfg.rope_theta_sliding, 1.0, self.max_len, dev),
             FULL: rope_table(cfg.global_head_dim, cfg.rope_theta_full, cfg.rope_partial_rotary_factor_full,
                              self.max_len, dev),
         }
-        # attention over positions < capacity: lmax = capacity (rounded to pages)
-        page = cache["k"][0].shape[2]
-        self.lmax = min(self.max_len, ((cap + page - 1) // page) * page)
-        self.splits = max(1, ops.attention_min_splits(self.lmax))
-        ws = 0
-        for lt in set(cfg.layer_types):
-            ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(
-                qchunk, cfg.num_attention_heads, cfg.head_dim_for(lt), self.lmax, self.splits))
-        self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
 
     def run(self, tokens: torch.Tensor, n: int) -> None:
         """Runs the layers for tokens[:n] (device int32) on the current stream."""
@@ -411,13 +399,9 @@ class PrefillRunner:
                           self.cache["k"][i], self.cache["v"][i], self.page_row, pos, self.max_len, eps)
             ctx = self.ctx[: n * NH * d].view(n, NH, d)
             window = cfg.sliding_window if lt == SLIDING else 0
-            for c0 in range(0, n, self.qchunk):
-                c1 = min(n, c0 + self.qchunk)
-                b = c1 - c0
-                ops.decode_attention(q.view(n, NH, d)[c0:c1], k.view(n, kv, d)[c0:c1], None, lp["q_norm"],
-                                     lp["k_norm"], cos, sin, self.cache["k"][i], self.cache["v"][i],
-                                     self.pt_rep[:b], self.pos[c0:c1], window, cfg.attn_logit_softcapping, eps,
-                                     self.lmax, self.splits, append=False, ctx=ctx[c0:c1], ws=self.attn_ws)
+            qh = ops.q_norm_rope(q.view(n, NH, d), lp["q_norm"], cos, sin, 0, eps)
+            ops.prefill_attention(qh, self.cache["k"][i], self.cache["v"][i], self.page_row, 0, window,
+                                  cfg.attn_logit_softcapping, ctx=ctx)
             ops.prefill_gemm(ctx.view(n, NH * d), lp["o_proj"].reshape(H, NH * d), o)
             ops.rows_post_attn(x, o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
                                lp.get("pre_feedforward_layernorm_2"), eps, x1, xm, xe)

@@ -539,3 +539,35 @@ def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256)
         if tiles < blocks:
             k_slices = max(1, min((blocks + tiles - 1) // tiles, K // 128, 16))
     return gemm(a, w, out=out, epilogue=epilogue, pair_offset=pair_offset, n=N, k_slices=k_slices)
+
+
+def q_norm_rope(q, q_norm, rope_cos, rope_sin, p0, eps):
+    """q [T, NH, D] = rope(rms_norm(q, q_norm)) in place at positions p0 + t
+    (model.py:198-199)."""
+    T, NH, D = q.shape
+    _need(q, BF16, "q")
+    _need(q_norm, BF16, "q_norm", (D,))
+    _lib.call("g4mi_q_norm_rope", _ptr(q), _ptr(q_norm), _ptr(rope_cos), _ptr(rope_sin), T, NH, D, int(p0),
+              rope_cos.shape[0], float(eps), stream_handle(q.device))
+    return q
+
+
+def prefill_attention(q, k_pages, v_pages, page_table_row, p0, window, softcap, ctx=None):
+    """Causal prefill attention of T query rows q [T, NH, D] (normed and
+    rotated, positions p0 + t) over the paged cache (model.py:207-213, T > 1).
+    Returns ctx [T, NH, D] bf16."""
+    T, NH, D = q.shape
+    num_pages, KV, page, D2 = k_pages.shape
+    if D2 != D:
+        raise ValueError("head_dim mismatch between q and the cache")
+    _need(q, BF16, "q")
+    _need(k_pages, BF16, "k_pages")
+    _need(v_pages, BF16, "v_pages", tuple(k_pages.shape))
+    _need(page_table_row, torch.int32, "page_table_row")
+    if ctx is None:
+        ctx = torch.empty((T, NH, D), dtype=BF16, device=q.device)
+    _need(ctx, BF16, "ctx", (T, NH, D))
+    _lib.call("g4mi_prefill_attention", _ptr(q), _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table_row),
+              page_table_row.numel(), page, T, int(p0), NH, KV, D, int(window), float(softcap or 0.0), _ptr(ctx),
+              stream_handle(q.device))
+    return ctx

@@ -99,8 +99,8 @@ def test_prefill_and_teacher_forced_decode(c1):
 
 
 def test_batched_prefill_matches_oracle(c1):
-    """PrefillRunner (MFMA GEMMs, dense-MoE prefill, one attention query row
-    per prompt token, chunked 48 rows at a time) then the head: the
+    """PrefillRunner (MFMA GEMMs, dense-MoE prefill, MFMA prefill attention)
+    then the head: the
     first-token logits against the oracle's last prefill row (same bar as
     above), and the K/V cache of every layer against the oracle's prefill
     cache: corr >= 0.9999 and >= 99% of elements bit-identical (the GPU GEMMs
@@ -112,7 +112,7 @@ def test_batched_prefill_matches_oracle(c1):
     cfg, params_cpu, params, prompt, logits_o, gen_o, _ = c1
     cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
     r = gm.DecodeRunner(cfg, params, cache, device=DEV)
-    pr = gm.PrefillRunner(cfg, params, cache, P, device=DEV, qchunk=48, rope=r.rope)
+    pr = gm.PrefillRunner(cfg, params, cache, P, device=DEV, rope=r.rope)
     toks = torch.tensor(prompt, dtype=torch.int32, device=DEV)
     pr.run(toks, P)
     r.pos.fill_(P - 1)
