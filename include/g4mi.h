@@ -267,7 +267,7 @@ int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* param
  * max_tiles, m1 - m0 <= 64) each tile uses B + group * b_group_stride: the
  * grouped per-expert GEMM.  k_slices > 1 splits K over blocks (plain
  * epilogues 0/1 only) with a workspace of g4mi_gemm_workspace_bytes.
- * K % 32 == 0; rows 16-byte aligned.  No reference counterpart: XLA's dot. */
+ * K % 64 == 0; rows 16-byte aligned.  No reference counterpart: XLA's dot. */
 int64_t g4mi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t k_slices);
 int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
                    int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
@@ -281,7 +281,7 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
  * of one f32 sum over the selected experts.  Unselected experts contribute
  * exact zeros in the reference (masked weights), so only the selected
  * (token, expert) pairs are computed, as grouped MFMA GEMMs.  n <= 65535,
- * E <= 256, K <= 32, H and F multiples of 32. */
+ * E <= 256, K <= 32, H and F multiples of 64. */
 int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_t F, int64_t H);
 int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
                      const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,

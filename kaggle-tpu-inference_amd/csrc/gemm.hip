@@ -25,6 +25,8 @@
 //    model.py:246-247 and 269-271 with the routing weight w_row of the row).
 #include <stdlib.h>
 
+#include <type_traits>
+
 #include "capi_util.h"
 #include "common.h"
 
@@ -54,16 +56,17 @@ struct GemmArgs {
   float* partial;           // [k_slices, M, N] f32
 };
 
-constexpr int kBK = 32;
-constexpr int kPad = 8;  // LDS row padding (elements): rows of 80 bytes
+constexpr int kBK = 64;  // K per pipeline step
+constexpr int kPad = 8;  // LDS row padding (elements): rows of 144 bytes
 
 template <int BM, int BN, int EP>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
   constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
   constexpr int FM = WM / 16, FN = WN / 16; // MFMA fragments per wave
   constexpr int LDT = kBK + kPad;
-  constexpr int ACH = BM * kBK / 8 / 256;   // 16-byte A chunks per thread per step
-  constexpr int BCH = BN * kBK / 8 / 256;
+  constexpr int CPR = kBK / 8;              // 16-byte chunks per tile row
+  constexpr int ACH = BM * CPR / 256;       // A chunks per thread per step
+  constexpr int BCH = BN * CPR / 256;
   static_assert(ACH >= 1 && BCH >= 1, "tile too small for 256 threads");
   // one LDS block: the double-buffered A and B tiles, reused by the gated
   // epilogue's exchange
@@ -98,8 +101,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   int adst[ACH], bdst[BCH];
 #pragma unroll
   for (int q = 0; q < ACH; ++q) {
-    const int c = tid + 256 * q;  // chunk: row c/4, 8 elements at (c%4)*8
-    const int r = c >> 2, kc = (c & 3) * 8;
+    const int c = tid + 256 * q;  // chunk: row c/CPR, 8 elements at (c%CPR)*8
+    const int r = c / CPR, kc = (c % CPR) * 8;
     const int m = min(m0 + r, max(m1 - 1, m0));
     const int src = (g.a_rows != nullptr) ? g.a_rows[m] : m;
     asrc[q] = (const u32x4*)(g.a + (size_t)src * g.lda + kc);
@@ -108,7 +111,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
   for (int q = 0; q < BCH; ++q) {
     const int c = tid + 256 * q;
-    const int r = c >> 2, kc = (c & 3) * 8;
+    const int r = c / CPR, kc = (c % CPR) * 8;
     const uint16_t* row;
     if constexpr (EP == kEpGated) {
       const int half = r >= BN / 2;
@@ -128,34 +131,34 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  u32x4 ra[ACH], rb[BCH];
-  auto gload = [&](int ks) {
+  // Pipeline: tile j's global loads go to register stage j%2 two steps
+  // before it is multiplied; at step k the block multiplies LDS buffer k%2,
+  // stores register stage (k+1)%2 (tile k+1) into the other buffer and has
+  // tile k+2's loads in flight, so two steps of MFMA work cover each load.
+  u32x4 ra[2][ACH], rb[2][BCH];
+  auto gload = [&](int ks, u32x4* a_, u32x4* b_) {
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) ra[q] = ld16(asrc[q] + ks * (kBK / 8));
+    for (int q = 0; q < ACH; ++q) a_[q] = ld16(asrc[q] + ks * CPR);
 #pragma unroll
-    for (int q = 0; q < BCH; ++q) rb[q] = ld_stream(bsrc[q] + ks * (kBK / 8));
+    for (int q = 0; q < BCH; ++q) b_[q] = ld_stream(bsrc[q] + ks * CPR);
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const u32x4* a_, const u32x4* b_) {
 #pragma unroll
-    for (int q = 0; q < ACH; ++q) *(u32x4*)(smem + buf * BM * LDT + adst[q]) = ra[q];
+    for (int q = 0; q < ACH; ++q) *(u32x4*)(smem + buf * BM * LDT + adst[q]) = a_[q];
 #pragma unroll
-    for (int q = 0; q < BCH; ++q) *(u32x4*)(smem + SB0 + buf * BN * LDT + bdst[q]) = rb[q];
+    for (int q = 0; q < BCH; ++q) *(u32x4*)(smem + SB0 + buf * BN * LDT + bdst[q]) = b_[q];
   };
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  if (ks0 < ks1) {
-    gload(ks0);
-    lstore(0);
-    __syncthreads();
-    int buf = 0;
-    for (int ks = ks0; ks < ks1; ++ks) {
-      const bool more = ks + 1 < ks1;
-      if (more) gload(ks + 1);
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int kk = 0; kk < kBK / 32; ++kk) {
       u32x4 af[FM], bf[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = *(const u32x4*)(smem + buf * BM * LDT + (wm * WM + i * 16 + fr) * LDT + fk);
+      for (int i = 0; i < FM; ++i)
+        af[i] = *(const u32x4*)(smem + buf * BM * LDT + (wm * WM + i * 16 + fr) * LDT + 32 * kk + fk);
 #pragma unroll
       for (int j = 0; j < FN; ++j)
-        bf[j] = *(const u32x4*)(smem + SB0 + buf * BN * LDT + (wn * WN + j * 16 + fr) * LDT + fk);
+        bf[j] = *(const u32x4*)(smem + SB0 + buf * BN * LDT + (wn * WN + j * 16 + fr) * LDT + 32 * kk + fk);
 #pragma unroll
       for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -163,12 +166,27 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
                                                               __builtin_bit_cast(bf16x8, bf[j]), acc[i][j], 0, 0,
                                                               0);
-      if (more) {
-        lstore(buf ^ 1);
-        __syncthreads();
-        buf ^= 1;
-      }
     }
+  };
+  // one pipeline step on buffer BUF (register stages are compile-time)
+  auto step = [&](int ks, auto bufc) {
+    constexpr int BUF = decltype(bufc)::value;
+    if (ks + 2 < ks1) gload(ks + 2, ra[BUF], rb[BUF]);
+    compute(BUF);
+    if (ks + 1 < ks1) lstore(BUF ^ 1, ra[BUF ^ 1], rb[BUF ^ 1]);
+    __syncthreads();
+  };
+  if (ks0 < ks1) {
+    gload(ks0, ra[0], rb[0]);
+    if (ks0 + 1 < ks1) gload(ks0 + 1, ra[1], rb[1]);
+    lstore(0, ra[0], rb[0]);
+    __syncthreads();
+    int ks = ks0;
+    for (; ks + 1 < ks1; ks += 2) {
+      step(ks, std::integral_constant<int, 0>{});
+      step(ks + 1, std::integral_constant<int, 1>{});
+    }
+    if (ks < ks1) step(ks, std::integral_constant<int, 0>{});
   }
 
   // ---- epilogue.  Fragment (i, j), register q: row wm*WM + 16i + 4(l/16) + q,

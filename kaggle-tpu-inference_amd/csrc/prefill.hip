@@ -230,7 +230,7 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
   G4MI_REQUIRE(xn && top_w && top_i && gate_up && down && out && ws, G4MI_EINVAL, "moe_prefill: missing argument");
   G4MI_REQUIRE(n >= 1 && n <= 65535 && K >= 1 && K <= 32 && E >= 1 && E <= kMaxExperts, G4MI_EINVAL,
                "moe_prefill: bad n/K/E");
-  G4MI_REQUIRE(H % 32 == 0 && F % 32 == 0, G4MI_EUNSUPPORTED, "moe_prefill: H and F must be multiples of 32");
+  G4MI_REQUIRE(H % 64 == 0 && F % 64 == 0, G4MI_EUNSUPPORTED, "moe_prefill: H and F must be multiples of 64");
   G4MI_REQUIRE(ws_bytes >= g4mi_moe_prefill_workspace_bytes(n, K, E, F, H), G4MI_EWORKSPACE,
                "moe_prefill: workspace too small");
   hipStream_t st = as_stream(stream);
