@@ -264,7 +264,7 @@ int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* param
  * and the up rows at B + pair_offset, C[m, n] = bf16(bf16(bf16(gelu(bf16(g)))
  * * bf16(u)) * bf16(row_scale[m])) (model.py:220, 246-247; row_scale may be
  * NULL).  With tiles (device int32 triples (group, m0, m1), count *ntiles <=
- * max_tiles, m1 - m0 <= 64) each tile uses B + group * b_group_stride: the
+ * max_tiles, m1 - m0 <= 128) each tile uses B + group * b_group_stride: the
  * grouped per-expert GEMM.  k_slices > 1 splits K over blocks (plain
  * epilogues 0/1 only) with a workspace of g4mi_gemm_workspace_bytes.
  * K % 64 == 0; rows 16-byte aligned.  No reference counterpart: XLA's dot. */

@@ -306,8 +306,8 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   g.ntiles = ntiles; g.c = c; g.ldc = ldc; g.row_scale = row_scale; g.k_slices = (int)k_slices;
   g.partial = (float*)ws;
   hipStream_t st = as_stream(stream);
-  // grouped tiles are 64 rows; small plain M takes 64-row tiles too
-  const bool small = tiles != nullptr || M <= 64;
+  // grouped tiles are up to 128 rows (128-row kernels); small plain M takes 64-row tiles
+  const bool small = tiles == nullptr && M <= 64;
   const int64_t mtiles = tiles ? max_tiles : (M + (small ? 63 : 127)) / (small ? 64 : 128);
   G4MI_REQUIRE(mtiles <= 2147483647, G4MI_EINVAL, "gemm: too many tiles");
   if (small) {

@@ -273,10 +273,96 @@ static float bf16_inv_sqrt(int64_t H) {
   return r;
 }
 
+// Many rows (prefill): a block takes kRouterRows token rows and every
+// expert, so each router row is read once per kRouterRows tokens instead of
+// once per token.  Wave w normalises rows 2w and 2w+1 into LDS (wave-level f64
+// reductions, the same rounding steps as router_scores_kernel), then thread t
+// accumulates in f64 the dots of expert e0 + t % 128 with rows 4*(t/128) ..
+// +3, reading the expert's router row 128 bytes at a time.  H <= 4096 (the
+// rows fit 64 KB of LDS).
+constexpr int kRouterRows = 8;
+__global__ __launch_bounds__(256) void router_scores_tile_kernel(const uint16_t* __restrict__ x,
+                                                                 const uint16_t* __restrict__ pre_w,
+                                                                 const uint16_t* __restrict__ scale,
+                                                                 const uint16_t* __restrict__ proj, int N, int H,
+                                                                 int E, float eps, float inv_sqrt_h_bf,
+                                                                 float* __restrict__ scores) {
+  extern __shared__ u32x4 xs_rows[];  // kRouterRows x H/8 chunks
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int CH = H / 8;
+  const int r0 = blockIdx.x * kRouterRows;
+  const u32x4* pw = (const u32x4*)pre_w;
+  const u32x4* sw = (const u32x4*)scale;
+  for (int rr = 0; rr < 2; ++rr) {
+    const int r = wave * 2 + rr;
+    const u32x4* xr = (const u32x4*)(x + (size_t)min(r0 + r, N - 1) * H);
+    float rp = 1.0f;
+    if (pre_w != nullptr) {  // pre_feedforward_layernorm_2 (model.py:315)
+      double s0 = 0.0;
+      for (int c8 = lane; c8 < CH; c8 += 64) s0 = sumsq8_f64(ld16(xr + c8), s0);
+      rp = rms_scale(group_sum_f64<64>(s0), H, eps);
+    }
+    double s1 = 0.0;
+    for (int c8 = lane; c8 < CH; c8 += 64) {
+      u32x4 v = ld16(xr + c8);
+      if (pre_w != nullptr) {
+        const u32x4 wc = ld16(pw + c8);
+        v = scale8(v, rp, &wc);
+      }
+      s1 = sumsq8_f64(v, s1);
+    }
+    const float r1 = rms_scale(group_sum_f64<64>(s1), H, eps);
+    for (int c8 = lane; c8 < CH; c8 += 64) {
+      u32x4 v = ld16(xr + c8);
+      if (pre_w != nullptr) {
+        const u32x4 wc = ld16(pw + c8);
+        v = scale8(v, rp, &wc);
+      }
+      const u32x4 sc = ld16(sw + c8);
+      float f[8], g[8];
+      unpack8(v, f);
+      unpack8(sc, g);
+#pragma unroll
+      for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r1) * g[q]) * inv_sqrt_h_bf);
+      u32x4 o;
+      o.x = pack2(f[0], f[1]); o.y = pack2(f[2], f[3]); o.z = pack2(f[4], f[5]); o.w = pack2(f[6], f[7]);
+      xs_rows[r * CH + c8] = o;
+    }
+  }
+  __syncthreads();
+  const int rg = tid >> 7;
+  for (int e0 = 0; e0 < E; e0 += 128) {
+    const int e = e0 + (tid & 127);
+    if (e >= E) continue;
+    const u32x4* wrow = (const u32x4*)(proj + (size_t)e * H);
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (int c0 = 0; c0 < CH; c0 += 8) {  // CH % 8 == 0 on this path
+      u32x4 w[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) w[u] = ld16(wrow + c0 + u);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[q] = dot8_f64(w[u], xs_rows[(4 * rg + q) * CH + c0 + u], acc[q]);
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int n = r0 + 4 * rg + q;
+      if (n < N) scores[(size_t)n * E + e] = rbf(f32_of(acc[q]));
+    }
+  }
+}
+
 static void launch_scores(const uint16_t* x, const uint16_t* pre_w, const uint16_t* scale, const uint16_t* proj,
                           int N, int H, int E, float eps, float* scores, hipStream_t st) {
   dim3 grid((unsigned)((E + 7) / 8), (unsigned)N);
   const float c = bf16_inv_sqrt(H);
+  if (N >= 32 && H % 64 == 0 && H <= 4096 && ((uintptr_t)scale & 15u) == 0 && ((uintptr_t)pre_w & 15u) == 0) {
+    const size_t lds = (size_t)kRouterRows * (H / 8) * 16;
+    hipLaunchKernelGGL(router_scores_tile_kernel, dim3((unsigned)((N + kRouterRows - 1) / kRouterRows)), dim3(256),
+                       lds, st, x, pre_w, scale, proj, N, H, E, eps, c, scores);
+    return;
+  }
   const bool aligned = ((uintptr_t)scale & 15u) == 0 && ((uintptr_t)pre_w & 15u) == 0;
   if (H % 256 == 0 && H / 256 <= 16 && aligned) {
     switch (H / 256) {

@@ -8,7 +8,8 @@
 // the selected (token, expert) pairs as grouped GEMMs, 16x fewer FLOPs at
 // E = 128, k = 8, with the same rounding points:
 //   1. moe_sort_kernel: tokens grouped by expert (counts, offsets, a gather
-//      list, the per-slot routing weight) and 64-row GEMM tiles per expert;
+//      list, the per-slot routing weight) and 128-row GEMM tiles per expert
+//      (one tile covers an expert's rows up to 128, so its weights stream once);
 //   2. gate/up GEMM over the gathered rows with the gated epilogue:
 //      act = bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w))   (model.py:246-247);
 //   3. down GEMM, f32 output per (token, expert);
@@ -29,13 +30,13 @@ extern "C" int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_r
 
 namespace g4mi {
 
-constexpr int kTileRows = 64;  // grouped GEMM tile height (gemm.hip's small tiles)
+constexpr int kTileRows = 128;  // grouped GEMM tile height (gemm.hip's grouped tiles)
 constexpr int kMaxExperts = 256;
 
 // One block.  entries i = t*K + s (token t, slot s) of the routing.
 //   sorted position p of entry i: offsets[e] + (rank among entries of expert e)
 //   a_rows[p] = t, w_sorted[p] = top_w[i], slot_pos[i] = p (-1: invalid expert)
-//   tiles: (e, m0, m1) for every 64 rows of every expert, ntiles[0] = count.
+//   tiles: (e, m0, m1) for every kTileRows rows of every expert, ntiles[0] = count.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ top_i,
                                                         const float* __restrict__ top_w, int n, int K, int E,
                                                         int32_t* __restrict__ a_rows, float* __restrict__ w_sorted,
