@@ -19,12 +19,17 @@ struct VecT {
 };
 using Vec = VecT<256>;
 
+// Branch-free: every lane loads (a clamped chunk past the end) and zeroes
+// afterwards.  A load under a branch makes the compiler's s_waitcnt placement
+// conservative: it then waits for loads issued after the vector (the weight
+// rows) before using it.
 template <int NT>
 __device__ __forceinline__ void vload(VecT<NT>& v, const uint16_t* __restrict__ p, int nch) {
 #pragma unroll
   for (int j = 0; j < VecT<NT>::NC; ++j) {
     const int c = threadIdx.x + NT * j;
-    v.c[j] = (c < nch) ? ld16((const u32x4*)p + c) : u32x4{0u, 0u, 0u, 0u};
+    const u32x4 t = ld16((const u32x4*)p + min(c, nch - 1));
+    v.c[j] = (c < nch) ? t : u32x4{0u, 0u, 0u, 0u};
   }
 }
 // vload of a vector other blocks of this kernel wrote with coherent stores
@@ -153,16 +158,17 @@ struct TailRegs {
   VecT<NT> a, b, x1, w1, w2, w3;
   uint16_t ls;
 };
+// Unconditional loads (see vload): without the MoE block the MoE operands
+// are read from the dense ones and ignored.
 template <int NT>
 __device__ __forceinline__ void tail_load(TailRegs<NT>& T, const TailArgs& t, int nch) {
+  const bool moe = t.moe != nullptr;
   vload(T.a, t.mlp, nch);
   vload(T.x1, t.x1, nch);
   vload(T.w3, t.w_pf, nch);
-  if (t.moe != nullptr) {
-    vload(T.b, t.moe, nch);
-    vload(T.w1, t.w_pf1, nch);
-    vload(T.w2, t.w_pf2, nch);
-  }
+  vload(T.b, moe ? t.moe : t.mlp, nch);
+  vload(T.w1, moe ? t.w_pf1 : t.w_pf, nch);
+  vload(T.w2, moe ? t.w_pf2 : t.w_pf, nch);
   T.ls = t.ls[0];
 }
 template <int NT>
