@@ -28,6 +28,10 @@ Workloads (--workload):
              batched-decode configuration); value = prompt tok/s, roofline =
              the dense-MoE prefill block's useful TFLOP/s against 2.5 PFLOP/s.
   gateup     the decode expert gate/up kernel alone (rocprofv3 counter runs).
+  batch_decode  batched greedy decode (seed 4): --batch sequences (default
+             8) at --prompt-len positions each (8192 for the prefill +
+             batched-decode configuration), --steps batched steps; value =
+             aggregate tok/s.
 """
 
 from __future__ import annotations
@@ -548,8 +552,74 @@ def run_prefill(args) -> dict:
     }
 
 
+def run_batch_decode(args) -> dict:
+    """Batched greedy decode of the 26B-A4B-shaped model (seed 4): --batch
+    sequences (8 by default) each prefilled with --prompt-len (default 8192)
+    uniform-random tokens, then --steps batched steps (gemma4_mi.batch).
+    value = aggregate tok/s (batch / step time)."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi.batch import BatchEngine
+    from gemma4_mi.config import gemma4_26b_a4b_config
+    from gemma4_mi.weights import active_params_per_token, init_random_params
+
+    cfg = gemma4_26b_a4b_config()
+    seed, B, ctx = 4, (args.batch if args.batch > 1 else 8), args.prompt_len
+    max_len = ctx + args.warmup + args.steps + 64
+    params = init_random_params(cfg, seed, device="cuda:0")
+    eng = BatchEngine(cfg, params, batch=B, max_len=max_len, device="cuda:0")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for b in range(B):
+        eng.add(b, np.random.default_rng(seed + b).integers(0, cfg.vocab_size, size=ctx).tolist())
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    _log(f"{B} sequences prefilled ({ctx} tokens each) in {prefill_s:.2f}s")
+    for _ in range(args.warmup):
+        eng.step()
+    torch.cuda.synchronize()
+    p0 = eng.pos_host[0]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        eng.step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    p1 = eng.pos_host[0]
+    # algorithmic bytes per step: shared weights once, the union of the routed experts per layer (expected
+    # value under uniform routing), and each sequence's window-clamped K/V
+    H, E, K, F, L = (cfg.hidden_size, cfg.num_experts, cfg.top_k_experts, cfg.moe_intermediate_size,
+                     cfg.num_hidden_layers)
+    expert_bytes = 3 * F * H * 2
+    shared = 2 * active_params_per_token(cfg) - L * K * expert_bytes
+    union = E * (1.0 - (1.0 - K / E) ** B)
+    pos_mid = (p0 + p1) // 2
+    kv = 0
+    for lt in cfg.layer_types:
+        n = pos_mid + 1 if lt != "sliding_attention" else min(pos_mid + 1, cfg.sliding_window)
+        kv += 2 * 2 * cfg.kv_heads_for(lt) * cfg.head_dim_for(lt) * n
+    step_bytes = shared + L * union * expert_bytes + B * kv
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    return {
+        "metric": "batched decode aggregate tok/s",
+        "value": B / (ms * 1e-3),
+        "unit": "tok/s",
+        "ms_per_step": ms,
+        "dtype": "bf16",
+        "config": {
+            "workload": f"gemma4-26B-A4B-shaped random-init batched greedy decode, {B} sequences at ~{ctx} positions",
+            "seed": seed, "batch": B, "context": ctx, "positions_timed": [p0, p1], "prefill_s": prefill_s,
+            "step_bytes": step_bytes, "expected_union_experts_per_layer": union,
+        },
+        "roofline": {"kernel": "whole batched decode step", "bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS, "traffic": None},
+    }
+
+
 WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup,
-             "prefill": run_prefill}
+             "prefill": run_prefill, "batch_decode": run_batch_decode}
 
 
 def main() -> int:
@@ -565,9 +635,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.steps is None:
-        args.steps = {"decode": 704, "prefill": 5}.get(args.workload, 1000)
+        args.steps = {"decode": 704, "prefill": 5, "batch_decode": 256}.get(args.workload, 1000)
     if args.warmup is None:
-        args.warmup = {"decode": 64, "prefill": 1}.get(args.workload, 100)
+        args.warmup = {"decode": 64, "prefill": 1, "batch_decode": 8}.get(args.workload, 100)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (--gpus {args.gpus} refused)",
               file=sys.stderr)

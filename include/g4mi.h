@@ -324,6 +324,14 @@ int g4mi_prefill_attention(const uint16_t* q, const uint16_t* k_pages, const uin
                            int64_t NH, int64_t KV, int64_t D, int64_t window, float softcap, uint16_t* ctx,
                            void* stream);
 
+/* Batched greedy head (model.py:381-385, 416 for B sequences): logits [B, V]
+ * bf16 (x . embed^T, e.g. from g4mi_gemm_bf16) -> softcap in f32 (softcap 0:
+ * off), optional f32 copy [B, V], first index of the maximum per row; tok[b] =
+ * it, pos[b] += 1 and hist[b * hist_len + pos[b]] = it when pos / hist are
+ * given. */
+int g4mi_argmax_rows(const uint16_t* logits, int64_t B, int64_t V, float softcap, float* logits_f32, int32_t* tok,
+                     int32_t* pos, int32_t* hist, int64_t hist_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -163,7 +163,71 @@ static int64_t stage_keys(int64_t n) { return ((n + kSortN - 1) / kSortN) * kKee
 
 using namespace g4mi;
 
+// ------------------------------------------------------------------ batched head
+// One block per sequence row b of bf16 logits [B, V] (x . embed^T rounded to
+// bf16, model.py:381): v = f32 logit, softcap c*tanh(v/c) when c > 0
+// (model.py:382-385), optional f32 copy, then the first index of the maximum
+// (model.py:416 greedy): tok[b] = it; pos[b] += 1; hist[b][pos[b]] = it.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t* __restrict__ logits, int V, float cap,
+                                                           float* __restrict__ out_f32, int32_t* tok, int32_t* pos,
+                                                           int32_t* hist, int hist_len) {
+  __shared__ float vs[32];
+  __shared__ int is[32];
+  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint16_t* row = logits + (size_t)b * V;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int j = tid; j < V; j += 1024) {
+    float v = bf2f(row[j]);
+    if (cap > 0.0f) v = tanhf(v / cap) * cap;
+    if (out_f32 != nullptr) out_f32[(size_t)b * V + j] = v;
+    if (v > bv) {  // j increases: strict > keeps the first index of a tie
+      bv = v;
+      bi = j;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(bv, m, kWave);
+    const int oi = __shfl_xor(bi, m, kWave);
+    if (ov > bv || (ov == bv && oi < bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if (lane == 0) {
+    vs[wave] = bv;
+    is[wave] = bi;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; ++w)
+      if (vs[w] > bv || (vs[w] == bv && is[w] < bi)) {
+        bv = vs[w];
+        bi = is[w];
+      }
+    bi = (bi == 0x7fffffff) ? 0 : bi;
+    tok[b] = bi;
+    if (pos != nullptr) {
+      const int p = pos[b] + 1;
+      pos[b] = p;
+      if (hist != nullptr && p >= 0 && p < hist_len) hist[(size_t)b * hist_len + p] = bi;
+    }
+  }
+}
+
 extern "C" {
+
+int g4mi_argmax_rows(const uint16_t* logits, int64_t B, int64_t V, float softcap, float* logits_f32, int32_t* tok,
+                     int32_t* pos, int32_t* hist, int64_t hist_len, void* stream) {
+  G4MI_REQUIRE(logits && tok && B >= 1 && B <= 65535 && V >= 1 && V <= 2147483647, G4MI_EINVAL,
+               "argmax_rows: bad arguments (B=%lld V=%lld)", (long long)B, (long long)V);
+  G4MI_REQUIRE(hist == nullptr || (pos && hist_len >= 1), G4MI_EINVAL, "argmax_rows: hist needs pos and hist_len");
+  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)B), dim3(1024), 0, as_stream(stream), logits, (int)V, softcap,
+                     logits_f32, tok, pos, hist, (int)hist_len);
+  return check_launch("argmax_rows");
+}
+
 
 int64_t g4mi_sample_workspace_bytes(int64_t V) {
   const int64_t a = stage_keys(V);

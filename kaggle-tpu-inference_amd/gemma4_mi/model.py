@@ -97,21 +97,28 @@ PAGE_SIZE = 64
 
 
 def init_cache(cfg: TextConfig, mesh=None, batch: int = 1, max_len: int = 4096, dtype=torch.bfloat16,
-               device="cuda", page_size: int = PAGE_SIZE) -> dict:
+               device="cuda", page_size: int = PAGE_SIZE, num_pages: int | None = None) -> dict:
     """Zero K and V caches, one pair per layer (model.py:178-185), stored as
-    pages: k[i], v[i] are [batch*max_pages, KV, PAGE, D] bf16 and
+    pages: k[i], v[i] are [num_pages, KV, PAGE, D] bf16 and
     cache["page_table"] [batch, max_pages] int32 maps position p of sequence
-    b to page page_table[b, p // PAGE].  `mesh` is accepted for signature
-    compatibility (one GPU, no mesh)."""
+    b to page page_table[b, p // PAGE].  By default every sequence owns
+    max_pages pages (num_pages = batch * max_pages, identity table); with a
+    smaller shared pool the table starts unmapped (-1) and batch.PagePool
+    hands pages out.  `mesh` is accepted for signature compatibility (one
+    GPU, no mesh)."""
     if dtype != torch.bfloat16:
         raise ValueError("the cache is bf16")
     max_pages = (max_len + page_size - 1) // page_size
+    pool = batch * max_pages if num_pages is None else int(num_pages)
     pools_k, pools_v = [], []
     for lt in cfg.layer_types:
-        shape = (batch * max_pages, cfg.kv_heads_for(lt), page_size, cfg.head_dim_for(lt))
+        shape = (pool, cfg.kv_heads_for(lt), page_size, cfg.head_dim_for(lt))
         pools_k.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
         pools_v.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
-    pt = torch.arange(batch * max_pages, dtype=torch.int32, device=device).reshape(batch, max_pages)
+    if num_pages is None:
+        pt = torch.arange(batch * max_pages, dtype=torch.int32, device=device).reshape(batch, max_pages)
+    else:
+        pt = torch.full((batch, max_pages), -1, dtype=torch.int32, device=device)
     return {"k": pools_k, "v": pools_v, "page_table": pt, "page_size": page_size, "max_len": max_len,
             "batch": batch}
 
@@ -363,15 +370,15 @@ class PrefillRunner:
             self.top_w = z(cap, cfg.top_k_experts, dt=torch.float32)
             self.top_i = z(cap, cfg.top_k_experts, dt=torch.int32)
         self.pos = torch.arange(cap, dtype=torch.int32, device=dev)
-        self.page_row = cache["page_table"][0].contiguous()
         self.rope = rope if rope is not None else {
             SLIDING: rope_table(cfg.head_dim, cfg.rope_theta_sliding, 1.0, self.max_len, dev),
             FULL: rope_table(cfg.global_head_dim, cfg.rope_theta_full, cfg.rope_partial_rotary_factor_full,
                              self.max_len, dev),
         }
 
-    def run(self, tokens: torch.Tensor, n: int) -> None:
-        """Runs the layers for tokens[:n] (device int32) on the current stream."""
+    def run(self, tokens: torch.Tensor, n: int, seq: int = 0) -> None:
+        """Runs the layers for tokens[:n] (device int32) of sequence `seq`
+        (its page-table row) on the current stream."""
         ops, cfg, p = self.ops, self.cfg, self.params
         if not 1 <= n <= self.capacity:
             raise ValueError(f"{n} prompt tokens outside [1, {self.capacity}]")
@@ -383,6 +390,7 @@ class PrefillRunner:
         xe = self.xe[:n] if moe else None
         moe_out = self.moe_out[:n] if moe else None
         pos = self.pos[:n]
+        page_row = self.cache["page_table"][seq]
         ops.rows_embed(tokens[:n], p["embed"], self.layers[0]["input_layernorm"], eps, x, xn)
         for i, lt in enumerate(cfg.layer_types):
             lp = self.layers[i]
@@ -396,11 +404,11 @@ class PrefillRunner:
                 ops.prefill_gemm(xn, lp["v_proj"].reshape(kv * d, H), v)
             cos, sin = self.rope[lt]
             ops.kv_append(k.view(n, kv, d), None if v is None else v.view(n, kv, d), lp["k_norm"], cos, sin,
-                          self.cache["k"][i], self.cache["v"][i], self.page_row, pos, self.max_len, eps)
+                          self.cache["k"][i], self.cache["v"][i], page_row, pos, self.max_len, eps)
             ctx = self.ctx[: n * NH * d].view(n, NH, d)
             window = cfg.sliding_window if lt == SLIDING else 0
             qh = ops.q_norm_rope(q.view(n, NH, d), lp["q_norm"], cos, sin, 0, eps)
-            ops.prefill_attention(qh, self.cache["k"][i], self.cache["v"][i], self.page_row, 0, window,
+            ops.prefill_attention(qh, self.cache["k"][i], self.cache["v"][i], page_row, 0, window,
                                   cfg.attn_logit_softcapping, ctx=ctx)
             ops.prefill_gemm(ctx.view(n, NH * d), lp["o_proj"].reshape(H, NH * d), o)
             ops.rows_post_attn(x, o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],

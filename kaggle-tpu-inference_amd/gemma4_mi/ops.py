@@ -571,3 +571,18 @@ def prefill_attention(q, k_pages, v_pages, page_table_row, p0, window, softcap, 
               page_table_row.numel(), page, T, int(p0), NH, KV, D, int(window), float(softcap or 0.0), _ptr(ctx),
               stream_handle(q.device))
     return ctx
+
+
+def argmax_rows(logits_bf16, softcap, tok, pos=None, hist=None, logits_f32=None):
+    """Greedy head for B rows of bf16 logits [B, V] (model.py:381-385, 416):
+    softcap, first index of the maximum -> tok [B]; with pos [B] / hist
+    [B, L] the positions advance and the tokens are recorded."""
+    B, V = logits_bf16.shape
+    _need(logits_bf16, BF16, "logits")
+    _need(tok, torch.int32, "tok", (B,))
+    hist_len = 0
+    if hist is not None:
+        _need(hist, torch.int32, "hist")
+        hist_len = hist.shape[1]
+    _lib.call("g4mi_argmax_rows", _ptr(logits_bf16), B, V, float(softcap or 0.0), _ptr(logits_f32), _ptr(tok),
+              _ptr(pos), _ptr(hist), hist_len, stream_handle(logits_bf16.device))

@@ -170,3 +170,31 @@ def test_checkpoint_loading_from_arrays(tmp_path):
     save_file(ckpt, str(tmp_path / "partial" / "model.safetensors"))
     with pytest.raises(KeyError):
         gw.load_params(cfg, str(tmp_path / "partial"), device="cpu")
+
+
+def test_page_pool_allocates_and_releases_pages():
+    """batch.PagePool on a CPU cache: rows start unmapped, ensure() maps
+    whole pages in order from the shared pool, release() returns them, and an
+    exhausted pool or an over-long sequence is refused."""
+    from gemma4_mi import model as gm
+    from gemma4_mi.batch import PagePool
+    from gemma4_mi.config import tiny_parity_config
+
+    cfg = tiny_parity_config()
+    cache = gm.init_cache(cfg, None, 2, 256, device="cpu", num_pages=5)
+    pool = PagePool(cache)
+    pt = cache["page_table"]
+    assert pt.shape == (2, 4) and bool((pt == -1).all())
+    pool.ensure(0, 1)
+    pool.ensure(0, 64)  # still one page
+    pool.ensure(1, 130)  # three pages
+    assert pool.owned[0] == [0] and pool.owned[1] == [1, 2, 3]
+    assert pt[0].tolist() == [0, -1, -1, -1] and pt[1].tolist() == [1, 2, 3, -1]
+    with pytest.raises(MemoryError):
+        pool.ensure(0, 200)  # needs 3 more, 1 free
+    pool.release(1)
+    assert pool.free_pages() == 4 and pt[1].tolist() == [-1, -1, -1, -1]
+    pool.ensure(0, 256)
+    assert len(pool.owned[0]) == 4 and len(set(pt[0].tolist())) == 4
+    with pytest.raises(ValueError):
+        pool.ensure(1, 257)
