@@ -267,7 +267,9 @@ int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* param
  * max_tiles, m1 - m0 <= 128) each tile uses B + group * b_group_stride: the
  * grouped per-expert GEMM.  k_slices > 1 splits K over blocks (plain
  * epilogues 0/1 only) with a workspace of g4mi_gemm_workspace_bytes.
- * K % 64 == 0; rows 16-byte aligned.  No reference counterpart: XLA's dot. */
+ * K % 64 == 0; rows 16-byte aligned.  M <= 16 without tiles or split-K
+ * runs a skinny kernel (16 output columns per block, K split over its waves).
+ * No reference counterpart: XLA's dot. */
 int64_t g4mi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t k_slices);
 int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
                    int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,

@@ -253,6 +253,75 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
       }
 }
 
+// ---- skinny GEMM (M <= 16 rows: batched decode, short prompts)
+// A block owns 16 output columns (16 B rows; with the gated epilogue 16 gate
+// and 16 up rows) for all M <= 16 A rows; its 4 waves split K into quarters
+// and run one 16x16 MFMA chain each (A rows beyond M are clamped duplicates
+// and are not stored).  The wave partials meet in LDS and are summed in wave
+// order, so there is no split-K reduce kernel; each wave requests kSkChunk
+// k-steps of A and B before multiplying them, which keeps the weight rows
+// streaming.  The grid is ceil(N/16) blocks.
+constexpr int kSkChunk = 16;
+
+template <int EP>
+__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
+  constexpr bool GATED = EP == kEpGated;
+  __shared__ float part[2][4][16][17];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+  const int n0 = blockIdx.x * 16;
+  const int ksteps = g.K / 32;
+  const int s0 = (ksteps * wave) / 4, s1 = (ksteps * (wave + 1)) / 4;
+  const int m = min(fr, g.M - 1);
+  const int arow = (g.a_rows != nullptr) ? g.a_rows[m] : m;
+  const u32x4* ap = (const u32x4*)(g.a + (size_t)arow * g.lda + fk);
+  const int n = min(n0 + fr, g.N - 1);
+  const u32x4* bp = (const u32x4*)(g.b + (size_t)n * g.ldb + fk);
+  const u32x4* up = (const u32x4*)(g.b + g.pair_offset + (size_t)n * g.ldb + fk);
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = s0; c0 < s1; c0 += kSkChunk) {
+    u32x4 af[kSkChunk], bf[kSkChunk], uf[GATED ? kSkChunk : 1];
+#pragma unroll
+    for (int j = 0; j < kSkChunk; ++j) {
+      const int st = min(c0 + j, s1 - 1);  // clamped: always in range
+      af[j] = ld16(ap + st * 4);
+      bf[j] = ld_stream(bp + st * 4);
+      if constexpr (GATED) uf[j] = ld_stream(up + st * 4);
+    }
+#pragma unroll
+    for (int j = 0; j < kSkChunk; ++j) {
+      if (c0 + j < s1) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
+                                                      __builtin_bit_cast(bf16x8, bf[j]), acc, 0, 0, 0);
+        if constexpr (GATED)
+          accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
+                                                         __builtin_bit_cast(bf16x8, uf[j]), accu, 0, 0, 0);
+      }
+    }
+  }
+  // C layout: row (A row) 4*(l/16)+i, column (output n) l%16
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    part[0][wave][4 * (lane >> 4) + i][fr] = acc[i];
+    if constexpr (GATED) part[1][wave][4 * (lane >> 4) + i][fr] = accu[i];
+  }
+  __syncthreads();
+  const int r = tid >> 4, c = tid & 15;  // one output per thread
+  const int mo = r, no = n0 + c;
+  if (mo >= g.M || no >= g.N) return;
+  const float v = ((part[0][0][r][c] + part[0][1][r][c]) + part[0][2][r][c]) + part[0][3][r][c];
+  if constexpr (GATED) {
+    const float uv = ((part[1][0][r][c] + part[1][1][r][c]) + part[1][2][r][c]) + part[1][3][r][c];
+    float a = rbf(rbf(gelu_tanh(rbf(v))) * rbf(uv));
+    if (g.row_scale != nullptr) a = rbf(a * rbf(g.row_scale[mo]));
+    ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(a);
+  } else if constexpr (EP == kEpF32) {
+    ((float*)g.c)[(size_t)mo * g.ldc + no] = v;
+  } else {
+    ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(v);
+  }
+}
+
 // C = sum over the k_slices f32 partials, in slice order.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ partial, int slices, int64_t mn,
                                                           int N, void* c, int64_t ldc, int f32_out) {
@@ -306,6 +375,13 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   g.ntiles = ntiles; g.c = c; g.ldc = ldc; g.row_scale = row_scale; g.k_slices = (int)k_slices;
   g.partial = (float*)ws;
   hipStream_t st = as_stream(stream);
+  if (tiles == nullptr && M <= 16 && k_slices == 1) {
+    const dim3 grid((unsigned)((N + 15) / 16));
+    if (epilogue == kEpGated) hipLaunchKernelGGL(gemm_skinny_kernel<kEpGated>, grid, dim3(256), 0, st, g);
+    else if (epilogue == kEpF32) hipLaunchKernelGGL(gemm_skinny_kernel<kEpF32>, grid, dim3(256), 0, st, g);
+    else hipLaunchKernelGGL(gemm_skinny_kernel<kEpBf16>, grid, dim3(256), 0, st, g);
+    return check_launch("gemm_bf16 (skinny)");
+  }
   // grouped tiles are up to 128 rows (128-row kernels); small plain M takes 64-row tiles
   const bool small = tiles == nullptr && M <= 64;
   const int64_t mtiles = tiles ? max_tiles : (M + (small ? 63 : 127)) / (small ? 64 : 128);

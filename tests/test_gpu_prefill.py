@@ -12,7 +12,8 @@ GEMM (g4mi_gemm_bf16) against float64 products of the same bf16 operands:
     (a one-ulp flip of a rounded gate or up moves the product by one ulp).
 Cases: plain 128x128 tiles with ragged edges, small M with split-K (the
 slices are summed in order, so split-K equals the one-slice result within
-f32 reassociation), row gather, grouped per-expert tiles.
+f32 reassociation), the skinny kernel (M <= 16), row gather, grouped
+per-expert tiles.
 
 MoE prefill (g4mi_moe_prefill) against the oracle's dense path
 (oracle.twin.moe(dense=True): every expert, masked by the routing weights),
@@ -80,6 +81,20 @@ def test_gemm_small_m_split_k(m, slices):
     ad, bd = a.to(DEV), b.to(DEV)
     _check_f32(ops.gemm(ad, bd, epilogue=ops.EP_F32, k_slices=slices), ref, absum)
     _check_bf16(ops.gemm(ad, bd, k_slices=slices), ref, absum)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 2816), (8, 1000, 2112), (16, 2816, 4096), (5, 300, 320)])
+def test_gemm_skinny_rows(m, n, k):
+    """M <= 16 without split-K: the skinny kernel (K split over the block's
+    waves, partials summed in wave order)."""
+    a, b = _rand((m, k), 12), _rand((n, k), 13, 0.02)
+    ref, absum = _ref(a, b)
+    ad, bd = a.to(DEV), b.to(DEV)
+    _check_bf16(ops.gemm(ad, bd), ref, absum)
+    _check_f32(ops.gemm(ad, bd, epilogue=ops.EP_F32), ref, absum)
+    rows = torch.tensor([3, 0, 2, 1, 0][: min(m, 5)] * 3, dtype=torch.int32)[:m] % m
+    ref2, absum2 = _ref(a[rows.long()], b)
+    _check_bf16(ops.gemm(ad, bd, a_rows=rows.to(DEV)), ref2, absum2)
 
 
 def test_gemm_row_gather_and_strides():
