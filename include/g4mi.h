@@ -330,9 +330,10 @@ int g4mi_prefill_attention(const uint16_t* q, const uint16_t* k_pages, const uin
  * bf16 (x . embed^T, e.g. from g4mi_gemm_bf16) -> softcap in f32 (softcap 0:
  * off), optional f32 copy [B, V], first index of the maximum per row; tok[b] =
  * it, pos[b] += 1 and hist[b * hist_len + pos[b]] = it when pos / hist are
- * given. */
+ * given.  Workspace: g4mi_argmax_rows_workspace_bytes(B). */
+int64_t g4mi_argmax_rows_workspace_bytes(int64_t B);
 int g4mi_argmax_rows(const uint16_t* logits, int64_t B, int64_t V, float softcap, float* logits_f32, int32_t* tok,
-                     int32_t* pos, int32_t* hist, int64_t hist_len, void* stream);
+                     int32_t* pos, int32_t* hist, int64_t hist_len, void* ws, int64_t ws_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -254,71 +254,88 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 }
 
 // ---- skinny GEMM (M <= 16 rows: batched decode, short prompts)
-// A block owns 16 output columns (16 B rows; with the gated epilogue 16 gate
-// and 16 up rows) for all M <= 16 A rows; its 4 waves split K into quarters
-// and run one 16x16 MFMA chain each (A rows beyond M are clamped duplicates
-// and are not stored).  The wave partials meet in LDS and are summed in wave
-// order, so there is no split-K reduce kernel; each wave requests kSkChunk
-// k-steps of A and B before multiplying them, which keeps the weight rows
-// streaming.  The grid is ceil(N/16) blocks.
-constexpr int kSkChunk = 16;
-
-template <int EP>
+// A block owns 16*NTL output columns (B rows; with the gated epilogue the
+// gate and the up rows) for all M <= 16 A rows; its 4 waves split K into
+// quarters.  Per k-step a wave loads one A fragment and multiplies it into
+// NTL 16x16 MFMA chains (A rows beyond M are clamped duplicates and are not
+// stored).  The wave partials meet in LDS and are summed in wave order, so
+// there is no split-K reduce kernel; each wave requests a chunk of k-steps of
+// A and B before multiplying them, which keeps the weight rows streaming.
+// NTL = 4 amortises the A fragments over 64 columns when N is large (the
+// lm_head); NTL = 1 keeps ceil(N/16) blocks for the layer projections.
+template <int EP, int NTL>
 __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
   constexpr bool GATED = EP == kEpGated;
-  __shared__ float part[2][4][16][17];
+  constexpr int CHK = (NTL == 1) ? 16 : 8;  // k-steps requested per chunk
+  constexpr int NP = GATED ? 2 : 1;         // B row sets (gate, up)
+  __shared__ float part[NP][4][16][16 * NTL + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  const int n0 = blockIdx.x * 16;
+  const int n0 = blockIdx.x * 16 * NTL;
   const int ksteps = g.K / 32;
   const int s0 = (ksteps * wave) / 4, s1 = (ksteps * (wave + 1)) / 4;
   const int m = min(fr, g.M - 1);
   const int arow = (g.a_rows != nullptr) ? g.a_rows[m] : m;
   const u32x4* ap = (const u32x4*)(g.a + (size_t)arow * g.lda + fk);
-  const int n = min(n0 + fr, g.N - 1);
-  const u32x4* bp = (const u32x4*)(g.b + (size_t)n * g.ldb + fk);
-  const u32x4* up = (const u32x4*)(g.b + g.pair_offset + (size_t)n * g.ldb + fk);
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f}, accu = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c0 = s0; c0 < s1; c0 += kSkChunk) {
-    u32x4 af[kSkChunk], bf[kSkChunk], uf[GATED ? kSkChunk : 1];
+  const u32x4* bp[NP][NTL];
 #pragma unroll
-    for (int j = 0; j < kSkChunk; ++j) {
+  for (int t = 0; t < NTL; ++t) {
+    const int n = min(n0 + 16 * t + fr, g.N - 1);
+    bp[0][t] = (const u32x4*)(g.b + (size_t)n * g.ldb + fk);
+    if constexpr (GATED) bp[NP - 1][t] = (const u32x4*)(g.b + g.pair_offset + (size_t)n * g.ldb + fk);
+  }
+  f32x4 acc[NP][NTL];
+#pragma unroll
+  for (int q = 0; q < NP; ++q)
+#pragma unroll
+    for (int t = 0; t < NTL; ++t) acc[q][t] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c0 = s0; c0 < s1; c0 += CHK) {
+    u32x4 af[CHK], bf[NP][NTL][CHK];
+#pragma unroll
+    for (int j = 0; j < CHK; ++j) {
       const int st = min(c0 + j, s1 - 1);  // clamped: always in range
       af[j] = ld16(ap + st * 4);
-      bf[j] = ld_stream(bp + st * 4);
-      if constexpr (GATED) uf[j] = ld_stream(up + st * 4);
+#pragma unroll
+      for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int t = 0; t < NTL; ++t) bf[q][t][j] = ld_stream(bp[q][t] + st * 4);
     }
 #pragma unroll
-    for (int j = 0; j < kSkChunk; ++j) {
+    for (int j = 0; j < CHK; ++j) {
       if (c0 + j < s1) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
-                                                      __builtin_bit_cast(bf16x8, bf[j]), acc, 0, 0, 0);
-        if constexpr (GATED)
-          accu = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
-                                                         __builtin_bit_cast(bf16x8, uf[j]), accu, 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < NP; ++q)
+#pragma unroll
+          for (int t = 0; t < NTL; ++t)
+            acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
+                                                                __builtin_bit_cast(bf16x8, bf[q][t][j]), acc[q][t],
+                                                                0, 0, 0);
       }
     }
   }
-  // C layout: row (A row) 4*(l/16)+i, column (output n) l%16
+  // C layout: row (A row) 4*(l/16)+i, column (output n) 16*t + l%16
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    part[0][wave][4 * (lane >> 4) + i][fr] = acc[i];
-    if constexpr (GATED) part[1][wave][4 * (lane >> 4) + i][fr] = accu[i];
-  }
+  for (int q = 0; q < NP; ++q)
+#pragma unroll
+    for (int t = 0; t < NTL; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) part[q][wave][4 * (lane >> 4) + i][16 * t + fr] = acc[q][t][i];
   __syncthreads();
-  const int r = tid >> 4, c = tid & 15;  // one output per thread
-  const int mo = r, no = n0 + c;
-  if (mo >= g.M || no >= g.N) return;
-  const float v = ((part[0][0][r][c] + part[0][1][r][c]) + part[0][2][r][c]) + part[0][3][r][c];
-  if constexpr (GATED) {
-    const float uv = ((part[1][0][r][c] + part[1][1][r][c]) + part[1][2][r][c]) + part[1][3][r][c];
-    float a = rbf(rbf(gelu_tanh(rbf(v))) * rbf(uv));
-    if (g.row_scale != nullptr) a = rbf(a * rbf(g.row_scale[mo]));
-    ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(a);
-  } else if constexpr (EP == kEpF32) {
-    ((float*)g.c)[(size_t)mo * g.ldc + no] = v;
-  } else {
-    ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(v);
+  for (int e = tid; e < 16 * 16 * NTL; e += 256) {  // one output per (row, column)
+    const int r = e / (16 * NTL), c = e % (16 * NTL);
+    const int mo = r, no = n0 + c;
+    if (mo >= g.M || no >= g.N) continue;
+    const float v = ((part[0][0][r][c] + part[0][1][r][c]) + part[0][2][r][c]) + part[0][3][r][c];
+    if constexpr (GATED) {
+      const float uv = ((part[1][0][r][c] + part[1][1][r][c]) + part[1][2][r][c]) + part[1][3][r][c];
+      float act = rbf(rbf(gelu_tanh(rbf(v))) * rbf(uv));
+      if (g.row_scale != nullptr) act = rbf(act * rbf(g.row_scale[mo]));
+      ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(act);
+    } else if constexpr (EP == kEpF32) {
+      ((float*)g.c)[(size_t)mo * g.ldc + no] = v;
+    } else {
+      ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(v);
+    }
   }
 }
 
@@ -376,10 +393,16 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   g.partial = (float*)ws;
   hipStream_t st = as_stream(stream);
   if (tiles == nullptr && M <= 16 && k_slices == 1) {
-    const dim3 grid((unsigned)((N + 15) / 16));
-    if (epilogue == kEpGated) hipLaunchKernelGGL(gemm_skinny_kernel<kEpGated>, grid, dim3(256), 0, st, g);
-    else if (epilogue == kEpF32) hipLaunchKernelGGL(gemm_skinny_kernel<kEpF32>, grid, dim3(256), 0, st, g);
-    else hipLaunchKernelGGL(gemm_skinny_kernel<kEpBf16>, grid, dim3(256), 0, st, g);
+    if (N >= 16384 && epilogue != kEpGated) {  // wide: 64 columns per block
+      const dim3 grid((unsigned)((N + 63) / 64));
+      if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 4>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 4>), grid, dim3(256), 0, st, g);
+    } else {
+      const dim3 grid((unsigned)((N + 15) / 16));
+      if (epilogue == kEpGated) hipLaunchKernelGGL((gemm_skinny_kernel<kEpGated, 1>), grid, dim3(256), 0, st, g);
+      else if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 1>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1>), grid, dim3(256), 0, st, g);
+    }
     return check_launch("gemm_bf16 (skinny)");
   }
   // grouped tiles are up to 128 rows (128-row kernels); small plain M takes 64-row tiles

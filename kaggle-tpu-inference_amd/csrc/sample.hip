@@ -164,48 +164,61 @@ static int64_t stage_keys(int64_t n) { return ((n + kSortN - 1) / kSortN) * kKee
 using namespace g4mi;
 
 // ------------------------------------------------------------------ batched head
-// One block per sequence row b of bf16 logits [B, V] (x . embed^T rounded to
-// bf16, model.py:381): v = f32 logit, softcap c*tanh(v/c) when c > 0
-// (model.py:382-385), optional f32 copy, then the first index of the maximum
-// (model.py:416 greedy): tok[b] = it; pos[b] += 1; hist[b][pos[b]] = it.
-__global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t* __restrict__ logits, int V, float cap,
-                                                           float* __restrict__ out_f32, int32_t* tok, int32_t* pos,
-                                                           int32_t* hist, int hist_len) {
-  __shared__ float vs[32];
-  __shared__ int is[32];
-  const int b = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// Rows b of bf16 logits [B, V] (x . embed^T rounded to bf16, model.py:381):
+// v = f32 logit, softcap c*tanh(v/c) when c > 0 (model.py:382-385), optional
+// f32 copy, then the first index of the maximum (model.py:416 greedy).  Stage
+// 1: grid (kArgParts, B), each block the best (value, index) of its slice of
+// the row; stage 2: one block per row reduces the slices and writes tok[b] =
+// it; pos[b] += 1; hist[b][pos[b]] = it.
+constexpr int kArgParts = 64;
+
+__device__ __forceinline__ void better_vi(float& bv, int& bi, float v, int i) {
+  if (v > bv || (v == bv && i < bi)) {
+    bv = v;
+    bi = i;
+  }
+}
+
+__global__ __launch_bounds__(256) void argmax_rows_part_kernel(const uint16_t* __restrict__ logits, int V, float cap,
+                                                               float* __restrict__ out_f32, float* __restrict__ pv,
+                                                               int* __restrict__ pi) {
+  __shared__ float vs[4];
+  __shared__ int is[4];
+  const int part = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int span = (V + kArgParts - 1) / kArgParts;
+  const int j0 = part * span, j1 = min(V, j0 + span);
   const uint16_t* row = logits + (size_t)b * V;
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int j = tid; j < V; j += 1024) {
+  for (int j = j0 + tid; j < j1; j += 256) {
     float v = bf2f(row[j]);
     if (cap > 0.0f) v = tanhf(v / cap) * cap;
     if (out_f32 != nullptr) out_f32[(size_t)b * V + j] = v;
-    if (v > bv) {  // j increases: strict > keeps the first index of a tie
-      bv = v;
-      bi = j;
-    }
+    better_vi(bv, bi, v, j);
   }
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = __shfl_xor(bv, m, kWave);
-    const int oi = __shfl_xor(bi, m, kWave);
-    if (ov > bv || (ov == bv && oi < bi)) {
-      bv = ov;
-      bi = oi;
-    }
-  }
+  for (int m = 32; m >= 1; m >>= 1) better_vi(bv, bi, __shfl_xor(bv, m, kWave), __shfl_xor(bi, m, kWave));
   if (lane == 0) {
     vs[wave] = bv;
     is[wave] = bi;
   }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < 16; ++w)
-      if (vs[w] > bv || (vs[w] == bv && is[w] < bi)) {
-        bv = vs[w];
-        bi = is[w];
-      }
+    for (int w = 1; w < 4; ++w) better_vi(bv, bi, vs[w], is[w]);
+    pv[b * kArgParts + part] = bv;
+    pi[b * kArgParts + part] = bi;
+  }
+}
+
+__global__ __launch_bounds__(64) void argmax_rows_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                               int32_t* tok, int32_t* pos, int32_t* hist,
+                                                               int hist_len) {
+  const int b = blockIdx.x, lane = threadIdx.x;
+  float bv = pv[b * kArgParts + lane];
+  int bi = pi[b * kArgParts + lane];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) better_vi(bv, bi, __shfl_xor(bv, m, kWave), __shfl_xor(bi, m, kWave));
+  if (lane == 0) {
     bi = (bi == 0x7fffffff) ? 0 : bi;
     tok[b] = bi;
     if (pos != nullptr) {
@@ -218,13 +231,24 @@ __global__ __launch_bounds__(1024) void argmax_rows_kernel(const uint16_t* __res
 
 extern "C" {
 
+int64_t g4mi_argmax_rows_workspace_bytes(int64_t B) { return B * kArgParts * 8; }
+
 int g4mi_argmax_rows(const uint16_t* logits, int64_t B, int64_t V, float softcap, float* logits_f32, int32_t* tok,
-                     int32_t* pos, int32_t* hist, int64_t hist_len, void* stream) {
+                     int32_t* pos, int32_t* hist, int64_t hist_len, void* ws, int64_t ws_bytes, void* stream) {
   G4MI_REQUIRE(logits && tok && B >= 1 && B <= 65535 && V >= 1 && V <= 2147483647, G4MI_EINVAL,
                "argmax_rows: bad arguments (B=%lld V=%lld)", (long long)B, (long long)V);
   G4MI_REQUIRE(hist == nullptr || (pos && hist_len >= 1), G4MI_EINVAL, "argmax_rows: hist needs pos and hist_len");
-  hipLaunchKernelGGL(argmax_rows_kernel, dim3((unsigned)B), dim3(1024), 0, as_stream(stream), logits, (int)V, softcap,
-                     logits_f32, tok, pos, hist, (int)hist_len);
+  G4MI_REQUIRE(ws && ws_bytes >= g4mi_argmax_rows_workspace_bytes(B), G4MI_EWORKSPACE,
+               "argmax_rows: workspace too small");
+  float* pv = (float*)ws;
+  int* pi = (int*)((char*)ws + B * kArgParts * 4);
+  hipStream_t st = as_stream(stream);
+  hipLaunchKernelGGL(argmax_rows_part_kernel, dim3(kArgParts, (unsigned)B), dim3(256), 0, st, logits, (int)V,
+                     softcap, logits_f32, pv, pi);
+  int rc = check_launch("argmax_rows (slices)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_rows_final_kernel, dim3((unsigned)B), dim3(64), 0, st, pv, pi, tok, pos, hist,
+                     (int)hist_len);
   return check_launch("argmax_rows");
 }
 

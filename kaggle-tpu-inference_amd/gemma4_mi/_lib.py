@@ -85,7 +85,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g4mi_moe_prefill": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _p, _i64, _p]),
     "g4mi_rows_embed": (_int, [_p, _i64, _p, _i64, _p, _i64, _f32, _p, _p, _p]),
     "g4mi_q_norm_rope": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p]),
-    "g4mi_argmax_rows": (_int, [_p, _i64, _i64, _f32, _p, _p, _p, _p, _i64, _p]),
+    "g4mi_argmax_rows_workspace_bytes": (_i64, [_i64]),
+    "g4mi_argmax_rows": (_int, [_p, _i64, _i64, _f32, _p, _p, _p, _p, _i64, _p, _i64, _p]),
     "g4mi_prefill_attention": (
         _int, [_p, _p, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _p, _p],
     ),

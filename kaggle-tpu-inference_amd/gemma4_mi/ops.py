@@ -584,5 +584,6 @@ def argmax_rows(logits_bf16, softcap, tok, pos=None, hist=None, logits_f32=None)
     if hist is not None:
         _need(hist, torch.int32, "hist")
         hist_len = hist.shape[1]
+    ws = WORKSPACE.get(logits_bf16.device, "argmax_rows", int(_lib.lib().g4mi_argmax_rows_workspace_bytes(B)))
     _lib.call("g4mi_argmax_rows", _ptr(logits_bf16), B, V, float(softcap or 0.0), _ptr(logits_f32), _ptr(tok),
-              _ptr(pos), _ptr(hist), hist_len, stream_handle(logits_bf16.device))
+              _ptr(pos), _ptr(hist), hist_len, _ptr(ws), ws.numel(), stream_handle(logits_bf16.device))

@@ -53,3 +53,29 @@ def test_batched_rows_are_independent():
     got = eng.generate([a, b, a], 10)
     assert got[0] == got[2]
     torch.cuda.synchronize()
+
+
+def test_argmax_rows_softcap_ties_and_history():
+    """The batched greedy head: softcap 30 in f32, the first index of the
+    maximum per row (an exact tie goes to the lower index), pos += 1 and the
+    token recorded in that row's history."""
+    from gemma4_mi import ops
+
+    rng = np.random.default_rng(7)
+    B, V = 5, 70001
+    lg = torch.tensor(rng.standard_normal((B, V)) * 8.0, dtype=torch.bfloat16)
+    lg[1, 100] = lg[1, 60000] = 120.0  # tie after the softcap
+    lg[3, 69999] = 200.0
+    d = lg.to(DEV)
+    tok = torch.zeros(B, dtype=torch.int32, device=DEV)
+    pos = torch.arange(B, dtype=torch.int32, device=DEV) * 3
+    hist = torch.zeros((B, 32), dtype=torch.int32, device=DEV)
+    f32 = torch.empty((B, V), dtype=torch.float32, device=DEV)
+    ops.argmax_rows(d, 30.0, tok, pos, hist, logits_f32=f32)
+    torch.cuda.synchronize()
+    v = torch.tanh(lg.float() / 30.0) * 30.0
+    exp = [int(np.argmax(v[b].numpy())) for b in range(B)]  # numpy argmax: first maximal index
+    assert tok.cpu().tolist() == exp and exp[1] == 100 and exp[3] == 69999
+    assert pos.cpu().tolist() == [3 * b + 1 for b in range(B)]
+    assert [int(hist[b, 3 * b + 1]) for b in range(B)] == exp
+    assert torch.allclose(f32.cpu(), v, rtol=0, atol=2e-6)

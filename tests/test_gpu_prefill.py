@@ -83,10 +83,12 @@ def test_gemm_small_m_split_k(m, slices):
     _check_bf16(ops.gemm(ad, bd, k_slices=slices), ref, absum)
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 4096, 2816), (8, 1000, 2112), (16, 2816, 4096), (5, 300, 320)])
+@pytest.mark.parametrize("m,n,k", [(1, 4096, 2816), (8, 1000, 2112), (16, 2816, 4096), (5, 300, 320),
+                                   (8, 20000, 512)])
 def test_gemm_skinny_rows(m, n, k):
     """M <= 16 without split-K: the skinny kernel (K split over the block's
-    waves, partials summed in wave order)."""
+    waves, partials summed in wave order; 64 columns per block from N =
+    16384)."""
     a, b = _rand((m, k), 12), _rand((n, k), 13, 0.02)
     ref, absum = _ref(a, b)
     ad, bd = a.to(DEV), b.to(DEV)
