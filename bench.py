@@ -629,7 +629,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None, help="untimed steps (decode: 64, moe_block: 100)")
     ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode")
     ap.add_argument("--max-len", type=int, default=32768)
-    ap.add_argument("--prompt-len", type=int, default=54)
+    ap.add_argument("--prompt-len", type=int, default=None,
+                    help="prompt tokens (decode: 54, prefill: 2048, batch_decode: 8192 per sequence)")
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -638,6 +639,8 @@ def main() -> int:
         args.steps = {"decode": 704, "prefill": 5, "batch_decode": 256}.get(args.workload, 1000)
     if args.warmup is None:
         args.warmup = {"decode": 64, "prefill": 1, "batch_decode": 8}.get(args.workload, 100)
+    if args.prompt_len is None:
+        args.prompt_len = {"prefill": 2048, "batch_decode": 8192}.get(args.workload, 54)
     if args.gpus != 1:
         print(f"bench.py measures one MI355X: this build has no multi-GPU path (--gpus {args.gpus} refused)",
               file=sys.stderr)
