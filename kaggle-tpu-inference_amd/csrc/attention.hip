@@ -64,6 +64,33 @@ __device__ __forceinline__ long long page_off(const AttnDims& a, const int32_t* 
   return ((((long long)page * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
 }
 
+// The same through page-table entries staged in LDS (ptl[i] = entry of page
+// first + i): no dependent global load per tile, so the next tile's rows can
+// be requested while the current one is multiplied.
+__device__ __forceinline__ long long page_off_lds(const AttnDims& a, const int* ptl, int first, int p, int kv) {
+  const int page = ptl[p / a.page - first];
+  if (page < 0 || page >= a.num_pages) return -1;
+  return ((((long long)page * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+}
+
+// Requests the page-table entries of pages [first, first + 2*256) of one
+// sequence (clamped to the row) into registers; stage_store() writes them to
+// LDS before the block's next barrier.  A split spans at most kChunkMax + 1
+// pages.
+struct PtStage {
+  int v[2];
+};
+__device__ __forceinline__ PtStage stage_load(const AttnDims& a, const int32_t* pt_row, int first) {
+  PtStage s;
+#pragma unroll
+  for (int r = 0; r < 2; ++r) s.v[r] = pt_row[min(first + (int)threadIdx.x + 256 * r, a.max_pages - 1)];
+  return s;
+}
+__device__ __forceinline__ void stage_store(const PtStage& s, int* ptl) {
+#pragma unroll
+  for (int r = 0; r < 2; ++r) ptl[threadIdx.x + 256 * r] = s.v[r];
+}
+
 __device__ __forceinline__ float wave_max_bfly(float m) {
 #pragma unroll
   for (int s = 1; s < 64; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, kWave));
@@ -136,6 +163,7 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   __shared__ float sc[G][kChunkMax];
   __shared__ float redm[4][G];
   __shared__ float redl[4][G];
+  __shared__ int ptl[512];
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = pos_arr[b];
@@ -146,20 +174,23 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   const int npos = end - start;
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
 
-  // The first K tile of this wave is requested before anything else: it
-  // does not depend on q, so its HBM latency overlaps the q prologue.
+  // The split's page-table entries and the first K tile of this wave are
+  // requested before anything else: they do not depend on q, so their HBM
+  // latency overlaps the q prologue.  Later tiles find their pages in LDS.
   const int kg = lane >> 4, col = lane & 15;
   const int ntiles = (npos + 15) >> 4;
-  auto load_tile = [&](int t, u32x4* bf, long long& off) {
+  const int first = start / a.page;
+  const PtStage pts = stage_load(a, pt_row, first);
+  auto load_tile = [&](int t, u32x4* bf, long long& off, bool staged) {
     const int jc = min(t * 16 + col, npos - 1);
-    off = page_off(a, pt_row, start + jc, kv);
+    off = staged ? page_off_lds(a, ptl, first, start + jc, kv) : page_off(a, pt_row, start + jc, kv);
     const uint16_t* kp = k_pages + max(off, 0ll) + 8 * kg;
 #pragma unroll
     for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
   };
   u32x4 bcur[KS];
   long long ocur;
-  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur);
+  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur, false);
 
   // Prologue: wave w owns q heads w, w+4 (G <= 8); with the append, waves 2
   // and 3 also own the new K and V rows.
@@ -201,9 +232,10 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
       if (wave == 2) kn16[so + i] = f2bf(kvx[i]);
     }
   }
+  stage_store(pts, ptl);
   __syncthreads();
   if (mine) {
-    const long long off = page_off(a, pt_row, pos, kv);
+    const long long off = page_off_lds(a, ptl, first, pos, kv);
     if (off >= 0)
       for (int d = tid; d < D; d += 256) {
         k_pages[off + d] = f2bf(knew[d]);
@@ -218,7 +250,7 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   for (int t = wave; t < ntiles; t += 4) {
     u32x4 bnext[KS];
     long long onext;
-    load_tile(min(t + 4, ntiles - 1), bnext, onext);  // clamped: always in range
+    load_tile(min(t + 4, ntiles - 1), bnext, onext, true);  // clamped: always in range
     const int j = t * 16 + col;
     const bool isnew = mine && (start + j == pos);
     if (mine) {
@@ -486,6 +518,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   float(*pr)[kChunkMax] = reinterpret_cast<float(*)[kChunkMax]>(lds_f);
   __shared__ float mg[G], sg[G];
   __shared__ int flag;
+  __shared__ int ptl[512];
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int pos = pos_arr[b];
@@ -519,18 +552,23 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
     sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo) + min(j, npos - 1)];
   }
   const int nsteps = (npos + PPV - 1) / PPV;
-  auto vload = [&](int st0, u32x4* vf, bool* okv) {
+  const int first = start / a.page;
+  const PtStage pts = stage_load(a, pt_row, first);
+  // the first batch through the page table in memory, later ones through LDS
+  auto vload = [&](int st0, u32x4* vf, bool* okv, bool staged) {
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       const int j = (st0 + u) * PPV + slot;
-      const long long off = page_off(a, pt_row, start + min(j, npos - 1), kv);
+      const int p = start + min(j, npos - 1);
+      const long long off = staged ? page_off_lds(a, ptl, first, p, kv) : page_off(a, pt_row, p, kv);
       vf[u] = ld16((const u32x4*)(v_pages + max(off, 0ll) + dofs));
       okv[u] = (j < npos) && (off >= 0);
     }
   };
   u32x4 vcur[UB];
   bool okcur[UB];
-  vload(0, vcur, okcur);
+  vload(0, vcur, okcur, false);
+  stage_store(pts, ptl);
   // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
 #pragma unroll
   for (int u = 0; u < (G + 3) / 4; ++u) {
@@ -582,7 +620,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   for (int st0 = 0; st0 < nsteps; st0 += UB) {
     u32x4 vnext[UB];
     bool oknext[UB];
-    if (st0 + UB < nsteps) vload(st0 + UB, vnext, oknext);
+    if (st0 + UB < nsteps) vload(st0 + UB, vnext, oknext, true);
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       const int j = (st0 + u) * PPV + slot;
