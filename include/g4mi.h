@@ -268,7 +268,8 @@ int g4mi_sample(const float* logits, int64_t V, int64_t top_k, const void* param
  * grouped per-expert GEMM.  k_slices > 1 splits K over blocks (plain
  * epilogues 0/1 only) with a workspace of g4mi_gemm_workspace_bytes.
  * K % 64 == 0; rows 16-byte aligned.  M <= 16 without tiles or split-K
- * runs a skinny kernel (16 output columns per block, K split over its waves).
+ * runs a skinny kernel (16 output columns per block, K split over its waves,
+ * each wave's K range requested in one round trip).
  * No reference counterpart: XLA's dot. */
 int64_t g4mi_gemm_workspace_bytes(int64_t M, int64_t N, int64_t k_slices);
 int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
@@ -276,6 +277,15 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
                    const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes,
                    void* stream);
+
+/* Several products that share A in one skinny launch: C_s = A . B_s^T for
+ * the nseg <= 4 segments, B_s [n[s], K] (row stride K), C_s [M, n[s]] bf16
+ * (row stride n[s]); M <= 16, every n[s] a multiple of 16, K % 64 == 0.
+ * For the batched decode step's q, k and v projections of the same
+ * normalised rows (model.py:197-200), which read 46 MB of weights per
+ * sliding layer in one launch instead of three. */
+int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K, int32_t nseg,
+                            const uint16_t* const* b, const int64_t* n, uint16_t* const* c, void* stream);
 
 /* The dense-MoE prefill of model.py:241-250 for n tokens: xn [n, H] (the
  * pre_feedforward_layernorm_2 output), routing top_w [n, K] f32 / top_i

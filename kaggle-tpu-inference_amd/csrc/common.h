@@ -83,6 +83,12 @@ __device__ __forceinline__ double sumsq8_f64(const u32x4 a, double acc) {
 // Weights are streamed once per token: mark them non-temporal so they do not
 // evict the activations and KV pages that are re-read.
 __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_nontemporal_load(p); }
+
+// The wave's index in its block as a scalar: every lane of a wave has the
+// same threadIdx.x >> 6, and saying so keeps loops and branches on it
+// uniform (scalar branches; no exec-masked loops whose loads the compiler
+// sinks into divergent blocks behind a full vmcnt(0) wait).
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 
 // ------------------------------------------------------------------ reductions

@@ -38,6 +38,8 @@ struct GemmTile {
   int32_t group, m0, m1;
 };
 
+constexpr int kMaxSeg = 4;
+
 struct GemmArgs {
   const uint16_t* a;
   int64_t lda;
@@ -54,6 +56,13 @@ struct GemmArgs {
   const float* row_scale;   // gated: per output row weight (null: 1)
   int k_slices;             // split-K slices (f32 partials when > 1)
   float* partial;           // [k_slices, M, N] f32
+  // column segments (skinny kernel only): nseg > 0 splits the N output
+  // columns at seg_end[]; segment s reads its own B rows seg_b[s] and writes
+  // its own C seg_c[s] (row stride = the segment's width)
+  int nseg;
+  int seg_end[kMaxSeg];
+  const uint16_t* seg_b[kMaxSeg];
+  void* seg_c[kMaxSeg];
 };
 
 constexpr int kBK = 64;  // K per pipeline step
@@ -259,30 +268,48 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
 // quarters.  Per k-step a wave loads one A fragment and multiplies it into
 // NTL 16x16 MFMA chains (A rows beyond M are clamped duplicates and are not
 // stored).  The wave partials meet in LDS and are summed in wave order, so
-// there is no split-K reduce kernel; each wave requests a chunk of k-steps of
-// A and B before multiplying them, which keeps the weight rows streaming.
-// NTL = 4 amortises the A fragments over 64 columns when N is large (the
-// lm_head); NTL = 1 keeps ceil(N/16) blocks for the layer projections.
-template <int EP, int NTL>
-__global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
+// there is no split-K reduce kernel.  Each wave requests CHK k-steps of A and
+// B -- its whole K quarter when that fits, so one round trip -- before the
+// first multiply.  NTL = 4 amortises the A fragments over 64 columns when N
+// is large (the lm_head); NTL = 1 keeps ceil(N/16) blocks for the layer
+// projections.  With column segments (NTL = 1) a block's 16 columns lie in
+// one segment, whose B rows and C it uses.
+template <int EP, int NTL, int CHK, int NWV = 4>
+__global__ __launch_bounds__(64 * NWV) void gemm_skinny_kernel(GemmArgs g) {
   constexpr bool GATED = EP == kEpGated;
-  constexpr int CHK = (NTL == 1) ? 16 : 8;  // k-steps requested per chunk
   constexpr int NP = GATED ? 2 : 1;         // B row sets (gate, up)
-  __shared__ float part[NP][4][16][16 * NTL + 1];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ float part[NP][NWV][16][16 * NTL + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  const int n0 = blockIdx.x * 16 * NTL;
+  int n0 = blockIdx.x * 16 * NTL;
+  const uint16_t* bmat = g.b;
+  void* cmat = g.c;
+  int ncols = g.N;
+  int64_t ldb = g.ldb, ldc = g.ldc;
+  if (g.nseg > 0) {  // block-uniform: selects, no indexed kernel arguments
+    int sg = 0;
+#pragma unroll
+    for (int i = 0; i + 1 < kMaxSeg; ++i) sg += (i + 1 < g.nseg && n0 >= g.seg_end[i]) ? 1 : 0;
+    const int lo = (sg == 0) ? 0 : (sg == 1) ? g.seg_end[0] : (sg == 2) ? g.seg_end[1] : g.seg_end[2];
+    const int hi = (sg == 0) ? g.seg_end[0] : (sg == 1) ? g.seg_end[1] : (sg == 2) ? g.seg_end[2] : g.seg_end[3];
+    bmat = (sg == 0) ? g.seg_b[0] : (sg == 1) ? g.seg_b[1] : (sg == 2) ? g.seg_b[2] : g.seg_b[3];
+    cmat = (sg == 0) ? g.seg_c[0] : (sg == 1) ? g.seg_c[1] : (sg == 2) ? g.seg_c[2] : g.seg_c[3];
+    n0 -= lo;
+    ncols = hi - lo;
+    ldb = g.K;
+    ldc = ncols;
+  }
   const int ksteps = g.K / 32;
-  const int s0 = (ksteps * wave) / 4, s1 = (ksteps * (wave + 1)) / 4;
+  const int s0 = (ksteps * wave) / NWV, s1 = (ksteps * (wave + 1)) / NWV;
   const int m = min(fr, g.M - 1);
   const int arow = (g.a_rows != nullptr) ? g.a_rows[m] : m;
   const u32x4* ap = (const u32x4*)(g.a + (size_t)arow * g.lda + fk);
   const u32x4* bp[NP][NTL];
 #pragma unroll
   for (int t = 0; t < NTL; ++t) {
-    const int n = min(n0 + 16 * t + fr, g.N - 1);
-    bp[0][t] = (const u32x4*)(g.b + (size_t)n * g.ldb + fk);
-    if constexpr (GATED) bp[NP - 1][t] = (const u32x4*)(g.b + g.pair_offset + (size_t)n * g.ldb + fk);
+    const int n = min(n0 + 16 * t + fr, ncols - 1);
+    bp[0][t] = (const u32x4*)(bmat + (size_t)n * ldb + fk);
+    if constexpr (GATED) bp[NP - 1][t] = (const u32x4*)(bmat + g.pair_offset + (size_t)n * ldb + fk);
   }
   f32x4 acc[NP][NTL];
 #pragma unroll
@@ -298,19 +325,22 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < NP; ++q)
 #pragma unroll
-        for (int t = 0; t < NTL; ++t) bf[q][t][j] = ld_stream(bp[q][t] + st * 4);
+        for (int t = 0; t < NTL; ++t) bf[q][t][j] = ld16(bp[q][t] + st * 4);
     }
+    // every load of the chunk is issued before the first wait
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < CHK; ++j) {
-      if (c0 + j < s1) {
+      // a clamped step past the wave's range multiplies a zero A fragment
+      // (a select, not a branch: the loads stay where they were issued)
+      const u32x4 aj = (c0 + j < s1) ? af[j] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int q = 0; q < NP; ++q)
+      for (int q = 0; q < NP; ++q)
 #pragma unroll
-          for (int t = 0; t < NTL; ++t)
-            acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[j]),
-                                                                __builtin_bit_cast(bf16x8, bf[q][t][j]), acc[q][t],
-                                                                0, 0, 0);
-      }
+        for (int t = 0; t < NTL; ++t)
+          acc[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, aj),
+                                                              __builtin_bit_cast(bf16x8, bf[q][t][j]), acc[q][t], 0, 0,
+                                                              0);
     }
   }
   // C layout: row (A row) 4*(l/16)+i, column (output n) 16*t + l%16
@@ -321,20 +351,24 @@ __global__ __launch_bounds__(256) void gemm_skinny_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) part[q][wave][4 * (lane >> 4) + i][16 * t + fr] = acc[q][t][i];
   __syncthreads();
-  for (int e = tid; e < 16 * 16 * NTL; e += 256) {  // one output per (row, column)
+  for (int e = tid; e < 16 * 16 * NTL; e += 64 * NWV) {  // one output per (row, column)
     const int r = e / (16 * NTL), c = e % (16 * NTL);
     const int mo = r, no = n0 + c;
-    if (mo >= g.M || no >= g.N) continue;
-    const float v = ((part[0][0][r][c] + part[0][1][r][c]) + part[0][2][r][c]) + part[0][3][r][c];
+    if (mo >= g.M || no >= ncols) continue;
+    float v = part[0][0][r][c];
+#pragma unroll
+    for (int w = 1; w < NWV; ++w) v += part[0][w][r][c];
     if constexpr (GATED) {
-      const float uv = ((part[1][0][r][c] + part[1][1][r][c]) + part[1][2][r][c]) + part[1][3][r][c];
+      float uv = part[1][0][r][c];
+#pragma unroll
+      for (int w = 1; w < NWV; ++w) uv += part[1][w][r][c];
       float act = rbf(rbf(gelu_tanh(rbf(v))) * rbf(uv));
       if (g.row_scale != nullptr) act = rbf(act * rbf(g.row_scale[mo]));
-      ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(act);
+      ((uint16_t*)cmat)[(size_t)mo * ldc + no] = f2bf(act);
     } else if constexpr (EP == kEpF32) {
-      ((float*)g.c)[(size_t)mo * g.ldc + no] = v;
+      ((float*)cmat)[(size_t)mo * ldc + no] = v;
     } else {
-      ((uint16_t*)g.c)[(size_t)mo * g.ldc + no] = f2bf(v);
+      ((uint16_t*)cmat)[(size_t)mo * ldc + no] = f2bf(v);
     }
   }
 }
@@ -391,17 +425,24 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   g.pair_offset = pair_offset; g.M = (int)M; g.N = (int)N; g.K = (int)K; g.tiles = (const GemmTile*)tiles;
   g.ntiles = ntiles; g.c = c; g.ldc = ldc; g.row_scale = row_scale; g.k_slices = (int)k_slices;
   g.partial = (float*)ws;
+  g.nseg = 0;
   hipStream_t st = as_stream(stream);
   if (tiles == nullptr && M <= 16 && k_slices == 1) {
     if (N >= 16384 && epilogue != kEpGated) {  // wide: 64 columns per block
       const dim3 grid((unsigned)((N + 63) / 64));
-      if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 4>), grid, dim3(256), 0, st, g);
-      else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 4>), grid, dim3(256), 0, st, g);
+      if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 4, 8>), grid, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 4, 8>), grid, dim3(256), 0, st, g);
     } else {
+      // a wave's whole K quarter in one request when it is at most 24 (or 32) steps
       const dim3 grid((unsigned)((N + 15) / 16));
-      if (epilogue == kEpGated) hipLaunchKernelGGL((gemm_skinny_kernel<kEpGated, 1>), grid, dim3(256), 0, st, g);
-      else if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 1>), grid, dim3(256), 0, st, g);
-      else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1>), grid, dim3(256), 0, st, g);
+      const bool wide = (K / 32 + 3) / 4 > 24;
+#define G4MI_SKINNY(E)                                                                          \
+  if (wide) hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 32>), grid, dim3(256), 0, st, g);      \
+  else hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 24>), grid, dim3(256), 0, st, g);
+      if (epilogue == kEpGated) { G4MI_SKINNY(kEpGated) }
+      else if (epilogue == kEpF32) { G4MI_SKINNY(kEpF32) }
+      else { G4MI_SKINNY(kEpBf16) }
+#undef G4MI_SKINNY
     }
     return check_launch("gemm_bf16 (skinny)");
   }
@@ -424,6 +465,39 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
                        (int)k_slices, mn, (int)N, c, ldc, epilogue == kEpF32 ? 1 : 0);
   }
   return check_launch("gemm_bf16");
+}
+
+int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K, int32_t nseg,
+                            const uint16_t* const* b, const int64_t* n, uint16_t* const* c, void* stream) {
+  G4MI_REQUIRE(a && b && n && c && nseg >= 1 && nseg <= kMaxSeg, G4MI_EINVAL,
+               "gemm_segments: need 1..%d segments", kMaxSeg);
+  G4MI_REQUIRE(M >= 1 && M <= 16, G4MI_EUNSUPPORTED, "gemm_segments: M=%lld not in [1, 16]", (long long)M);
+  G4MI_REQUIRE(K >= kBK && K % kBK == 0, G4MI_EUNSUPPORTED, "gemm_segments: K=%lld must be a multiple of %d",
+               (long long)K, kBK);
+  G4MI_REQUIRE(lda % 8 == 0 && ((uintptr_t)a & 15u) == 0, G4MI_EALIGN, "gemm_segments: A rows must be 16-byte aligned");
+  GemmArgs g = {};
+  g.a = a; g.lda = lda; g.M = (int)M; g.K = (int)K; g.ldb = K; g.k_slices = 1; g.nseg = nseg;
+  int64_t end = 0;
+  for (int s = 0; s < kMaxSeg; ++s) {
+    if (s < nseg) {
+      G4MI_REQUIRE(b[s] && c[s] && ((uintptr_t)b[s] & 15u) == 0, G4MI_EALIGN,
+                   "gemm_segments: segment %d needs 16-byte aligned B rows and a C", s);
+      G4MI_REQUIRE(n[s] >= 16 && n[s] % 16 == 0, G4MI_EUNSUPPORTED,
+                   "gemm_segments: segment %d width %lld must be a positive multiple of 16", s, (long long)n[s]);
+      end += n[s];
+      G4MI_REQUIRE(end <= 2147483647, G4MI_EINVAL, "gemm_segments: too many columns");
+      g.seg_b[s] = b[s]; g.seg_c[s] = c[s];
+    } else {
+      g.seg_b[s] = b[nseg - 1]; g.seg_c[s] = c[nseg - 1];
+    }
+    g.seg_end[s] = (int)end;
+  }
+  g.b = g.seg_b[0]; g.c = g.seg_c[0]; g.N = (int)end; g.ldc = n[0];
+  const dim3 grid((unsigned)(end / 16));
+  hipStream_t st = as_stream(stream);
+  if ((K / 32 + 3) / 4 > 24) hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 32>), grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 24>), grid, dim3(256), 0, st, g);
+  return check_launch("gemm_bf16_segments");
 }
 
 }  // extern "C"

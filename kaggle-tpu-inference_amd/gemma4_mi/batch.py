@@ -131,10 +131,17 @@ class BatchDecodeRunner:
             q = self.q[: B * NH * d].view(B, NH * d)
             k = self.k[: B * kv * d].view(B, kv * d)
             v = None if cfg.k_eq_v_for(lt) else self.v[: B * kv * d].view(B, kv * d)
-            ops.prefill_gemm(self.xn, lp["q_proj"].reshape(NH * d, H), q)
-            ops.prefill_gemm(self.xn, lp["k_proj"].reshape(kv * d, H), k)
+            # q, k and v of the B rows in one launch (model.py:197-200)
+            ws_ = [lp["q_proj"].reshape(NH * d, H), lp["k_proj"].reshape(kv * d, H)]
+            outs = [q, k]
             if v is not None:
-                ops.prefill_gemm(self.xn, lp["v_proj"].reshape(kv * d, H), v)
+                ws_.append(lp["v_proj"].reshape(kv * d, H))
+                outs.append(v)
+            if B <= 16:
+                ops.gemm_segments(self.xn, ws_, outs)
+            else:
+                for w_, o_ in zip(ws_, outs):
+                    ops.prefill_gemm(self.xn, w_, o_)
             cos, sin = self.rope[lt]
             ctx = self.ctx[: B * NH * d].view(B, NH, d)
             ops.decode_attention(q.view(B, NH, d), k.view(B, kv, d), None if v is None else v.view(B, kv, d),

@@ -479,6 +479,27 @@ def gemm(a, b, out=None, a_rows=None, epilogue=EP_BF16, pair_offset=0, n=None, r
     return out
 
 
+def gemm_segments(a, bs, outs):
+    """outs[s] = A . bs[s]^T (bf16) for up to 4 weight matrices sharing A, in
+    one launch: a [M <= 16, K], bs[s] [N_s, K] contiguous, outs[s] [M, N_s]
+    contiguous, N_s multiples of 16 (model.py:197-200 for B decode rows)."""
+    M, K = a.shape
+    _need(a, BF16, "a")
+    if not 1 <= len(bs) == len(outs) <= 4:
+        raise ValueError("gemm_segments takes 1 to 4 (weight, output) pairs")
+    for b, c in zip(bs, outs):
+        _need(b, BF16, "b")
+        _need(c, BF16, "out", (M, b.shape[0]))
+        if b.shape[1] != K or not b.is_contiguous() or not c.is_contiguous():
+            raise ValueError("segments need contiguous [N_s, K] weights and [M, N_s] outputs")
+    nseg = len(bs)
+    bp = (ctypes.c_void_p * nseg)(*[b.data_ptr() for b in bs])
+    cp = (ctypes.c_void_p * nseg)(*[c.data_ptr() for c in outs])
+    nn = (ctypes.c_int64 * nseg)(*[b.shape[0] for b in bs])
+    _lib.call("g4mi_gemm_bf16_segments", _ptr(a), a.stride(0), M, K, nseg, bp, nn, cp, stream_handle(a.device))
+    return outs
+
+
 def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
     """model.py:241-250 for xn [n, H]: out [n, H] bf16 (selected experts only,
     grouped MFMA GEMMs)."""

@@ -12,8 +12,9 @@ GEMM (g4mi_gemm_bf16) against float64 products of the same bf16 operands:
     (a one-ulp flip of a rounded gate or up moves the product by one ulp).
 Cases: plain 128x128 tiles with ragged edges, small M with split-K (the
 slices are summed in order, so split-K equals the one-slice result within
-f32 reassociation), the skinny kernel (M <= 16), row gather, grouped
-per-expert tiles.
+f32 reassociation), the skinny kernel (M <= 16) alone and with column
+segments (several weight matrices sharing A in one launch), row gather,
+grouped per-expert tiles.
 
 MoE prefill (g4mi_moe_prefill) against the oracle's dense path
 (oracle.twin.moe(dense=True): every expert, masked by the routing weights),
@@ -97,6 +98,21 @@ def test_gemm_skinny_rows(m, n, k):
     rows = torch.tensor([3, 0, 2, 1, 0][: min(m, 5)] * 3, dtype=torch.int32)[:m] % m
     ref2, absum2 = _ref(a[rows.long()], b)
     _check_bf16(ops.gemm(ad, bd, a_rows=rows.to(DEV)), ref2, absum2)
+
+
+@pytest.mark.parametrize("m", [1, 8, 16])
+def test_gemm_segments_share_a(m):
+    """q/k/v-style segments in one launch (2816 inputs; 4096 + 2048 + 2048
+    columns, and a full layer's 8192 + 1024 at K = 4096): each segment equals
+    its own product."""
+    for k, widths in ((2816, (4096, 2048, 2048)), (4096, (8192, 1024))):
+        a = _rand((m, k), 14)
+        bs = [_rand((w, k), 15 + i, 0.02) for i, w in enumerate(widths)]
+        outs = [torch.zeros((m, w), dtype=torch.bfloat16, device=DEV) for w in widths]
+        ops.gemm_segments(a.to(DEV), [b.to(DEV) for b in bs], outs)
+        for b, o in zip(bs, outs):
+            ref, absum = _ref(a, b)
+            _check_bf16(o, ref, absum)
 
 
 def test_gemm_row_gather_and_strides():
