@@ -165,7 +165,7 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   __shared__ float redl[4][G];
   __shared__ int ptl[512];
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int pos = pos_arr[b];
   const Range R = attn_range(a, pos);
   if (split >= R.n_eff) return;
@@ -374,6 +374,54 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
   }
 }
 
+// Merged softmax statistics of the splits of every head of a KV head into
+// mg/sg (LDS): wave w owns heads w, w+4; lanes stride the splits.  Every
+// head's split statistics are requested before the first reduction
+// (unconditional loads from clamped indices), so the merge costs one round
+// trip.  R.n_eff >= 1.
+template <int G>
+__device__ __forceinline__ void merge_split_stats(const AttnDims& a, const Range& R, int kv, int b, int wave,
+                                                  int lane, const float* __restrict__ ws_stats, float* mg, float* sg) {
+  constexpr int GU = (G + 3) / 4;
+  constexpr int Q = kMaxSplits / 64;
+  float st_m[GU][Q], st_l[GU][Q];
+#pragma unroll
+  for (int u = 0; u < GU; ++u) {
+    const int h = kv * G + min(wave + 4 * u, G - 1);
+    const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
+    const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+      const int ic = min(lane + 64 * q, R.n_eff - 1);
+      st_m[u][q] = sm[ic];
+      st_l[u][q] = sl[ic];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < GU; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      float m = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) {
+        const bool in = lane + 64 * q < R.n_eff;
+        st_m[u][q] = in ? st_m[u][q] : -INFINITY;
+        st_l[u][q] = in ? st_l[u][q] : 0.0f;
+        m = fmaxf(m, st_m[u][q]);
+      }
+      m = wave_max_bfly(m);
+      float t = 0.0f;
+#pragma unroll
+      for (int q = 0; q < Q; ++q) t += (st_m[u][q] == -INFINITY) ? 0.0f : expf(st_m[u][q] - m) * st_l[u][q];
+      t = group_sum<64>(t);
+      if (lane == 0) {
+        mg[g] = m;
+        sg[g] = t;
+      }
+    }
+  }
+}
+
 // Short ranges (len <= kShortLen): block x of a KV head owns head dims
 // [x*kSliceD, (x+1)*kSliceD) of its G query heads over every attended
 // position, so no partials cross blocks.  LPS lanes (8 dims each) cover a
@@ -393,23 +441,28 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
   constexpr int PPB = 4 * PPW;
   constexpr int NST = kShortLen / PPB;       // V steps per lane at most
   constexpr int SPT = G * kShortLen / 256;   // scores per thread at most
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int sub = lane % LPS, slot = lane / LPS;
   const int d0 = blockIdx.x * kSliceD + sub * 8;
   const int len = R.len;
   const int nst = (len + PPB - 1) / PPB;
-  // loads first: this block's V slice at every position, then the scores
+  // loads first: this block's V slice at every position, then the scores.
+  // Every step's page-table entry is requested before any V row (unconditional
+  // loads from clamped positions), so the V rows cost one round trip after
+  // the entries whatever the number of steps.
+  int pg[NST];
+#pragma unroll
+  for (int st = 0; st < NST; ++st) pg[st] = pt_row[(R.lo + min(st * PPB + wave * PPW + slot, len - 1)) / a.page];
   u32x4 vv[NST];
   bool ok[NST];
 #pragma unroll
   for (int st = 0; st < NST; ++st) {
-    ok[st] = false;
-    if (st < nst) {  // block-uniform
-      const int j = st * PPB + wave * PPW + slot;
-      const long long off = page_off(a, pt_row, R.lo + min(j, len - 1), kv);
-      vv[st] = ld16((const u32x4*)(v_pages + max(off, 0ll) + d0));
-      ok[st] = (j < len) && (off >= 0);
-    }
+    const int j = st * PPB + wave * PPW + slot;
+    const int p = R.lo + min(j, len - 1);
+    const bool valid = pg[st] >= 0 && pg[st] < a.num_pages;
+    const long long off = ((((long long)(valid ? pg[st] : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+    vv[st] = ld16((const u32x4*)(v_pages + off + d0));
+    ok[st] = (st < nst) && (j < len) && valid;
   }
   float sreg[SPT];
 #pragma unroll
@@ -417,36 +470,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
     const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
     sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + min(j, len - 1)];
   }
-  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
-#pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) {
-    const int g = wave + 4 * u;
-    if (g < G) {
-      const int h = kv * G + g;
-      const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
-      const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
-      float st_m[kMaxSplits / 64], st_l[kMaxSplits / 64];
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) {
-        const int ic = min(lane + 64 * q, R.n_eff - 1);
-        const bool in = lane + 64 * q < R.n_eff;
-        st_m[q] = in ? sm[ic] : -INFINITY;
-        st_l[q] = in ? sl[ic] : 0.0f;
-      }
-      float m = -INFINITY;
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) m = fmaxf(m, st_m[q]);
-      m = wave_max_bfly(m);
-      float t = 0.0f;
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) t += (st_m[q] == -INFINITY) ? 0.0f : expf(st_m[q] - m) * st_l[q];
-      t = group_sum<64>(t);
-      if (lane == 0) {
-        mg[g] = m;
-        sg[g] = t;
-      }
-    }
-  }
+  merge_split_stats<G>(a, R, kv, b, wave, lane, ws_stats, mg, sg);
   __syncthreads();
   // normalised probabilities, rounded to bf16 (model.py:212), zero past len
 #pragma unroll
@@ -520,7 +544,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   __shared__ int flag;
   __shared__ int ptl[512];
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int pos = pos_arr[b];
   const Range R = attn_range(a, pos);
   if (R.n_eff > 0 && R.len <= kShortLen) {  // grid.x >= D / kSliceD (see launch_attn)
@@ -541,10 +565,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const int sub = lane % LPV, slot = lane / LPV;
   const int dofs = wave * (D / 4) + sub * 8;
 
-  // loads in the order they are needed: split statistics, this split's
-  // scores, then the first batch of V rows
-  float st_m[kMaxSplits / 64], st_l[kMaxSplits / 64];
-  const int g_st = wave;  // heads wave, wave+4 merged below
+  // this split's scores, the first batch of V rows and (in the merge below)
+  // the split statistics are all in flight before the first wait
   float sreg[RS];
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
@@ -554,55 +576,30 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const int nsteps = (npos + PPV - 1) / PPV;
   const int first = start / a.page;
   const PtStage pts = stage_load(a, pt_row, first);
-  // the first batch through the page table in memory, later ones through LDS
+  // the first batch through the page table in memory (every entry requested
+  // before the first V row), later ones through LDS
   auto vload = [&](int st0, u32x4* vf, bool* okv, bool staged) {
+    int pg[UB];
+    if (!staged) {
+#pragma unroll
+      for (int u = 0; u < UB; ++u) pg[u] = pt_row[(start + min((st0 + u) * PPV + slot, npos - 1)) / a.page];
+    }
 #pragma unroll
     for (int u = 0; u < UB; ++u) {
       const int j = (st0 + u) * PPV + slot;
       const int p = start + min(j, npos - 1);
-      const long long off = staged ? page_off_lds(a, ptl, first, p, kv) : page_off(a, pt_row, p, kv);
-      vf[u] = ld16((const u32x4*)(v_pages + max(off, 0ll) + dofs));
-      okv[u] = (j < npos) && (off >= 0);
+      const int e = staged ? ptl[p / a.page - first] : pg[u];
+      const bool valid = e >= 0 && e < a.num_pages;
+      const long long off = ((((long long)(valid ? e : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+      vf[u] = ld16((const u32x4*)(v_pages + off + dofs));
+      okv[u] = (j < npos) && valid;
     }
   };
   u32x4 vcur[UB];
   bool okcur[UB];
   vload(0, vcur, okcur, false);
   stage_store(pts, ptl);
-  // merge the split statistics: wave w owns heads w, w+4; lanes stride the splits
-#pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) {
-    const int g = g_st + 4 * u;
-    if (g < G) {
-      const int h = kv * G + g;
-      const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
-      const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) {
-        const int ic = min(lane + 64 * q, R.n_eff - 1);
-        st_m[q] = sm[ic];
-        st_l[q] = sl[ic];
-      }
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) {
-        const bool in = lane + 64 * q < R.n_eff;
-        st_m[q] = in ? st_m[q] : -INFINITY;
-        st_l[q] = in ? st_l[q] : 0.0f;
-      }
-      float m = -INFINITY;
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) m = fmaxf(m, st_m[q]);
-      m = wave_max_bfly(m);
-      float t = 0.0f;
-#pragma unroll
-      for (int q = 0; q < kMaxSplits / 64; ++q) t += (st_m[q] == -INFINITY) ? 0.0f : expf(st_m[q] - m) * st_l[q];
-      t = group_sum<64>(t);
-      if (lane == 0) {
-        mg[g] = m;
-        sg[g] = t;
-      }
-    }
-  }
+  merge_split_stats<G>(a, R, kv, b, wave, lane, ws_stats, mg, sg);
   __syncthreads();
   // normalised probabilities, rounded to bf16 as the reference does (model.py:212)
 #pragma unroll

@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
   __shared__ __align__(16) uint16_t kt[KB * LDK];
   __shared__ __align__(16) uint16_t vt[D * LDV];
   __shared__ __align__(16) uint16_t pt[kPfRows * LDP];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int kv = blockIdx.y;
   const int nqb = (a.T + QP - 1) / QP;
   const int qb = nqb - 1 - (int)blockIdx.x;  // longest rows first
