@@ -161,8 +161,6 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   __shared__ float knew[D];
   __shared__ float vnew[D];
   __shared__ float sc[G][kChunkMax];
-  __shared__ float redm[4][G];
-  __shared__ float redl[4][G];
   __shared__ int ptl[512];
   const int split = blockIdx.x, kv = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -174,23 +172,25 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   const int npos = end - start;
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
 
-  // The split's page-table entries and the first K tile of this wave are
-  // requested before anything else: they do not depend on q, so their HBM
-  // latency overlaps the q prologue.  Later tiles find their pages in LDS.
+  // Everything that needs only pos is requested first, in this order: the
+  // split's page-table entries, this wave's first K tile's entry, and the
+  // prologue rows (q heads, norms, cos/sin, the new K/V); then the first K
+  // tile itself.  Its HBM latency overlaps the q prologue; later tiles find
+  // their pages in LDS.  The loads are unconditional (clamped indices,
+  // selected pointers), so each wait covers only what it needs.
   const int kg = lane >> 4, col = lane & 15;
   const int ntiles = (npos + 15) >> 4;
   const int first = start / a.page;
   const PtStage pts = stage_load(a, pt_row, first);
-  auto load_tile = [&](int t, u32x4* bf, long long& off, bool staged) {
+  auto load_tile = [&](int t, u32x4* bf, long long& off) {
     const int jc = min(t * 16 + col, npos - 1);
-    off = staged ? page_off_lds(a, ptl, first, start + jc, kv) : page_off(a, pt_row, start + jc, kv);
+    off = page_off_lds(a, ptl, first, start + jc, kv);
     const uint16_t* kp = k_pages + max(off, 0ll) + 8 * kg;
 #pragma unroll
     for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
   };
-  u32x4 bcur[KS];
-  long long ocur;
-  load_tile(min(wave, max(ntiles - 1, 0)), bcur, ocur, false);
+  const int jc0 = min(min(wave, ntiles - 1) * 16 + col, npos - 1);
+  const int pe0 = pt_row[(start + jc0) / a.page];
 
   // Prologue: wave w owns q heads w, w+4 (G <= 8); with the append, waves 2
   // and 3 also own the new K and V rows.
@@ -199,18 +199,25 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   const bool mine = append && (end == pos + 1);
   float qx[GW][PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
 #pragma unroll
-  for (int u = 0; u < GW; ++u) {
-    const int g = wave + 4 * u;
-    if (g < G) load_slice<PL>(q_raw + ((size_t)b * a.NH + kv * G + g) * D + so, qx[u]);
-  }
+  for (int u = 0; u < GW; ++u)
+    load_slice<PL>(q_raw + ((size_t)b * a.NH + kv * G + min(wave + 4 * u, G - 1)) * D + so, qx[u]);
   load_slice<PL>(q_norm + so, qw);
   load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
   load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
-  if (mine && wave >= 2) {
-    const uint16_t* kr = k_raw + ((size_t)b * a.KV + kv) * D;
-    const uint16_t* vr = (v_raw != nullptr) ? v_raw + ((size_t)b * a.KV + kv) * D : kr;
+  {
+    const uint16_t* kr = mine ? k_raw + ((size_t)b * a.KV + kv) * D : q_norm;
+    const uint16_t* vr = (mine && v_raw != nullptr) ? v_raw + ((size_t)b * a.KV + kv) * D : kr;
     load_slice<PL>((wave == 2 ? kr : vr) + so, kvx);
-    load_slice<PL>(k_norm + so, kw);
+    load_slice<PL>((mine ? k_norm : q_norm) + so, kw);
+  }
+  u32x4 bcur[KS];
+  long long ocur;
+  {
+    const bool valid = pe0 >= 0 && pe0 < a.num_pages;
+    ocur = valid ? ((((long long)pe0 * a.KV + kv) * a.page) + ((start + jc0) % a.page)) * (long long)D : -1ll;
+    const uint16_t* kp = k_pages + max(ocur, 0ll) + 8 * kg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bcur[s] = ld16((const u32x4*)(kp + 32 * s));
   }
   // padding rows G..15 of the A operand are zero
   for (int c = tid; c < (16 - G) * D / 8; c += 256) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
@@ -250,7 +257,9 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   for (int t = wave; t < ntiles; t += 4) {
     u32x4 bnext[KS];
     long long onext;
-    load_tile(min(t + 4, ntiles - 1), bnext, onext, true);  // clamped: always in range
+    // the next tile of this wave, or this tile again on the last pass (a
+    // cache hit, so the barrier after the loop does not wait on HBM)
+    load_tile(t + 4 < ntiles ? t + 4 : t, bnext, onext);
     const int j = t * 16 + col;
     const bool isnew = mine && (start + j == pos);
     if (mine) {
@@ -280,42 +289,37 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
     ocur = onext;
   }
   __syncthreads();
+  // the split's max and sum of exp per head: wave w owns heads w, w+4, so
+  // the heads reduce in parallel and no further barrier is needed
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float m = -INFINITY;
-    for (int j = tid; j < npos; j += 256) m = fmaxf(m, sc[g][j]);
-    m = wave_max_bfly(m);
-    if (lane == 0) redm[wave][g] = m;
-  }
-  __syncthreads();
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m = fmaxf(fmaxf(redm[0][g], redm[1][g]), fmaxf(redm[2][g], redm[3][g]));
-    float* srow = ws_scores + ((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo);
-    float l = 0.0f;
-    for (int j = tid; j < npos; j += 256) {
-      const float s = sc[g][j];
-      l += (s == -INFINITY) ? 0.0f : expf(s - m);
-      srow[j] = s;
+  for (int u = 0; u < GW; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      float m = -INFINITY;
+      for (int j = lane; j < npos; j += 64) m = fmaxf(m, sc[g][j]);
+      m = wave_max_bfly(m);
+      float* srow = ws_scores + ((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo);
+      float l = 0.0f;
+      for (int j = lane; j < npos; j += 64) {
+        const float s = sc[g][j];
+        l += (s == -INFINITY) ? 0.0f : expf(s - m);
+        srow[j] = s;
+      }
+      l = group_sum<64>(l);
+      if (lane == 0) {
+        const int h = kv * G + g;
+        ws_stats[((size_t)b * a.NH + h) * a.n_split_max + split] = m;
+        ws_stats[((size_t)(a.B + b) * a.NH + h) * a.n_split_max + split] = l;
+      }
     }
-    l = group_sum<64>(l);
-    if (lane == 0) redl[wave][g] = l;
-  }
-  __syncthreads();
-  if (tid < G) {
-    const int h = kv * G + tid;
-    const float m = fmaxf(fmaxf(redm[0][tid], redm[1][tid]), fmaxf(redm[2][tid], redm[3][tid]));
-    float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
-    float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
-    sm[split] = m;
-    sl[split] = redl[0][tid] + redl[1][tid] + redl[2][tid] + redl[3][tid];
   }
 }
 
 // ------------------------------------------------------------------ pv + reduce
 // grid (n_split_max, KV, B), 256 threads.  Wave w owns the values
-// [w*D/4, (w+1)*D/4) of every head; LPV = D/32 lanes per position.  The
-// block's V loads are issued before the split statistics are merged.  Each
+// [w*D/4, (w+1)*D/4) of every head; LPV = D/32 lanes per position, the PPV
+// positions of a step in consecutive lanes (their sum is a DPP reduction).
+// The block's V loads are issued before the split statistics are merged.  Each
 // split writes its f32 partial [G, D]; the last split of each group of
 // kGroup to finish sums the group's partials in split order, and with more
 // than one group the last group to finish sums the group sums in order, so
@@ -426,8 +430,9 @@ __device__ __forceinline__ void merge_split_stats(const AttnDims& a, const Range
 // [x*kSliceD, (x+1)*kSliceD) of its G query heads over every attended
 // position, so no partials cross blocks.  LPS lanes (8 dims each) cover a
 // position's slice, a wave takes PPW positions per step and the block PPB.
-// Each lane sums its positions in increasing order, then lanes with the same
-// dims are combined by a butterfly and the four waves in wave order.
+// Each lane sums its positions in increasing order, then the lanes with the
+// same dims (consecutive lanes) are combined by a DPP sum and the four waves
+// in wave order.
 constexpr int kShortLen = 512;
 constexpr int kSliceD = 32;
 
@@ -442,7 +447,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
   constexpr int NST = kShortLen / PPB;       // V steps per lane at most
   constexpr int SPT = G * kShortLen / 256;   // scores per thread at most
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int sub = lane % LPS, slot = lane / LPS;
+  const int slot = lane % PPW, sub = lane / PPW;  // the positions of a step are consecutive lanes
   const int d0 = blockIdx.x * kSliceD + sub * 8;
   const int len = R.len;
   const int nst = (len + PPB - 1) / PPB;
@@ -477,7 +482,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
   for (int r = 0; r < SPT; ++r) {
     const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
     const float sv = sreg[r];
-    pr[g * kShortLen + j] = (j >= len || sv == -INFINITY) ? 0.0f : rbf(expf(sv - mg[g]) / sg[g]);
+    if (j < len) pr[g * kShortLen + j] = (sv == -INFINITY) ? 0.0f : rbf(expf(sv - mg[g]) / sg[g]);
   }
   __syncthreads();
   float acc[G][8];
@@ -499,15 +504,11 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
       }
     }
   }
+  // the PPW positions of a wave step sit in consecutive lanes: a DPP sum
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[g][i];
-#pragma unroll
-      for (int m = LPS; m < 64; m <<= 1) v += __shfl_xor(v, m, kWave);
-      acc[g][i] = v;
-    }
+    for (int i = 0; i < 8; ++i) acc[g][i] = group_sum<PPW>(acc[g][i]);
   if (slot == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g)
@@ -562,7 +563,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
   const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
-  const int sub = lane % LPV, slot = lane / LPV;
+  const int slot = lane % PPV, sub = lane / PPV;  // the positions of a step are consecutive lanes
   const int dofs = wave * (D / 4) + sub * 8;
 
   // this split's scores, the first batch of V rows and (in the merge below)
@@ -646,11 +647,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   for (int g = 0; g < G; ++g) {
     float v[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      v[i] = acc[g][i];
-#pragma unroll
-      for (int m = LPV; m < 64; m <<= 1) v[i] += __shfl_xor(v[i], m, kWave);
-    }
+    for (int i = 0; i < 8; ++i) v[i] = group_sum<PPV>(acc[g][i]);
     if (slot == 0) {
       const uint32_t o = pbase + (uint32_t)(g * D + dofs) * 4;
       coherent_store4(rpart, o, make_float4(v[0], v[1], v[2], v[3]));
