@@ -254,27 +254,19 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
 #pragma unroll
   for (int s = 0; s < KS; ++s) af[s] = *(const u32x4*)(qa + col * D + 32 * s + 8 * kg);
   const float cap = a.softcap;
-  for (int t = wave; t < ntiles; t += 4) {
-    u32x4 bnext[KS];
-    long long onext;
-    // the next tile of this wave, or this tile again on the last pass (a
-    // cache hit, so the barrier after the loop does not wait on HBM)
-    load_tile(t + 4 < ntiles ? t + 4 : t, bnext, onext);
+  // scores of tile t (K rows in bf) into sc
+  auto score_tile = [&](int t, const u32x4* bf, long long off) {
     const int j = t * 16 + col;
     const bool isnew = mine && (start + j == pos);
-    if (mine) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 nv = *(const u32x4*)(kn16 + 32 * s + 8 * kg);
-        bcur[s] = isnew ? nv : bcur[s];
-      }
-    }
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[s]),
-                                                    __builtin_bit_cast(bf16x8, bcur[s]), acc, 0, 0, 0);
-    const bool ok = (ocur >= 0) || isnew;
+    for (int s = 0; s < KS; ++s) {
+      u32x4 kb = bf[s];
+      if (mine) kb = isnew ? *(const u32x4*)(kn16 + 32 * s + 8 * kg) : kb;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[s]), __builtin_bit_cast(bf16x8, kb),
+                                                    acc, 0, 0, 0);
+    }
+    const bool ok = (off >= 0) || isnew;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * kg + i;
@@ -284,6 +276,14 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
         sc[h][j] = ok ? sv : -INFINITY;
       }
     }
+  };
+  for (int t = wave; t < ntiles; t += 4) {
+    u32x4 bnext[KS];
+    long long onext;
+    // the next tile of this wave, or this tile again on the last pass (a
+    // cache hit, so the barrier after the loop does not wait on HBM)
+    load_tile(t + 4 < ntiles ? t + 4 : t, bnext, onext);
+    score_tile(t, bcur, ocur);
 #pragma unroll
     for (int s = 0; s < KS; ++s) bcur[s] = bnext[s];
     ocur = onext;
@@ -379,44 +379,52 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
 }
 
 // Merged softmax statistics of the splits of every head of a KV head into
-// mg/sg (LDS): wave w owns heads w, w+4; lanes stride the splits.  Every
-// head's split statistics are requested before the first reduction
-// (unconditional loads from clamped indices), so the merge costs one round
-// trip.  R.n_eff >= 1.
+// mg/sg (LDS): wave w owns heads w, w+4; lanes stride the splits.
+// load_split_stats requests every head's split statistics (unconditional
+// loads from clamped indices; issue it before any load that waits on a
+// page-table entry), reduce_split_stats merges them.  R.n_eff >= 1.
 template <int G>
-__device__ __forceinline__ void merge_split_stats(const AttnDims& a, const Range& R, int kv, int b, int wave,
-                                                  int lane, const float* __restrict__ ws_stats, float* mg, float* sg) {
-  constexpr int GU = (G + 3) / 4;
-  constexpr int Q = kMaxSplits / 64;
-  float st_m[GU][Q], st_l[GU][Q];
+struct SplitStats {
+  float m[(G + 3) / 4][kMaxSplits / 64], l[(G + 3) / 4][kMaxSplits / 64];
+};
+template <int G>
+__device__ __forceinline__ SplitStats<G> load_split_stats(const AttnDims& a, const Range& R, int kv, int b,
+                                                          int wave, int lane, const float* __restrict__ ws_stats) {
+  SplitStats<G> st;
 #pragma unroll
-  for (int u = 0; u < GU; ++u) {
+  for (int u = 0; u < (G + 3) / 4; ++u) {
     const int h = kv * G + min(wave + 4 * u, G - 1);
     const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
     const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
 #pragma unroll
-    for (int q = 0; q < Q; ++q) {
+    for (int q = 0; q < kMaxSplits / 64; ++q) {
       const int ic = min(lane + 64 * q, R.n_eff - 1);
-      st_m[u][q] = sm[ic];
-      st_l[u][q] = sl[ic];
+      st.m[u][q] = sm[ic];
+      st.l[u][q] = sl[ic];
     }
   }
+  return st;
+}
+template <int G>
+__device__ __forceinline__ void reduce_split_stats(SplitStats<G>& st, const Range& R, int wave, int lane, float* mg,
+                                                   float* sg) {
+  constexpr int Q = kMaxSplits / 64;
 #pragma unroll
-  for (int u = 0; u < GU; ++u) {
+  for (int u = 0; u < (G + 3) / 4; ++u) {
     const int g = wave + 4 * u;
     if (g < G) {
       float m = -INFINITY;
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const bool in = lane + 64 * q < R.n_eff;
-        st_m[u][q] = in ? st_m[u][q] : -INFINITY;
-        st_l[u][q] = in ? st_l[u][q] : 0.0f;
-        m = fmaxf(m, st_m[u][q]);
+        st.m[u][q] = in ? st.m[u][q] : -INFINITY;
+        st.l[u][q] = in ? st.l[u][q] : 0.0f;
+        m = fmaxf(m, st.m[u][q]);
       }
       m = wave_max_bfly(m);
       float t = 0.0f;
 #pragma unroll
-      for (int q = 0; q < Q; ++q) t += (st_m[u][q] == -INFINITY) ? 0.0f : expf(st_m[u][q] - m) * st_l[u][q];
+      for (int q = 0; q < Q; ++q) t += (st.m[u][q] == -INFINITY) ? 0.0f : expf(st.m[u][q] - m) * st.l[u][q];
       t = group_sum<64>(t);
       if (lane == 0) {
         mg[g] = m;
@@ -451,13 +459,21 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
   const int d0 = blockIdx.x * kSliceD + sub * 8;
   const int len = R.len;
   const int nst = (len + PPB - 1) / PPB;
-  // loads first: this block's V slice at every position, then the scores.
-  // Every step's page-table entry is requested before any V row (unconditional
-  // loads from clamped positions), so the V rows cost one round trip after
-  // the entries whatever the number of steps.
+  // Loads first, in this order: every step's page-table entry, the scores
+  // and the split statistics (none waits on anything but pos), then this
+  // block's V slice at every position (unconditional loads from clamped
+  // positions), so the V rows cost one round trip after the entries and the
+  // statistics merge runs while they are in flight.
   int pg[NST];
 #pragma unroll
   for (int st = 0; st < NST; ++st) pg[st] = pt_row[(R.lo + min(st * PPB + wave * PPW + slot, len - 1)) / a.page];
+  float sreg[SPT];
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
+    sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + min(j, len - 1)];
+  }
+  SplitStats<G> sst = load_split_stats<G>(a, R, kv, b, wave, lane, ws_stats);
   u32x4 vv[NST];
   bool ok[NST];
 #pragma unroll
@@ -469,13 +485,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
     vv[st] = ld16((const u32x4*)(v_pages + off + d0));
     ok[st] = (st < nst) && (j < len) && valid;
   }
-  float sreg[SPT];
-#pragma unroll
-  for (int r = 0; r < SPT; ++r) {
-    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
-    sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + min(j, len - 1)];
-  }
-  merge_split_stats<G>(a, R, kv, b, wave, lane, ws_stats, mg, sg);
+  reduce_split_stats<G>(sst, R, wave, lane, mg, sg);
   __syncthreads();
   // normalised probabilities, rounded to bf16 (model.py:212), zero past len
 #pragma unroll
@@ -566,8 +576,8 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const int slot = lane % PPV, sub = lane / PPV;  // the positions of a step are consecutive lanes
   const int dofs = wave * (D / 4) + sub * 8;
 
-  // this split's scores, the first batch of V rows and (in the merge below)
-  // the split statistics are all in flight before the first wait
+  // this split's scores, the split statistics and the first batch of V rows
+  // are all in flight before the first wait
   float sreg[RS];
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
@@ -596,11 +606,12 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
       okv[u] = (j < npos) && valid;
     }
   };
+  SplitStats<G> sst = load_split_stats<G>(a, R, kv, b, wave, lane, ws_stats);
   u32x4 vcur[UB];
   bool okcur[UB];
   vload(0, vcur, okcur, false);
   stage_store(pts, ptl);
-  merge_split_stats<G>(a, R, kv, b, wave, lane, ws_stats, mg, sg);
+  reduce_split_stats<G>(sst, R, wave, lane, mg, sg);
   __syncthreads();
   // normalised probabilities, rounded to bf16 as the reference does (model.py:212)
 #pragma unroll
