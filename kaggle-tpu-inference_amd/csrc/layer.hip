@@ -80,7 +80,7 @@ template <int IT>
 struct PairWalk {
   int p, pend, plast;
   __device__ __forceinline__ PairWalk(int ppb, int npairs) {
-    const int wave = threadIdx.x >> 6;
+    const int wave = wave_id();
     const int p0 = blockIdx.x * ppb;
     p = p0 + wave;
     pend = min(p0 + ppb, npairs);
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void oproj_kernel(const uint16_t* __restrict__
   constexpr int K = 8 * S * IT;
   constexpr int RPW = 64 / S;  // rows per wave step (a "group")
   __shared__ u32x4 xs[K / 8];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, sub = lane % S;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), sub = lane % S;
   const int ngroups = (rows + RPW - 1) / RPW;
   const int g0 = blockIdx.x * groups_per_block;
   const int gend = min(g0 + groups_per_block, ngroups), glast = max(gend - 1, 0);
@@ -222,7 +222,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   constexpr int NCH = H / 8;
   __shared__ u32x4 xs[NCH];
   __shared__ double red[16];
-  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
   const bool dense = (int)blockIdx.x < a.dense_blocks;
   // prologue operands first (see layer_in), then the weight rows
   Vec x, o, wpa, wf, rsc;
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
   constexpr int F = FIT * 64;
   constexpr int NT = kOutThreads;
   extern __shared__ u32x4 act_lds[];  // I/8 chunks
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int h = blockIdx.x * kOutRows + wave;
   const int ich = a.I / 8;
   constexpr int DIT = 8;  // dense chunks per lane, at most (I <= 4096)
@@ -464,7 +464,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   __shared__ double red[16];
   __shared__ float bvs[8];
   __shared__ int bis[8];
-  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
   const int r0 = blockIdx.x * a.rows_per_block;
   const int r1 = min(a.V, r0 + a.rows_per_block);
   // first row pair of this wave, loads issued before the prologue

@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void router_scores_kernel(
   __shared__ u32x4 xs[CH];
   __shared__ double red[4];
   const int tid = threadIdx.x;
-  const int lane = tid & 63, half = lane >> 5, l = lane & 31, wave = tid >> 6;
+  const int lane = tid & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
   const int n = blockIdx.y;
   const int e = blockIdx.x * 8 + wave * 2 + half;
   u32x4 w[IT];
@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void router_scores_generic_kernel(
       xs[i] = f2bf(rbf(rbf(bf2f(xs[i]) * r) * bf2f(scale[i])) * inv_sqrt_h_bf);
     __syncthreads();
   }
-  const int lane = tid & 63, l = lane & 31, wave = tid >> 6;
+  const int lane = tid & 63, l = lane & 31, wave = wave_id();
   const int e = blockIdx.x * 8 + wave * 2 + (lane >> 5);
   if (e < E) {
     const u32x4* row = (const u32x4*)(proj + (size_t)e * H);
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   constexpr int H = IT * 256;
   __shared__ SelectLds L;
   const int lane = threadIdx.x & 63, half = lane >> 5, l = lane & 31;
-  const int task = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int task = blockIdx.x * (blockDim.x >> 6) + wave_id();
   const int n = blockIdx.y;
   const u32x4* xv = (const u32x4*)(x + (size_t)n * H);
   u32x4 xr[IT];
@@ -226,7 +226,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
     int H, int E, int K, int bf16_running, uint16_t* __restrict__ out) {
   constexpr int F = IT * 64;
   const int lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
-  const int h = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const int h = blockIdx.x * (blockDim.x >> 6) + wave_id();
   const int n = blockIdx.y;
   if (h >= H) return;
   float run = 0.0f;
@@ -288,7 +288,7 @@ __global__ __launch_bounds__(256) void router_scores_tile_kernel(const uint16_t*
                                                                  int E, float eps, float inv_sqrt_h_bf,
                                                                  float* __restrict__ scores) {
   extern __shared__ u32x4 xs_rows[];  // kRouterRows x H/8 chunks
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int CH = H / 8;
   const int r0 = blockIdx.x * kRouterRows;
   const u32x4* pw = (const u32x4*)pre_w;
