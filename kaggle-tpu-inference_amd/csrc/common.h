@@ -51,12 +51,19 @@ __device__ __forceinline__ void unpack8(const u32x4 v, float* f) {
   f[6] = bf_lo(v.w); f[7] = bf_hi(v.w);
 }
 
-// f32 dot of 8 bf16 pairs, accumulated into acc in element order.
+// f32 dot of 8 bf16 pairs, accumulated into acc pairwise in element order
+// with v_dot2c_f32_bf16: each step adds two exact bf16 products to acc (one
+// instruction per 4 bytes of each operand instead of unpacking and two FMAs;
+// measured on gfx950: within 2^-23 of the sum of magnitudes of the exact
+// result, round to nearest, like two chained FMAs).
+__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), acc, false);
+}
 __device__ __forceinline__ float dot8(const u32x4 a, const u32x4 b, float acc) {
-  acc = fmaf(bf_lo(a.x), bf_lo(b.x), acc); acc = fmaf(bf_hi(a.x), bf_hi(b.x), acc);
-  acc = fmaf(bf_lo(a.y), bf_lo(b.y), acc); acc = fmaf(bf_hi(a.y), bf_hi(b.y), acc);
-  acc = fmaf(bf_lo(a.z), bf_lo(b.z), acc); acc = fmaf(bf_hi(a.z), bf_hi(b.z), acc);
-  acc = fmaf(bf_lo(a.w), bf_lo(b.w), acc); acc = fmaf(bf_hi(a.w), bf_hi(b.w), acc);
+  acc = dot2bf(a.x, b.x, acc);
+  acc = dot2bf(a.y, b.y, acc);
+  acc = dot2bf(a.z, b.z, acc);
+  acc = dot2bf(a.w, b.w, acc);
   return acc;
 }
 
