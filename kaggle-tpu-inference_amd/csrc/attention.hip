@@ -145,8 +145,10 @@ __device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const 
 // A[l%16][8(l/16)..+7], B[8(l/16)..+7][l%16] (16 contiguous bytes of the K row
 // of position l%16) and gets C[4(l/16)+i][l%16], i < 4.  Wave w takes the
 // 16-position tiles w, w+4, ... of the split; the next tile's K loads are in
-// flight while the current one is multiplied.
-template <int D, int G>
+// flight while the current one is multiplied.  ONE: the launch guarantees
+// at most kChunkMin positions per split (one tile per wave), so there is
+// nothing to prefetch.
+template <int D, int G, bool ONE>
 __global__ __launch_bounds__(256) void attn_qk_kernel(
     AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
     const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
@@ -277,16 +279,20 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
       }
     }
   };
-  for (int t = wave; t < ntiles; t += 4) {
-    u32x4 bnext[KS];
-    long long onext;
-    // the next tile of this wave, or this tile again on the last pass (a
-    // cache hit, so the barrier after the loop does not wait on HBM)
-    load_tile(t + 4 < ntiles ? t + 4 : t, bnext, onext);
-    score_tile(t, bcur, ocur);
+  if constexpr (ONE) {
+    if (wave < ntiles) score_tile(wave, bcur, ocur);
+  } else {
+    for (int t = wave; t < ntiles; t += 4) {
+      u32x4 bnext[KS];
+      long long onext;
+      // the next tile of this wave, or this tile again on the last pass (a
+      // cache hit, so the barrier after the loop does not wait on HBM)
+      load_tile(t + 4 < ntiles ? t + 4 : t, bnext, onext);
+      score_tile(t, bcur, ocur);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) bcur[s] = bnext[s];
-    ocur = onext;
+      for (int s = 0; s < KS; ++s) bcur[s] = bnext[s];
+      ocur = onext;
+    }
   }
   __syncthreads();
   // the split's max and sum of exp per head: wave w owns heads w, w+4, so
@@ -741,8 +747,14 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
                         const uint16_t* v_raw, const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* cs,
                         const uint16_t* sn, uint16_t* kp, uint16_t* vp, const int32_t* pt, const int32_t* pos,
                         int append, const AttnWs& w, uint16_t* ctx) {
-  hipLaunchKernelGGL((attn_qk_kernel<D, G>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm, cs, sn,
-                     kp, vp, pt, pos, append, w.scores, w.stats);
+  // every split holds at most kChunkMin positions when the longest range does
+  const int span = (a.window > 0 && a.window < a.lmax) ? a.window : a.lmax;
+  if (span <= kChunkMin * a.n_split_max)
+    hipLaunchKernelGGL((attn_qk_kernel<D, G, true>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm,
+                       cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
+  else
+    hipLaunchKernelGGL((attn_qk_kernel<D, G, false>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm,
+                       cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
   const dim3 pgrid(max(grid.x, (unsigned)(D / kSliceD)), grid.y, grid.z);  // short ranges use D / kSliceD blocks
   hipLaunchKernelGGL((attn_pv_kernel<D, G>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
                      w.group, w.counters, ctx);
