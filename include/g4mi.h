@@ -299,6 +299,20 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
                      const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
                      void* ws, int64_t ws_bytes, void* stream);
 
+/* The experts of a batched decode step (model.py:262-294 for each of n <= 16
+ * tokens): the routing's (token, slot) pairs are grouped by expert, and each
+ * selected expert's gate/up and down rows stream from HBM once for every
+ * token that chose it (GEMV row walks over the union of the routed experts);
+ * then the per-token combine in slot order, G4MI_COMBINE_BF16_RUNNING (the
+ * decode path) or G4MI_COMBINE_F32.  act and the down partials equal
+ * g4mi_moe_gateup / g4mi_moe_down's.  xn [n, H], top_w/top_i [n, K],
+ * gate_up [E, 2, F, H], down [E, H, F] -> out [n, H] bf16.  Workspace:
+ * g4mi_moe_prefill_workspace_bytes(n, K, E, F, H).  H = 256*i (i <= 16),
+ * F = 64*j (j <= 16). */
+int g4mi_moe_decode_grouped(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
+                            const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K,
+                            int32_t combine, uint16_t* out, void* ws, int64_t ws_bytes, void* stream);
+
 /* Row kernels between the batched prefill GEMMs, one token row of H <= 4096
  * per block, with the decode kernels' rounding recipe:
  *  rows_embed:     x = bf16(embed[tok] * bf16(sqrt(H))) (model.py:355-357),

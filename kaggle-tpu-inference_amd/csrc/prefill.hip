@@ -86,19 +86,121 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   }
 }
 
-// out[t, h] = bf16(sum over s < K, in order, of part[slot_pos[t*K + s], h]) (f32)
+// out[t, h] = bf16(sum over s < K, in order, of part[slot_pos[t*K + s], h]) (f32),
+// or with `running` the decode combine: a bf16 running sum of bf16(part) in
+// slot order (model.py:289-293)
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ part,
                                                           const int32_t* __restrict__ slot_pos, int n, int K, int H,
-                                                          uint16_t* __restrict__ out) {
+                                                          int running, uint16_t* __restrict__ out) {
   const int t = blockIdx.y;
   const int h = blockIdx.x * 256 + threadIdx.x;
   if (t >= n || h >= H) return;
   float s = 0.0f;
+  bool first = true;
   for (int q = 0; q < K; ++q) {
     const int p = slot_pos[t * K + q];
-    if (p >= 0) s += part[(size_t)p * H + h];
+    if (p < 0) continue;
+    const float v = part[(size_t)p * H + h];
+    if (running) {
+      const float b = rbf(v);
+      s = first ? b : rbf(s + b);
+    } else {
+      s += v;
+    }
+    first = false;
   }
   out[(size_t)t * H + h] = f2bf(s);
+}
+
+// ------------------------------------------------------------------ grouped decode experts
+// A decode step of n <= 16 tokens with their routing (model.py:262-294 per
+// token): after moe_sort_kernel every expert's (token, slot) pairs form one
+// tile, so each selected expert's rows stream from HBM once for all the
+// tokens that chose it, as GEMV row walks (the union of the routed experts,
+// not one read per pair).  The dot products use the decode kernels' lane
+// layout and order, so act and the partials equal moe_gateup / moe_down's.
+constexpr int kGrpPairs = 4;   // gate/up row pairs per wave
+constexpr int kGrpDownRows = 2;  // down rows per 8-lane group
+
+// act[p, f] = bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w_sorted[p]))
+// for the pairs p of tile blockIdx.x; wave w of block y takes row pairs
+// f = (4y + w) * kGrpPairs + r (lanes 0-31 the gate row, 32-63 the up row).
+template <int IT>
+__global__ __launch_bounds__(256) void moe_gateup_grouped_kernel(const uint16_t* __restrict__ xn,
+                                                                 const uint16_t* __restrict__ gate_up,
+                                                                 const int32_t* __restrict__ a_rows,
+                                                                 const float* __restrict__ w_sorted,
+                                                                 const int32_t* __restrict__ tiles,
+                                                                 const int32_t* __restrict__ ntiles, int F,
+                                                                 uint16_t* __restrict__ act) {
+  constexpr int H = IT * 256;
+  const int tile = blockIdx.x;
+  if (tile >= ntiles[0]) return;
+  const int e = tiles[3 * tile], m0 = tiles[3 * tile + 1], m1 = tiles[3 * tile + 2];
+  const int lane = threadIdx.x & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
+  const int fb = (blockIdx.y * 4 + wave) * kGrpPairs;
+  u32x4 w[kGrpPairs][IT];
+#pragma unroll
+  for (int r = 0; r < kGrpPairs; ++r) {
+    const u32x4* row = (const u32x4*)(gate_up + ((size_t)(e * 2 + half) * F + min(fb + r, F - 1)) * H);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[r][i] = ld_stream(row + l + 32 * i);
+  }
+  for (int p = m0; p < m1; ++p) {
+    const u32x4* xv = (const u32x4*)(xn + (size_t)a_rows[p] * H);
+    u32x4 xr[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) xr[i] = ld16(xv + l + 32 * i);
+    const float wt = rbf(w_sorted[p]);
+#pragma unroll
+    for (int r = 0; r < kGrpPairs; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int i = 0; i < IT; ++i) acc = dot8(w[r][i], xr[i], acc);
+      acc = group_sum<32>(acc);
+      const float up = __shfl(acc, 32, kWave);
+      if (lane == 0 && fb + r < F)
+        act[(size_t)p * F + fb + r] = f2bf(rbf(rbf(rbf(gelu_tanh(rbf(acc))) * rbf(up)) * wt));
+    }
+  }
+}
+
+// part[p, h] = act[p] . down[e, h] (f32) for the pairs p of tile blockIdx.x;
+// 8-lane group g of wave w in block y takes rows h = ((4y + w) * 8 + g) *
+// kGrpDownRows + r.
+template <int FIT>
+__global__ __launch_bounds__(256) void moe_down_grouped_kernel(const uint16_t* __restrict__ act,
+                                                               const uint16_t* __restrict__ down,
+                                                               const int32_t* __restrict__ tiles,
+                                                               const int32_t* __restrict__ ntiles, int H,
+                                                               float* __restrict__ part) {
+  constexpr int F = FIT * 64;
+  const int tile = blockIdx.x;
+  if (tile >= ntiles[0]) return;
+  const int e = tiles[3 * tile], m0 = tiles[3 * tile + 1], m1 = tiles[3 * tile + 2];
+  const int lane = threadIdx.x & 63, g = lane >> 3, l8 = lane & 7, wave = wave_id();
+  const int hb = ((blockIdx.y * 4 + wave) * 8 + g) * kGrpDownRows;
+  u32x4 wd[kGrpDownRows][FIT];
+#pragma unroll
+  for (int r = 0; r < kGrpDownRows; ++r) {
+    const u32x4* row = (const u32x4*)(down + ((size_t)e * H + min(hb + r, H - 1)) * F);
+#pragma unroll
+    for (int i = 0; i < FIT; ++i) wd[r][i] = ld_stream(row + l8 + 8 * i);
+  }
+  for (int p = m0; p < m1; ++p) {
+    const u32x4* av = (const u32x4*)(act + (size_t)p * F);
+    u32x4 ar[FIT];
+#pragma unroll
+    for (int i = 0; i < FIT; ++i) ar[i] = ld16(av + l8 + 8 * i);
+#pragma unroll
+    for (int r = 0; r < kGrpDownRows; ++r) {
+      float d = 0.0f;
+#pragma unroll
+      for (int i = 0; i < FIT; ++i) d = dot8(wd[r][i], ar[i], d);
+      d = group_sum<8>(d);
+      if (l8 == 0 && hb + r < H) part[(size_t)p * H + hb + r] = d;
+    }
+  }
 }
 
 // ------------------------------------------------------------------ row kernels
@@ -250,8 +352,57 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
                       H, nullptr, 1, nullptr, 0, stream);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
-                     w.slot_pos, (int)n, (int)K, (int)H, out);
+                     w.slot_pos, (int)n, (int)K, (int)H, 0, out);
   return check_launch("moe_prefill combine");
+}
+
+int g4mi_moe_decode_grouped(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
+                            const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K,
+                            int32_t combine, uint16_t* out, void* ws, int64_t ws_bytes, void* stream) {
+  G4MI_REQUIRE(xn && top_w && top_i && gate_up && down && out && ws, G4MI_EINVAL,
+               "moe_decode_grouped: missing argument");
+  G4MI_REQUIRE(n >= 1 && n <= 16 && K >= 1 && K <= 32 && E >= 1 && E <= kMaxExperts, G4MI_EINVAL,
+               "moe_decode_grouped: n=%lld (at most 16 tokens), K=%lld, E=%lld", (long long)n, (long long)K,
+               (long long)E);
+  G4MI_REQUIRE(H % 256 == 0 && H / 256 <= 16 && F % 64 == 0 && F / 64 >= 1 && F / 64 <= 16, G4MI_EUNSUPPORTED,
+               "moe_decode_grouped: H=%lld must be 256*i (i <= 16), F=%lld 64*j (j <= 16)", (long long)H,
+               (long long)F);
+  G4MI_REQUIRE(combine == 0 || combine == 1, G4MI_EINVAL, "moe_decode_grouped: bad combine %d", combine);
+  G4MI_REQUIRE(((uintptr_t)xn & 15u) == 0 && ((uintptr_t)gate_up & 15u) == 0 && ((uintptr_t)down & 15u) == 0,
+               G4MI_EALIGN, "moe_decode_grouped: operands must be 16-byte aligned");
+  G4MI_REQUIRE(ws_bytes >= g4mi_moe_prefill_workspace_bytes(n, K, E, F, H), G4MI_EWORKSPACE,
+               "moe_decode_grouped: workspace too small (g4mi_moe_prefill_workspace_bytes)");
+  hipStream_t st = as_stream(stream);
+  const MoePrefillWs w = moe_prefill_ws(ws, n, K, E, F, H);
+  // at most n <= 16 pairs per expert: one tile per selected expert
+  const int tiles = (int)(n * K < E ? n * K : E);
+  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, (int)n, (int)K, (int)E, w.a_rows,
+                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles);
+  const dim3 ggrid((unsigned)tiles, (unsigned)((F + 4 * kGrpPairs - 1) / (4 * kGrpPairs)));
+  switch (H / 256) {
+#define G4MI_GU(I)                                                                                             \
+  case I:                                                                                                      \
+    hipLaunchKernelGGL(moe_gateup_grouped_kernel<I>, ggrid, dim3(256), 0, st, xn, gate_up, w.a_rows, w.w_sorted, \
+                       w.tiles, w.ntiles, (int)F, w.act);                                                     \
+    break;
+    G4MI_GU(1) G4MI_GU(2) G4MI_GU(3) G4MI_GU(4) G4MI_GU(5) G4MI_GU(6) G4MI_GU(7) G4MI_GU(8)
+    G4MI_GU(9) G4MI_GU(10) G4MI_GU(11) G4MI_GU(12) G4MI_GU(13) G4MI_GU(14) G4MI_GU(15) G4MI_GU(16)
+#undef G4MI_GU
+  }
+  const dim3 dgrid((unsigned)tiles, (unsigned)((H + 32 * kGrpDownRows - 1) / (32 * kGrpDownRows)));
+  switch (F / 64) {
+#define G4MI_DN(I)                                                                                              \
+  case I:                                                                                                       \
+    hipLaunchKernelGGL(moe_down_grouped_kernel<I>, dgrid, dim3(256), 0, st, w.act, down, w.tiles, w.ntiles,     \
+                       (int)H, w.part);                                                                         \
+    break;
+    G4MI_DN(1) G4MI_DN(2) G4MI_DN(3) G4MI_DN(4) G4MI_DN(5) G4MI_DN(6) G4MI_DN(7) G4MI_DN(8)
+    G4MI_DN(9) G4MI_DN(10) G4MI_DN(11) G4MI_DN(12) G4MI_DN(13) G4MI_DN(14) G4MI_DN(15) G4MI_DN(16)
+#undef G4MI_DN
+  }
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
+                     w.slot_pos, (int)n, (int)K, (int)H, combine == 0 ? 1 : 0, out);
+  return check_launch("moe_decode_grouped");
 }
 
 int g4mi_rows_embed(const int32_t* tok, int64_t n, const uint16_t* embed, int64_t vocab, const uint16_t* input_ln,

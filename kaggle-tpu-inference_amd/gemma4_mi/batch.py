@@ -118,6 +118,12 @@ class BatchDecodeRunner:
             ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(
                 B, cfg.num_attention_heads, cfg.head_dim_for(lt), self.max_len, ns))
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        # the grouped experts (g4mi_moe_decode_grouped) read each selected expert
+        # once per step; the per-pair kernels read it once per (row, slot) and
+        # let the MALL serve the repeats.  Measured on the 26B shapes at ~8K
+        # positions: 8 rows 1149 (per pair) vs 1128 tok/s (grouped: a sort and
+        # a combine launch more), 16 rows 1414 vs 1604 tok/s.
+        self.grouped_moe = B > 8
 
     def launch(self) -> None:
         ops, cfg, p = self.ops, self.cfg, self.params
@@ -159,8 +165,12 @@ class BatchDecodeRunner:
             if moe:
                 ops.moe_router_topk(self.xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],
                                     cfg.top_k_experts, eps, out=(self.top_w, self.top_i))
-                ops.moe_gateup(self.xe, lp["experts.gate_up_proj"], self.top_w, self.top_i, act=self.act_moe)
-                ops.moe_down(self.act_moe, lp["experts.down_proj"], self.top_i, "bf16_running", out=self.moe_out)
+                if self.grouped_moe and B <= 16:  # each selected expert's rows once for all rows that chose it
+                    ops.moe_decode_grouped(self.xe, self.top_w, self.top_i, lp["experts.gate_up_proj"],
+                                           lp["experts.down_proj"], "bf16_running", out=self.moe_out)
+                else:
+                    ops.moe_gateup(self.xe, lp["experts.gate_up_proj"], self.top_w, self.top_i, act=self.act_moe)
+                    ops.moe_down(self.act_moe, lp["experts.down_proj"], self.top_i, "bf16_running", out=self.moe_out)
             nxt = self.layers[i + 1]["input_layernorm"] if i + 1 < L else p["norm"]
             ops.rows_tail(self.x1, self.mlp_out, self.moe_out, lp.get("post_feedforward_layernorm_1"),
                           lp.get("post_feedforward_layernorm_2"), lp["post_feedforward_layernorm"],

@@ -500,6 +500,30 @@ def gemm_segments(a, bs, outs):
     return outs
 
 
+def moe_decode_grouped(xn, top_w, top_i, gate_up, down, combine="bf16_running", out=None, ws=None):
+    """The experts of a decode step of n <= 16 tokens (model.py:262-294 per
+    token) with each selected expert's rows read once for all the tokens
+    that chose it: xn [n, H], top_w/top_i [n, K] -> out [n, H] bf16."""
+    n, H = xn.shape
+    E, _, F, _ = gate_up.shape
+    K = top_i.shape[1]
+    _need(xn, BF16, "xn")
+    _need(top_w, torch.float32, "top_w", (n, K))
+    _need(top_i, torch.int32, "top_i", (n, K))
+    _need(gate_up, BF16, "gate_up", (E, 2, F, H))
+    _need(down, BF16, "down", (E, H, F))
+    if out is None:
+        out = torch.empty((n, H), dtype=BF16, device=xn.device)
+    _need(out, BF16, "out", (n, H))
+    nbytes = int(_lib.lib().g4mi_moe_prefill_workspace_bytes(n, K, E, F, H))
+    if ws is None:
+        ws = WORKSPACE.get(xn.device, "moe_decode_grouped", nbytes)
+    mode = {"bf16_running": _lib.COMBINE_BF16_RUNNING, "f32": _lib.COMBINE_F32}[combine]
+    _lib.call("g4mi_moe_decode_grouped", _ptr(xn), _ptr(top_w), _ptr(top_i), _ptr(gate_up), _ptr(down), n, H, F, E,
+              K, mode, _ptr(out), _ptr(ws), ws.numel(), stream_handle(xn.device))
+    return out
+
+
 def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
     """model.py:241-250 for xn [n, H]: out [n, H] bf16 (selected experts only,
     grouped MFMA GEMMs)."""

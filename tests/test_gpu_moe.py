@@ -1,5 +1,5 @@
-"""GPU parity of the MoE decode block (router/top-k, expert GEMVs, combine)
-against the CPU oracle, on the isolated-block workload (hidden 2816, 128
+"""GPU parity of the MoE decode block (router/top-k, expert GEMVs, combine,
+and the batched decode's grouped experts) against the CPU oracle, on the isolated-block workload (hidden 2816, 128
 experts top-8, width 704, seed 1, batches 1/4/8) and on the tiny model's
 shapes.  Also checks the device weight generator bit for bit against its
 numpy restatement.
@@ -117,6 +117,47 @@ def test_experts_decode_c2(c2, n):
     torch.cuda.synchronize()
     exp = twin.moe(cfg, cpu, x.cpu(), dense=False)
     _check_out(out, exp, f"experts decode n={n}")
+
+
+@pytest.mark.parametrize("n", [2, 8, 16])
+def test_grouped_decode_experts_equal_pair_path_c2(c2, n):
+    """The batched decode's grouped experts (each selected expert's rows read
+    once for all the tokens that chose it) compute the same act and partial
+    dot products as the per-(token, slot) kernels, so the output is
+    bit-identical to moe_experts for both combines; rows 1 and 3 repeat row 0
+    so that some experts serve several tokens."""
+    cfg, g, cpu = c2
+    x = _gen((n, cfg.hidden_size), 1, f"xg.n{n}", 1.0)
+    x[1] = x[0]
+    if n > 3:
+        x[3] = x[0]
+    tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                 cfg.top_k_experts, cfg.rms_norm_eps)
+    gu, dn = g["experts.gate_up_proj"], g["experts.down_proj"]
+    for combine in ("bf16_running", "f32"):
+        ref = ops.moe_experts(x, gu, dn, tw, ti, combine=combine)
+        got = ops.moe_decode_grouped(x, tw, ti, gu, dn, combine=combine)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (n, combine)
+    _check_out(got, _dense_selected(cfg, cpu, x.cpu()), f"grouped experts f32 combine n={n}")
+
+
+def test_grouped_decode_experts_tiny_shapes():
+    """Tiny-model expert shapes (hidden 256, 16 experts top-4, width 128) at
+    16 tokens: 64 pairs over at most 16 experts."""
+    cfg = tiny_parity_config()
+    h, e, f = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size
+    gu = _gen((e, 2, f, h), 7, "tiny.gate_up", 0.02)
+    dn = _gen((e, h, f), 7, "tiny.down", 0.02)
+    x = _gen((16, h), 7, "tiny.x", 1.0)
+    rng = np.random.default_rng(7)
+    ti = torch.tensor(np.stack([rng.permutation(e)[: cfg.top_k_experts] for _ in range(16)]), dtype=torch.int32,
+                      device=DEV)
+    tw = torch.tensor(rng.random((16, cfg.top_k_experts)), dtype=torch.float32, device=DEV)
+    ref = ops.moe_experts(x, gu, dn, tw, ti)
+    got = ops.moe_decode_grouped(x, tw, ti, gu, dn)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
 
 
 def _dense_selected(cfg, lp, x):
