@@ -42,6 +42,28 @@ def test_batched_decode_matches_single_sequence_oracle():
         assert div is None or div >= 8
 
 
+def test_batched_decode_above_eight_rows_uses_grouped_experts():
+    """Ten rows (the grouped expert path, each selected expert read once per
+    step): rows holding the same prompt produce the same tokens, and each
+    distinct prompt's tokens follow the single-sequence oracle (first token
+    equal, no divergence before step 8)."""
+    cfg = tiny_parity_config()
+    params = init_random_params(cfg, 0, device=DEV)
+    params_cpu = twin.random_params(cfg, 0)
+    base = [np.random.default_rng(20 + i).integers(0, cfg.vocab_size, size=n).tolist()
+            for i, n in enumerate((33, 64, 95))]
+    prompts = [base[i % 3] for i in range(10)]
+    eng = BatchEngine(cfg, params, batch=10, max_len=192, device=DEV)
+    assert eng.runner.grouped_moe
+    got = eng.generate(prompts, 10)
+    for b in range(10):
+        assert got[b] == got[b % 3], b
+    for i, pr in enumerate(base):
+        _, exp = twin.prefill_then_decode(cfg, params_cpu, pr, 9, 192)
+        div = next((j for j, (x, y) in enumerate(zip(got[i], exp)) if x != y), None)
+        assert got[i][0] == exp[0] and (div is None or div >= 8), (i, div)
+
+
 def test_batched_rows_are_independent():
     """Row b's tokens do not depend on what the other rows hold: a batch of
     [A, B, A] yields the same stream for both A rows."""
