@@ -103,12 +103,17 @@ def test_batched_prefill_matches_oracle(c1):
     then the head: the
     first-token logits against the oracle's last prefill row (same bar as
     above), and the K/V cache of every layer against the oracle's prefill
-    cache: corr >= 0.9999 and >= 99% of elements bit-identical (the GPU GEMMs
-    accumulate in f32, the oracle in f64; a flipped bf16 rounding in one
-    layer's hidden state moves later layers' K/V by an ulp here and there).
-    The token-at-a-time prefill's cache is printed beside it and held to
-    corr >= 0.9999 (its GEMV reductions drift further: ~85% identical by the
-    last layer)."""
+    cache: corr >= 0.9999 in every layer, and >= 99% of elements
+    bit-identical in the first layer, whose K/V are one GEMM away from the
+    embedding.  Past the first layer the bit-identical fraction is chaotic,
+    not a precision measure: the GPU GEMMs accumulate in f32 and the oracle
+    in f64, so ~1e-4 of each product's bf16 roundings flip, and a flipped
+    K or V element reaches every query row of its attention window.  Which
+    elements flip depends on the summation order: over the prompts of seeds
+    0-3 the last layer's K ranges from 76% to 99.96% identical for one-pass
+    f32 sums and from 85% to 99.96% for two-slice split-K sums, each order
+    winning on some seeds.  The token-at-a-time prefill's cache is printed
+    beside it and held to the same corr bar."""
     cfg, params_cpu, params, prompt, logits_o, gen_o, _ = c1
     cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
     r = gm.DecodeRunner(cfg, params, cache, device=DEV)
@@ -142,7 +147,7 @@ def test_batched_prefill_matches_oracle(c1):
                 c = np.corrcoef(g, o)[0, 1]
                 print(f"layer {i} {kind} {name}: identical {same:.4f} corr {c:.7f}")
                 assert c >= 0.9999, (i, kind, name, c)
-                if name == "batched":
+                if name == "batched" and i == 0:
                     assert same >= 0.99, (i, kind, same)
 
 

@@ -10,7 +10,9 @@ GEMM (g4mi_gemm_bf16) against float64 products of the same bf16 operands:
   * the gated epilogue against the same rounding points built from f64 gate
     and up values (model.py:220, 246-247): >= 97% bit-identical, corr >= 0.9999
     (a one-ulp flip of a rounded gate or up moves the product by one ulp).
-Cases: plain 128x128 tiles with ragged edges, small M with split-K (the
+Cases: the library GEMM (rocBLAS) the batched prefill uses above 16 rows,
+and its gated path (two products and gated_act); plain 128x128 tiles with
+ragged edges, small M with split-K (the
 slices are summed in order, so split-K equals the one-slice result within
 f32 reassociation), the skinny kernel (M <= 16) alone and with column
 segments (several weight matrices sharing A in one launch), row gather,
@@ -139,6 +141,34 @@ def _close_bf16(got, ref, same_min=0.97):
     same = (g == r).float().mean().item()
     corr = np.corrcoef(g.flatten().numpy(), r.flatten().numpy())[0, 1]
     assert same >= same_min and corr >= 0.9999, (same, corr)
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 2816), (300, 1000, 2112), (17, 2816, 4096)])
+def test_gemm_library_bf16_and_f32(m, n, k):
+    """The library GEMM (rocBLAS, atomics disallowed) that the batched prefill
+    uses above 16 rows, to the same bounds as the MFMA kernel; repeated calls
+    are bit-identical."""
+    a, b = _rand((m, k), 16), _rand((n, k), 17, 0.02)
+    ref, absum = _ref(a, b)
+    ad, bd = a.to(DEV), b.to(DEV)
+    out = ops.gemm_library(ad, bd)
+    _check_bf16(out, ref, absum)
+    assert torch.equal(ops.gemm_library(ad, bd).view(torch.int16), out.view(torch.int16))
+    _check_f32(ops.gemm_library(ad, bd, f32_out=True), ref, absum)
+
+
+@pytest.mark.parametrize("m", [17, 300])
+def test_prefill_gemm_gated_through_library(m):
+    """Above 16 rows prefill_gemm's gated epilogue is two library products and
+    gated_act: the same rounding points as the fused epilogue."""
+    h, f = 2816, 2112
+    a = _rand((m, h), 18)
+    gate, up = _rand((f, h), 19, 0.02), _rand((f, h), 20, 0.02)
+    gd, ud = gate.to(DEV), up.to(DEV)
+    out = torch.empty((m, f), dtype=torch.bfloat16, device=DEV)
+    ops.prefill_gemm(a.to(DEV), gd, out, epilogue=ops.EP_GATED, pair_offset=(ud.data_ptr() - gd.data_ptr()) // 2,
+                     n=f, up=ud)
+    _close_bf16(out, _gated_ref(a, gate, up, None))
 
 
 @pytest.mark.parametrize("m", [5, 64, 300])
