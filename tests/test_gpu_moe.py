@@ -291,3 +291,28 @@ def test_router_scores_many_rows_match_row_path(c2):
                                                 cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, 67, 8)])
         torch.cuda.synchronize()
         assert torch.equal(many, rows), (pw is None, (many != rows).sum().item())
+
+
+@pytest.mark.parametrize("e,k,n", [(128, 8, 64), (16, 4, 64), (256, 32, 16), (200, 8, 16)])
+def test_wave_selection_equals_block_selection(e, k, n):
+    """The selection every gate/up block makes from the router scores
+    (moe_block) against the standalone selection kernel (moe_router_topk) on
+    the same scores: expert indices and weights bit-identical.  The
+    per-expert scale is not all ones (the weight picks up the selected
+    expert's scale), E runs from 16 to 256 (one to four waves of experts, the
+    last one ragged at 200), and bf16 scores tie within most rows."""
+    h, f = 256, 64
+    proj = _gen((e, h), 7, f"sel.proj{e}", 0.05)
+    scale = _gen((h,), 7, f"sel.scale{e}", 1.0)
+    pes = (1.0 + _gen((e,), 7, f"sel.pes{e}", 1.0).float().abs()).to(torch.bfloat16)
+    gate_up = _gen((e, 2, f, h), 7, f"sel.gu{e}", 0.02)
+    down = _gen((e, h, f), 7, f"sel.dn{e}", 0.02)
+    x = _gen((n, h), 8, f"sel.x{e}", 1.0)
+    tw_b, ti_b = ops.moe_router_topk(x, scale, proj, pes, k, 1e-6)
+    _, tw_w, ti_w = ops.moe_block(x, scale, proj, pes, gate_up, down, k, 1e-6)
+    s = ops.moe_router_scores(x, scale, proj, 1e-6)
+    torch.cuda.synchronize()
+    tied = sum(len(r) != len(set(r)) for r in s.cpu().numpy().tolist())
+    print(f"E={e} k={k}: {tied} of {n} rows hold tied scores")
+    assert torch.equal(ti_b, ti_w)
+    assert torch.equal(tw_b.view(torch.int32), tw_w.view(torch.int32))
