@@ -32,6 +32,10 @@ Workloads (--workload):
              8) at --prompt-len positions each (8192 for the prefill +
              batched-decode configuration), --steps batched steps; value =
              aggregate tok/s.
+  attention  isolated decode attention at position 32,767 (seed 2, softcap
+             50): the sliding layer (16 q / 8 KV heads, head_dim 256, window
+             1024) and the full k==v layer (16 q / 2 KV heads, head_dim 512);
+             value = the full layer's GB/s of attended K/V bytes.
 """
 
 from __future__ import annotations
@@ -231,6 +235,82 @@ def run_moe_block(args) -> dict:
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = wl.cpu_baseline(args.cpu_seconds)
     return res
+
+
+def run_attention(args) -> dict:
+    """Isolated decode attention, one query token at position 32,767 (seed 2),
+    RoPE and softcap 50, over a paged bf16 cache (64-position pages) filled
+    with N(0, 1):
+      (a) sliding layer: 16 q / 8 KV heads, head_dim 256, window 1024;
+      (b) full layer: 16 q / 2 KV heads, head_dim 512, k==v, 32,768 cached
+          positions (K and V rows stored separately, as the decode step does).
+    Each case is the decode step's call (append of the new K/V row, then the
+    split qk and pv kernels), --steps launches captured in HIP graphs and
+    timed with HIP events.  Algorithmic bytes per launch: the attended K and V
+    rows, 2 * positions * KV * D * 2 B.  value = (b)'s GB/s."""
+    import torch
+    from gemma4_mi import model as gm
+    from gemma4_mi import ops
+    from gemma4_mi.weights import tensor_key
+
+    dev, seed, lmax, page, pos = "cuda:0", 2, 32768, 64, 32767
+    cases = {
+        "sliding": dict(NH=16, KV=8, D=256, window=1024, k_eq_v=False, theta=1e4, partial=1.0),
+        "full": dict(NH=16, KV=2, D=512, window=0, k_eq_v=True, theta=1e6, partial=0.25),
+    }
+    steps = args.steps
+    G = _chunk(steps)
+    out = {}
+    for name, c in cases.items():
+        NH, KV, D = c["NH"], c["KV"], c["D"]
+
+        def gen(shape, tag, std=1.0):
+            t = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+            ops.fill_normal_(t, tensor_key(seed, f"attn.{name}.{tag}"), std)
+            return t
+
+        q_raw, k_raw = gen((1, NH, D), "q"), gen((1, KV, D), "k")
+        v_raw = None if c["k_eq_v"] else gen((1, KV, D), "v")
+        q_norm, k_norm = gen((D,), "q_norm", 0.5), gen((D,), "k_norm", 0.5)
+        cos, sin = gm.rope_table(D, c["theta"], c["partial"], lmax, dev)
+        pages = lmax // page
+        kp, vp = gen((pages, KV, page, D), "cache_k"), gen((pages, KV, page, D), "cache_v")
+        pt = torch.arange(pages, dtype=torch.int32, device=dev).view(1, pages)
+        p_t = torch.tensor([pos], dtype=torch.int32, device=dev)
+        span = min(pos + 1, c["window"]) if c["window"] else pos + 1
+        ns = gm.decode_splits(KV, span)  # the decode step's split count for this layer
+        ctx = torch.empty((1, NH, D), dtype=torch.bfloat16, device=dev)
+        ws = torch.zeros(int(ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, NH, D, lmax, ns)),
+                         dtype=torch.uint8, device=dev)
+
+        def call():
+            ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, pt, p_t, c["window"], 50.0,
+                                 1e-6, lmax, n_split_max=ns, append=True, ctx=ctx, ws=ws)
+
+        g = _capture(lambda: [call() for _ in range(G)])
+        _time_graph(g, max(1, args.warmup // G))
+        us = _time_graph(g, steps // G) / steps * 1e3
+        nbytes = 2 * span * KV * D * 2
+        out[name] = {"heads": NH, "kv_heads": KV, "head_dim": D, "window": c["window"], "k_eq_v": c["k_eq_v"],
+                     "positions_attended": span, "splits": ns, "us_per_launch": us, "bytes_per_launch": nbytes,
+                     "gbs": nbytes / (us * 1e-6) / 1e9}
+        _log(f"attention {name}: {us:.2f} us, {out[name]['gbs']:.0f} GB/s")
+        del kp, vp
+    full = out["full"]
+    return {
+        "metric": "isolated decode attention GB/s (full layer, 32K positions)",
+        "value": full["gbs"],
+        "unit": "GB/s",
+        "ms_per_step": full["us_per_launch"] * 1e-3,
+        "dtype": "bf16",
+        "config": {"workload": "isolated decode attention at position 32767, softcap 50, seed 2", **out,
+                   "launch": "HIP graph"},
+        "roofline": {
+            "kernel": "attn_qk + attn_pv (full layer, 32K positions)", "bound": "hbm", "achieved": full["gbs"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": full["gbs"] / HBM_PEAK_GBS, "traffic": None,
+            "bytes_per_launch": full["bytes_per_launch"], "avg_launch_us": full["us_per_launch"],
+        },
+    }
 
 
 def run_copy(args) -> dict:
@@ -619,7 +699,7 @@ def run_batch_decode(args) -> dict:
 
 
 WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup,
-             "prefill": run_prefill, "batch_decode": run_batch_decode}
+             "prefill": run_prefill, "batch_decode": run_batch_decode, "attention": run_attention}
 
 
 def main() -> int:

@@ -556,7 +556,6 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   constexpr int kLdsF = (G * kShortLen + 4 * G * kSliceD > G * kChunkMax) ? G * kShortLen + 4 * G * kSliceD
                                                                           : G * kChunkMax;
   __shared__ float lds_f[kLdsF];
-  float(*pr)[kChunkMax] = reinterpret_cast<float(*)[kChunkMax]>(lds_f);
   __shared__ float mg[G], sg[G];
   __shared__ int flag;
   __shared__ int ptl[512];
@@ -619,14 +618,20 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   stage_store(pts, ptl);
   reduce_split_stats<G>(sst, R, wave, lane, mg, sg);
   __syncthreads();
-  // normalised probabilities, rounded to bf16 as the reference does (model.py:212)
+  // normalised probabilities, rounded to bf16 as the reference does
+  // (model.py:212), stored as bf16 pairs: the positions of wave steps 2q and
+  // 2q + 1 at lane slot `sl` share word q * PPV + sl (zero past npos)
+  uint16_t* pr16 = reinterpret_cast<uint16_t*>(lds_f);
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
     const int idx = tid + 256 * r, g = idx / kChunkMax, j = idx % kChunkMax;
     const float s = sreg[r];
-    if (j < npos) pr[g][j] = (s == -INFINITY) ? 0.0f : rbf(expf(s - mg[g]) / sg[g]);
+    const float pv = (j < npos && s != -INFINITY) ? rbf(expf(s - mg[g]) / sg[g]) : 0.0f;
+    const int step = j / PPV, sl = j % PPV;
+    pr16[g * kChunkMax + ((step >> 1) * PPV + sl) * 2 + (step & 1)] = f2bf(pv);
   }
   __syncthreads();
+  const uint32_t* pr32 = reinterpret_cast<const uint32_t*>(lds_f);
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -636,16 +641,28 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
     u32x4 vnext[UB];
     bool oknext[UB];
     if (st0 + UB < nsteps) vload(st0 + UB, vnext, oknext, true);
+    // two wave steps at a time: each dim's values at the two positions form
+    // one bf16 pair, dotted with the pair of probabilities (v_dot2c_f32_bf16;
+    // the products are exact, the pair is added to acc with one rounding)
 #pragma unroll
-    for (int u = 0; u < UB; ++u) {
-      const int j = (st0 + u) * PPV + slot;
-      float vf[8];
-      unpack8(vcur[u], vf);
+    for (int u = 0; u < UB; u += 2) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 va = okcur[u] ? vcur[u] : z, vb = okcur[u + 1] ? vcur[u + 1] : z;
+      uint32_t vp[8];
+      vp[0] = __builtin_amdgcn_perm(vb.x, va.x, 0x05040100u);
+      vp[1] = __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u);
+      vp[2] = __builtin_amdgcn_perm(vb.y, va.y, 0x05040100u);
+      vp[3] = __builtin_amdgcn_perm(vb.y, va.y, 0x07060302u);
+      vp[4] = __builtin_amdgcn_perm(vb.z, va.z, 0x05040100u);
+      vp[5] = __builtin_amdgcn_perm(vb.z, va.z, 0x07060302u);
+      vp[6] = __builtin_amdgcn_perm(vb.w, va.w, 0x05040100u);
+      vp[7] = __builtin_amdgcn_perm(vb.w, va.w, 0x07060302u);
+      const int pi = ((st0 + u) >> 1) * PPV + slot;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float p = okcur[u] ? pr[g][min(j, npos - 1)] : 0.0f;
+        const uint32_t pp = pr32[g * (kChunkMax / 2) + pi];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(p, vf[i], acc[g][i]);
+        for (int i = 0; i < 8; ++i) acc[g][i] = dot2bf(vp[i], pp, acc[g][i]);
       }
     }
     if (st0 + UB < nsteps) {

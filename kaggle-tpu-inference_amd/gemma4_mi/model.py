@@ -77,6 +77,16 @@ def rope_inv_freq(head_dim: int, theta: float, partial_rotary_factor: float = 1.
     return inv.astype(np.float32)
 
 
+def decode_splits(kv_heads: int, span: int) -> int:
+    """Split count of the decode attention for a layer whose rows attend to at
+    most `span` positions: ~256 blocks per KV pass at full length (one split
+    per 64 positions below that), never fewer than the kernel's minimum."""
+    from . import ops
+
+    want = max(1, 256 // kv_heads)
+    return max(ops.attention_min_splits(span), min(want, (span + 63) // 64))
+
+
 def rope_table(head_dim: int, theta: float, partial: float, max_pos: int, device="cuda"):
     """(cos, sin) bf16 tables [max_pos, head_dim/2] of the angles
     f32(pos) * inv_freq (f32 product, model.py:65); each entry is the f64
@@ -228,11 +238,8 @@ class DecodeRunner:
 
     def _splits(self, lt: str) -> int:
         cfg = self.cfg
-        kv = cfg.kv_heads_for(lt)
         span = min(cfg.sliding_window, self.max_len) if lt == SLIDING else self.max_len
-        want = max(1, 256 // kv)  # ~256 blocks per KV pass at full length
-        need = self.ops.attention_min_splits(span)
-        return max(need, min(want, (span + 63) // 64))
+        return decode_splits(cfg.kv_heads_for(lt), span)
 
     def launch(self, combine: str = "bf16_running", advance: bool = True, sampler=None, feed=None):
         """Enqueues one token step reading tok/pos.
