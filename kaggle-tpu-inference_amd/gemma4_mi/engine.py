@@ -241,6 +241,12 @@ class Engine:
         out = {}
         toks = torch.zeros((1, bucket), dtype=torch.int32)
         t0 = time.perf_counter()
+        if self.prefill_mode == "batched":
+            # prompts of more than 16 rows run their dense products through the
+            # ROCm library GEMM, which creates its handle and loads its kernel
+            # code objects on first use: do that here, not in the first request
+            for n in sorted({min(32, bucket), bucket}):
+                self.prefill_fn(bucket)(self.params, toks, self.cache, n, 0, 0.0, 1.0)
         tok, self.cache, pos = self.prefill_fn(bucket)(self.params, toks, self.cache, 4, 0, 0.0, 1.0)
         if self.prefill_mode == "stepwise":
             self._graph("head", False)

@@ -277,18 +277,20 @@ def test_moe_block_tiny_and_f32_combine():
 
 
 def test_router_scores_many_rows_match_row_path(c2):
-    """N >= 32 rows take the tiled router kernel (8 rows per block, every
-    expert); its scores equal the per-row kernel's (N < 32) bit for bit (both
-    sum exact bf16 products in f64 and round once), with and without the
-    pre_feedforward_layernorm_2 pre-norm."""
+    """N >= 1024 rows take the tiled router kernel (8 rows per block, every
+    expert); its scores equal the per-row kernel's (fewer rows) bit for bit
+    (both sum exact bf16 products in f64 and round once), with and without
+    the pre_feedforward_layernorm_2 pre-norm; 1,031 rows leave a ragged last
+    tile."""
     cfg, g, _ = c2
     h, e = cfg.hidden_size, cfg.num_experts
-    x = _gen((67, h), 9, "router.rows", 1.0)
+    n = 1031
+    x = _gen((n, h), 9, "router.rows", 1.0)
     pre = _gen((h,), 9, "router.pre", 0.5)
     for pw in (None, pre):
         many = ops.moe_router_scores(x, g["router.scale"], g["router.proj"], cfg.rms_norm_eps, pre_norm_w=pw)
-        rows = torch.cat([ops.moe_router_scores(x[i:i + 8].contiguous(), g["router.scale"], g["router.proj"],
-                                                cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, 67, 8)])
+        rows = torch.cat([ops.moe_router_scores(x[i:i + 256].contiguous(), g["router.scale"], g["router.proj"],
+                                                cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, n, 256)])
         torch.cuda.synchronize()
         assert torch.equal(many, rows), (pw is None, (many != rows).sum().item())
 
