@@ -164,31 +164,50 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
 }
 
 // ------------------------------------------------------------------ oproj
-// out[H] = ctx[K] . W[H, K]; S lanes per row (64/S rows per wave).
+// out[H] = ctx[K] . W[H, K]; S lanes per row (64/S rows per wave).  Each wave
+// requests its first kOprojPrefetch row groups before ctx reaches LDS (ctx is
+// loaded into registers first: loads complete in issue order, so the LDS
+// store waits for ctx alone), then refills a group as it consumes one.
+constexpr int kOprojPrefetch = 3;  // the 26B o_proj: 2,816 rows over 235 blocks is 3 rows per wave
+
 template <int S, int IT>
 __global__ __launch_bounds__(256) void oproj_kernel(const uint16_t* __restrict__ ctx, const uint16_t* __restrict__ W,
                                                     int rows, int groups_per_block, uint16_t* __restrict__ out) {
   constexpr int K = 8 * S * IT;
   constexpr int RPW = 64 / S;  // rows per wave step (a "group")
+  constexpr int CPT = (K / 8 + 255) / 256;  // ctx chunks per thread
+  constexpr int NPF = kOprojPrefetch;
   __shared__ u32x4 xs[K / 8];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), sub = lane % S;
   const int ngroups = (rows + RPW - 1) / RPW;
   const int g0 = blockIdx.x * groups_per_block;
   const int gend = min(g0 + groups_per_block, ngroups), glast = max(gend - 1, 0);
-  int gi = g0 + wave;
   auto rowp = [&](int grp) { return W + (size_t)min(grp * RPW + lane / S, rows - 1) * K; };
-  for (int c = tid; c < K / 8; c += 256) xs[c] = ld16((const u32x4*)ctx + c);
-  u32x4 w[IT];
-  load_row<S, IT>(rowp(min(gi, glast)), sub, w);
-  __syncthreads();
-  for (; gi < gend; gi += 4) {
-    u32x4 wn[IT];
-    load_row<S, IT>(rowp(min(gi + 4, glast)), sub, wn);
-    const float acc = dot_row<S, IT>(w, xs, sub);
-    const int r = gi * RPW + lane / S;
-    if (r < rows && sub == 0) out[r] = f2bf(acc);
+  u32x4 cv[CPT];
 #pragma unroll
-    for (int i = 0; i < IT; ++i) w[i] = wn[i];
+  for (int j = 0; j < CPT; ++j) cv[j] = ld16((const u32x4*)ctx + min(tid + 256 * j, K / 8 - 1));
+  int gi = g0 + wave;
+  u32x4 w[NPF][IT];
+#pragma unroll
+  for (int d = 0; d < NPF; ++d) load_row<S, IT>(rowp(min(gi + 4 * d, glast)), sub, w[d]);
+#pragma unroll
+  for (int j = 0; j < CPT; ++j)
+    if (tid + 256 * j < K / 8) xs[tid + 256 * j] = cv[j];
+  __syncthreads();
+  for (; gi + 4 * NPF < gend; gi += 4 * NPF) {
+#pragma unroll
+    for (int d = 0; d < NPF; ++d) {
+      const float acc = dot_row<S, IT>(w[d], xs, sub);
+      const int r = (gi + 4 * d) * RPW + lane / S;
+      if (r < rows && sub == 0) out[r] = f2bf(acc);
+      load_row<S, IT>(rowp(min(gi + 4 * d + 4 * NPF, glast)), sub, w[d]);
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < NPF; ++d) {
+    const float acc = dot_row<S, IT>(w[d], xs, sub);
+    const int r = (gi + 4 * d) * RPW + lane / S;
+    if (gi + 4 * d < gend && r < rows && sub == 0) out[r] = f2bf(acc);
   }
 }
 

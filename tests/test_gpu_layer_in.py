@@ -63,3 +63,22 @@ def test_layer_in_tail_matches_oracle(h, moe, rows):
     ref = (xn.double() @ torch.cat([wq, wk] + ([wv] if wv is not None else [])).double().T)
     err = (out1.cpu().double() - ref).abs().max().item()
     assert err <= ref.abs().max().item() * 2.0 ** -7
+
+
+@pytest.mark.parametrize("rows,k", [(2816, 4096), (2816, 8192), (256, 256), (1001, 512), (37, 1024)])
+def test_oproj_matches_f64_products(rows, k):
+    """The decode o_proj GEMV (out = ctx . W^T, one bf16 rounding of an f32
+    dot) against the f64 product: every element within one bf16 rounding plus
+    the f32 accumulation bound, >= 99% equal to the rounded f64 value.  The
+    26B sliding (4096) and full (8192) widths, the tiny model's, and row
+    counts that leave partial row groups."""
+    g = torch.Generator().manual_seed(rows + k)
+    ctx, w = _r((k,), g), _r((rows, k), g, 0.02)
+    out = torch.empty(rows, dtype=torch.bfloat16, device=DEV)
+    ops.oproj(ctx.to(DEV), w.to(DEV), rows, k, out)
+    torch.cuda.synchronize()
+    ref = w.double() @ ctx.double()
+    absum = w.double().abs() @ ctx.double().abs()
+    got = out.cpu().double()
+    assert bool(((got - ref).abs() <= ref.abs() * 2.0 ** -8 + absum * 2.0 ** -16).all())
+    assert (out.cpu() == twin.rb(ref)).float().mean().item() >= 0.99
