@@ -776,7 +776,19 @@ int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint1
   return check_launch("ffn_out");
 }
 
-int64_t g4mi_lm_head_blocks(int64_t V) { return (V + 255) / 256; }
+// lm_head rows per block: the vocabulary in about 3 * gemv_blocks() blocks,
+// the number resident at once (3 per CU at 148 VGPRs), so no second, partial
+// round of blocks trails the stream; a multiple of the 8 rows a block step takes
+static int lm_rows_per_block(int64_t V) {
+  const int64_t nb = 3 * (int64_t)gemv_blocks();
+  const int64_t r = ((V + nb - 1) / nb + 7) / 8 * 8;
+  return (int)std::max<int64_t>(8, r);
+}
+
+int64_t g4mi_lm_head_blocks(int64_t V) {
+  const int r = lm_rows_per_block(V);
+  return (V + r - 1) / r;
+}
 
 int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* moe_out, const uint16_t* post_ff1_ln,
                  const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln, const uint16_t* layer_scalar,
@@ -792,7 +804,7 @@ int g4mi_lm_head(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* mo
   LmArgs a;
   a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
   a.w_norm = final_norm; a.embed = embed; a.V = (int)V; a.softcap = softcap; a.logits = logits;
-  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = 256; a.H = (int)H; a.eps = eps;
+  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = lm_rows_per_block(V); a.H = (int)H; a.eps = eps;
   dim3 grid((unsigned)g4mi_lm_head_blocks(V));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {
@@ -811,7 +823,7 @@ int g4mi_lm_head_normed(const uint16_t* xn, const uint16_t* embed, int64_t V, in
                "lm_head_normed: H=%lld must be 256*i, i <= 16", (long long)H);
   LmArgs a = {};
   a.xn = xn; a.embed = embed; a.V = (int)V; a.softcap = softcap; a.logits = logits;
-  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = 256; a.H = (int)H;
+  a.blk_val = blk_val; a.blk_idx = blk_idx; a.rows_per_block = lm_rows_per_block(V); a.H = (int)H;
   dim3 grid((unsigned)g4mi_lm_head_blocks(V));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {

@@ -72,8 +72,10 @@ def test_host_size_helpers(lib):
     assert lib.g4mi_attention_min_splits(32768) == 128
     assert lib.g4mi_attention_min_splits(1024) == 4
     assert lib.g4mi_attention_min_splits(1) == 1
-    assert lib.g4mi_lm_head_blocks(262144) == 1024
-    assert lib.g4mi_lm_head_blocks(4097) == 17
+    # the vocabulary over ~3 blocks per CU (768), rows per block a multiple of 8
+    assert lib.g4mi_lm_head_blocks(262144) == 763  # 344 rows per block
+    assert lib.g4mi_lm_head_blocks(4097) == 513  # 8 rows per block
+    assert lib.g4mi_lm_head_blocks(1) == 1
     assert lib.g4mi_moe_router_workspace_bytes(1, 128) == 512
     assert lib.g4mi_moe_router_workspace_bytes(3, 16) == 256
     assert lib.g4mi_moe_experts_workspace_bytes(8, 704, 8) == 8 * 8 * 704 * 2
