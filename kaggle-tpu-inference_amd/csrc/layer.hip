@@ -218,7 +218,7 @@ struct FfnInArgs {
   const uint16_t *gate, *up;   // dense MLP [I, H]
   int I;
   uint16_t* act_mlp;           // [I]
-  int dense_blocks;            // blocks [0, dense_blocks) do dense rows
+  int dense_blocks;            // the last dense_blocks blocks do dense rows (router blocks first)
   int tasks_per_block;         // dense (gate, up) row pairs per dense block
   const uint16_t *r_scale, *r_proj;  // router (null: no MoE)
   int E;
@@ -242,7 +242,10 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   __shared__ u32x4 xs[NCH];
   __shared__ double red[16];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
-  const bool dense = (int)blockIdx.x < a.dense_blocks;
+  // router blocks come first in dispatch order: the router and the expert
+  // selection are this kernel's longest chain
+  const int rblocks = (int)gridDim.x - a.dense_blocks;
+  const bool dense = (int)blockIdx.x >= rblocks;
   // prologue operands first (see layer_in), then the weight rows
   Vec x, o, wpa, wf, rsc;
   vload(o, a.o, NCH);
@@ -252,9 +255,9 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   if (!dense) vload(rsc, a.r_scale, NCH);
   // dense: this block owns tasks (one (gate, up) row pair each) [t0, tend),
   // wave w takes t0+w, t0+w+4, ...; router blocks own 8 expert rows each.
-  const int t0 = blockIdx.x * a.tasks_per_block;
+  const int t0 = ((int)blockIdx.x - rblocks) * a.tasks_per_block;
   const int tend = min(t0 + a.tasks_per_block, a.I), tlast = max(tend - 1, 0);
-  const int e = (blockIdx.x - a.dense_blocks) * 8 + wave * 2 + half;
+  const int e = (int)blockIdx.x * 8 + wave * 2 + half;
   auto dense_row = [&](int f) { return (half ? a.up : a.gate) + (size_t)f * H; };
   // every task of this wave (t0 + wave + 4j, j < kFfnInTasks) is requested
   // before the prologue; router blocks request their one row
@@ -274,7 +277,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   } else {
     Vec xe = x;
     vscale_w(xe, r1, wf);
-    if (blockIdx.x == a.dense_blocks) vstore(xe, (u32x4*)a.xe_out, NCH);
+    if (blockIdx.x == 0) vstore(xe, (u32x4*)a.xe_out, NCH);
     // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
     const float r2 = vrms(xe, H, a.eps, red);
 #pragma unroll
@@ -325,7 +328,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     // once, so the expert kernel starts from the routing instead of the scores
     __shared__ SelectLds L;
     __shared__ int flag;
-    if (!arrive_last(a.counter, (unsigned)(gridDim.x - a.dense_blocks), &flag)) return;
+    if (!arrive_last(a.counter, (unsigned)rblocks, &flag)) return;
     const int t = threadIdx.x;
     const float sv = (t < a.E) ? __hip_atomic_load(a.scores + min(t, a.E - 1), __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT)
