@@ -128,9 +128,11 @@ int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, cons
  * g4mi_attention_min_splits(span) <= n_split_max <= 256, span = window (when
  * 0 < window < lmax) else lmax (a split holds <= 256 positions, so span <=
  * 65536).  A position outside [0, lmax) attends to nothing (ctx = 0).  The
- * workspace holds arrival counters: zero-fill it once before first use (each
- * call leaves the counters at zero); concurrent calls need separate
- * workspaces. */
+ * workspace starts with arrival counters: zero-fill it once before first use
+ * (each call leaves the counters at zero).  Calls may share a workspace when
+ * they have the same B and NH (their counters coincide; the rest is scratch),
+ * e.g. the sliding and full layers of one decode step; concurrent calls need
+ * separate workspaces. */
 int64_t g4mi_attention_min_splits(int64_t lmax);
 int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max);
 int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,

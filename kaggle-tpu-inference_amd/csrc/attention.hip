@@ -785,9 +785,13 @@ using namespace g4mi;
 
 extern "C" {
 
+// Workspace layout: the arrival counters first, so calls with the same B and
+// NH find them at the same place whatever their head_dim, lmax and split
+// count (the decode step shares one workspace between its sliding and full
+// layers); then scores, split statistics, split partials, group partials.
 int64_t g4mi_decode_attention_workspace_bytes(int64_t B, int64_t NH, int64_t D, int64_t lmax, int64_t n_split_max) {
-  return al256(B * NH * lmax * 4) + al256(2 * B * NH * n_split_max * 4) + al256(B * n_split_max * NH * D * 4) +
-         al256(B * kMaxGroups * NH * D * 4) + al256(B * NH * (kMaxGroups + 1) * 4);
+  return al256(B * NH * (kMaxGroups + 1) * 4) + al256(B * NH * lmax * 4) + al256(2 * B * NH * n_split_max * 4) +
+         al256(B * n_split_max * NH * D * 4) + al256(B * kMaxGroups * NH * D * 4);
 }
 
 int64_t g4mi_attention_min_splits(int64_t lmax) { return (lmax + kChunkMax - 1) / kChunkMax; }
@@ -827,11 +831,11 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
   a.max_pages = (int)max_pages; a.num_pages = (int)num_pages; a.window = (int)window;
   a.n_split_max = (int)n_split_max; a.lmax = (int)lmax; a.softcap = softcap; a.eps = eps;
   AttnWs w;
-  w.scores = (float*)ws;
+  w.counters = (unsigned int*)ws;
+  w.scores = (float*)((char*)ws + al256(B * NH * (kMaxGroups + 1) * 4));
   w.stats = (float*)((char*)w.scores + al256(B * NH * lmax * 4));
   w.part = (float*)((char*)w.stats + al256(2 * B * NH * n_split_max * 4));
   w.group = (float*)((char*)w.part + al256(B * n_split_max * NH * D * 4));
-  w.counters = (unsigned int*)((char*)w.group + al256(B * kMaxGroups * NH * D * 4));
   hipStream_t st = as_stream(stream);
   dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
 #define G4MI_ATT(DD, GG)                                                                                         \

@@ -303,7 +303,10 @@ def decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_
     _need(ctx, BF16, "ctx", (b, nh, d))
     nbytes = _lib.lib().g4mi_decode_attention_workspace_bytes(b, nh, d, lmax, n_split_max)
     if ws is None:
+        # the shared scratch buffer may have held another layout (other B or
+        # NH put data where this call's arrival counters sit): zero it
         ws = WORKSPACE.get(q_raw.device, "attention", nbytes)
+        ws[:nbytes].zero_()
     _lib.call("g4mi_decode_attention", _ptr(q_raw), _ptr(k_raw), _ptr(v_raw), _ptr(q_norm), _ptr(k_norm),
               _ptr(rope_cos), _ptr(rope_sin), _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table), max_pages,
               _ptr(pos), b, nh, kv, d, page, int(window), float(softcap or 0.0), float(eps), 1 if append else 0,

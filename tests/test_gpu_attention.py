@@ -182,3 +182,35 @@ def test_out_of_range_position_attends_to_nothing():
     torch.cuda.synchronize()
     assert torch.count_nonzero(ctx).item() == 0
     assert torch.equal(kp, kp0) and torch.equal(vp, vp0)
+
+
+def test_sliding_and_full_layers_share_one_workspace():
+    """The decode step hands its sliding layers (head_dim 256, 16 splits) and
+    full layers (head_dim 512, 128 splits) one workspace.  Its arrival
+    counters sit at the start for any head_dim, lmax and split count, so
+    alternating the two layouts at positions where both use split partials
+    (1,500 and 20,000: the full layer writes partials of 79 splits) gives the
+    same results as a fresh workspace per call."""
+    lmax, page, seed, eps, NH = 32768, 64, 6, 1e-6, 16
+    layers = []
+    for D, KV, window, theta, partial, ns in ((256, 8, 1024, 1e4, 1.0, 16), (512, 2, 0, 1e6, 0.25, 128)):
+        q_raw, k_raw = _gen((1, NH, D), seed, f"q{D}"), _gen((1, KV, D), seed, f"k{D}")
+        v_raw = _gen((1, KV, D), seed, f"v{D}") if window else None
+        qn, kn = _gen((D,), seed, f"qn{D}", 0.5), _gen((D,), seed, f"kn{D}", 0.5)
+        cos, sin = gm.rope_table(D, theta, partial, lmax, DEV)
+        kp = _gen((lmax // page, KV, page, D), seed, f"pk{D}")
+        vp = _gen((lmax // page, KV, page, D), seed, f"pv{D}")
+        layers.append((D, window, ns, q_raw, k_raw, v_raw, qn, kn, cos, sin, kp, vp))
+    nbytes = max(ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, NH, L[0], lmax, L[2]) for L in layers)
+    shared = torch.zeros(nbytes, dtype=torch.uint8, device=DEV)
+    pt = torch.arange(lmax // page, dtype=torch.int32, device=DEV).view(1, -1)
+    for p in (1500, 20000, 1500):
+        pos = torch.tensor([p], dtype=torch.int32, device=DEV)
+        for (D, window, ns, q_raw, k_raw, v_raw, qn, kn, cos, sin, kp, vp) in layers + layers:
+            got = ops.decode_attention(q_raw, k_raw, v_raw, qn, kn, cos, sin, kp, vp, pt, pos, window, 50.0, eps,
+                                       lmax, n_split_max=ns, ws=shared)
+            fresh = torch.zeros_like(shared)
+            exp = ops.decode_attention(q_raw, k_raw, v_raw, qn, kn, cos, sin, kp, vp, pt, pos, window, 50.0, eps,
+                                       lmax, n_split_max=ns, ws=fresh)
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), exp.view(torch.int16)), (p, D)
