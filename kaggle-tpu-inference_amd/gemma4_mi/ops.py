@@ -611,7 +611,7 @@ def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256,
     N = n if n is not None else w.shape[0]
     if M > 16 and epilogue in (EP_BF16, EP_F32) and out.stride(1) == 1 and w.is_contiguous():
         return gemm_library(a, w.reshape(-1, K)[:N], out=out, f32_out=epilogue == EP_F32)
-    if M > 16 and epilogue == EP_GATED and up is not None and out.is_contiguous() and w.is_contiguous():
+    if M > 16 and epilogue == EP_GATED and up is not None and N % 8 == 0 and out.is_contiguous() and w.is_contiguous():
         tmp = WORKSPACE.get(a.device, "gated_gu", 2 * M * N * 2).view(BF16)[: 2 * M * N].view(2, M, N)
         gemm_library(a, w.reshape(-1, K)[:N], out=tmp[0])
         gemm_library(a, up.reshape(-1, K)[:N], out=tmp[1])
