@@ -31,6 +31,7 @@ extern "C" int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_r
 namespace g4mi {
 
 constexpr int kTileRows = 128;  // grouped GEMM tile height (gemm.hip's grouped tiles)
+constexpr int kSortIpt = 16;    // routing items per thread per chunk in moe_sort_kernel
 constexpr int kMaxExperts = 256;
 
 // One block.  entries i = t*K + s (token t, slot s) of the routing.
@@ -47,9 +48,19 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   for (int e = tid; e < E; e += blockDim.x) cnt[e] = 0;
   __syncthreads();
   const int total = n * K;
-  for (int i = tid; i < total; i += blockDim.x) {
-    const int e = top_i[i];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  // items in chunks of kSortIpt per thread: each chunk's loads are all in
+  // flight before its LDS atomics (one memory round trip per chunk, not per item)
+  const int stride = (int)blockDim.x;
+  for (int i0 = 0; i0 < total; i0 += stride * kSortIpt) {
+    int ev[kSortIpt];
+#pragma unroll
+    for (int u = 0; u < kSortIpt; ++u) {
+      const int i = i0 + u * stride + tid;
+      ev[u] = (i < total) ? top_i[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kSortIpt; ++u)
+      if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[ev[u]], 1);
   }
   __syncthreads();
   if (tid == 0) {
@@ -64,15 +75,28 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
     ntiles[0] = to;
   }
   __syncthreads();
-  for (int i = tid; i < total; i += blockDim.x) {
-    const int e = top_i[i];
-    if (e >= 0 && e < E) {
-      const int p = off[e] + atomicAdd(&cur[e], 1);
-      a_rows[p] = i / K;
-      w_sorted[p] = top_w[i];
-      slot_pos[i] = p;
-    } else {
-      slot_pos[i] = -1;
+  for (int i0 = 0; i0 < total; i0 += stride * kSortIpt) {
+    int ev[kSortIpt];
+    float wv[kSortIpt];
+#pragma unroll
+    for (int u = 0; u < kSortIpt; ++u) {
+      const int i = i0 + u * stride + tid;
+      ev[u] = (i < total) ? top_i[i] : -1;
+      wv[u] = (i < total) ? top_w[i] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kSortIpt; ++u) {
+      const int i = i0 + u * stride + tid;
+      if (i >= total) continue;
+      const int e = ev[u];
+      if (e >= 0 && e < E) {
+        const int p = off[e] + atomicAdd(&cur[e], 1);
+        a_rows[p] = i / K;
+        w_sorted[p] = wv[u];
+        slot_pos[i] = p;
+      } else {
+        slot_pos[i] = -1;
+      }
     }
   }
   for (int e = tid; e < E; e += blockDim.x) {
