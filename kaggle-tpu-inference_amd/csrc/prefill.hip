@@ -116,24 +116,41 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float* __restrict__ part,
                                                           const int32_t* __restrict__ slot_pos, int n, int K, int H,
                                                           int running, uint16_t* __restrict__ out) {
+  // four consecutive h per thread (H % 4 == 0): every slot's float4 is
+  // requested before the first is added
   const int t = blockIdx.y;
-  const int h = blockIdx.x * 256 + threadIdx.x;
+  const int h = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (t >= n || h >= H) return;
-  float s = 0.0f;
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   bool first = true;
-  for (int q = 0; q < K; ++q) {
-    const int p = slot_pos[t * K + q];
-    if (p < 0) continue;
-    const float v = part[(size_t)p * H + h];
-    if (running) {
-      const float b = rbf(v);
-      s = first ? b : rbf(s + b);
-    } else {
-      s += v;
+  for (int q0 = 0; q0 < K; q0 += 8) {
+    float4 v[8];
+    int pv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      pv[u] = (q0 + u < K) ? slot_pos[t * K + q0 + u] : -1;
+      v[u] = *(const float4*)(part + (size_t)max(pv[u], 0) * H + h);
     }
-    first = false;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (pv[u] < 0) continue;
+      const float x[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (running) {
+          const float b = rbf(x[i]);
+          s[i] = first ? b : rbf(s[i] + b);
+        } else {
+          s[i] += x[i];
+        }
+      }
+      first = false;
+    }
   }
-  out[(size_t)t * H + h] = f2bf(s);
+  uint2 o;
+  o.x = pack2(s[0], s[1]);
+  o.y = pack2(s[2], s[3]);
+  *(uint2*)(out + (size_t)t * H + h) = o;
 }
 
 // ------------------------------------------------------------------ grouped decode experts
@@ -375,7 +392,7 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
   rc = g4mi_gemm_bf16(w.act, F, nullptr, down, F, H * F, 0, n * K, H, F, w.tiles, w.ntiles, max_tiles, 1, w.part,
                       H, nullptr, 1, nullptr, 0, stream);
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
                      w.slot_pos, (int)n, (int)K, (int)H, 0, out);
   return check_launch("moe_prefill combine");
 }
@@ -424,7 +441,7 @@ int g4mi_moe_decode_grouped(const uint16_t* xn, const float* top_w, const int32_
     G4MI_DN(9) G4MI_DN(10) G4MI_DN(11) G4MI_DN(12) G4MI_DN(13) G4MI_DN(14) G4MI_DN(15) G4MI_DN(16)
 #undef G4MI_DN
   }
-  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
+  hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
                      w.slot_pos, (int)n, (int)K, (int)H, combine == 0 ? 1 : 0, out);
   return check_launch("moe_decode_grouped");
 }
