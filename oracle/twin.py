@@ -239,17 +239,50 @@ def router(cfg, lp, flat, precise=True):
     return top_w, top_i
 
 
-def moe(cfg, lp, flat, dense: bool, precise=True, return_route=False):
+def moe_dense_selected(cfg, flat, top_w, top_i, gate_up, down, precise=True):
+    """model.py:241-250 (the dense-MoE contraction) evaluated on the selected
+    (token, expert) pairs only.  An unselected expert's routing weight is 0,
+    so its activation is bf16(x * 0) = 0 exactly and it adds exact zeros to
+    the contraction over experts: the result is the dense path's (up to the
+    order of the f64 sum before its rounding), at k/E of the products.
+    flat [N,H] bf16, top_w [N,k] f32, top_i [N,k] int -> [N,H] bf16."""
+    n_tok, k = top_i.shape
+    f = gate_up.shape[2]
+    acts = torch.zeros((n_tok, k, f), dtype=BF16)
+    ti = top_i.long()
+    experts = torch.unique(ti).tolist()
+    for e in experts:
+        rows, slots = (ti == e).nonzero(as_tuple=True)
+        gu = ein("nh,cfh->ncf", flat[rows], gate_up[e], precise)
+        act = rb(f32(gelu(gu[:, 0])) * f32(gu[:, 1]))
+        acts[rows, slots] = rb(f32(act) * f32(rb(top_w[rows, slots]))[:, None])
+    acc = torch.zeros((n_tok, down.shape[1]), dtype=torch.float64 if precise else torch.float32)
+    for e in experts:
+        rows, slots = (ti == e).nonzero(as_tuple=True)
+        a = acts[rows, slots]
+        if precise:
+            acc.index_add_(0, rows, a.double() @ down[e].double().T)
+        else:
+            acc.index_add_(0, rows, (a @ down[e].to(BF16).T).float())
+    return rb(acc)
+
+
+def moe(cfg, lp, flat, dense, precise=True, return_route=False):
     """model.py:235-294.  flat [N,H] bf16 (pre_feedforward_layernorm_2 output).
 
     dense=True: all experts for every token as one contraction masked by the
-    routing weight (model.py:241-250).  dense=False: the default "slice" decode
-    path, a bf16 running sum over the selected experts in top-k order
-    (model.py:262-294)."""
+    routing weight (model.py:241-250).  dense="selected": the same
+    contraction restricted to the selected experts (moe_dense_selected).
+    dense=False: the default "slice" decode path, a bf16 running sum over the
+    selected experts in top-k order (model.py:262-294)."""
     top_w, top_i = router(cfg, lp, flat, precise)
     gate_up, down = lp["experts.gate_up_proj"], lp["experts.down_proj"]
     n_tok = flat.shape[0]
-    if dense:
+    if isinstance(dense, str):
+        if dense != "selected":
+            raise ValueError(f"dense={dense!r}")
+        out = moe_dense_selected(cfg, flat, top_w, top_i, gate_up, down, precise)
+    elif dense:
         w_full = torch.zeros((n_tok, cfg.num_experts), dtype=torch.float32)
         w_full.scatter_(1, top_i, top_w)
         gu = ein("nh,ecfh->necf", flat, gate_up, precise)
@@ -347,22 +380,29 @@ def greedy(logits: torch.Tensor) -> int:
 
 
 # ----------------------------------------------------------------- drivers
-def prefill_then_decode(cfg, params, prompt, n_decode: int, max_len: int, precise=True, trace=None):
+def prefill_then_decode(cfg, params, prompt, n_decode: int, max_len: int, precise=True, trace=None,
+                        all_logits: bool = True, prefill_dense=True, forced=None):
     """The engine's call pattern (engine.py:149-221) with greedy sampling and no
     bucket padding (padded positions are never attended): dense-MoE prefill of
-    the whole prompt with every position's logits, then n_decode greedy steps.
-    Returns (logits [P + n_decode, V] f32, tokens generated [n_decode + 1])."""
+    the whole prompt with every position's logits (only the last prompt
+    row's with all_logits=False), then n_decode greedy steps.  prefill_dense
+    is passed to moe() as `dense` for the prompt rows.  With `forced` (a
+    token list of length >= n_decode) decode step s is fed forced[s]
+    instead of the previous greedy token (teacher forcing), and the greedy
+    tokens are still returned.
+    Returns (logits [P or 1, + n_decode, V] f32, tokens generated [n_decode + 1])."""
     p = len(prompt)
     cache = init_cache(cfg, 1, max_len)
     toks = np.asarray(prompt, np.int64)[None]
-    logits, cache = forward(cfg, params, toks, np.arange(p), cache, 0, prefill_masks(cfg, p, p), p, True,
-                            None, precise, trace)
+    logits, cache = forward(cfg, params, toks, np.arange(p), cache, 0, prefill_masks(cfg, p, p), p, prefill_dense,
+                            None if all_logits else p - 1, precise, trace)
     out = [logits[0]]
     nxt = greedy(logits[0, -1])
     gen = [nxt]
     for step in range(n_decode):
         pos = p + step
-        lg, cache = forward(cfg, params, np.array([[nxt]]), np.array([pos]), cache, pos,
+        feed = nxt if forced is None else int(forced[step])
+        lg, cache = forward(cfg, params, np.array([[feed]]), np.array([pos]), cache, pos,
                             decode_masks(cfg, max_len, pos), max_len, False, None, precise, trace)
         out.append(lg[0])
         nxt = greedy(lg[0, 0])

@@ -1,0 +1,376 @@
+"""Oracle parity of the production kernel instances on the 26B-A4B shapes.
+
+The model is the 26B-A4B configuration cut to two layers, one of each kind:
+a sliding layer (16 query / 8 KV heads of 256, window 1024) and a full k==v
+layer (16 query / 2 KV heads of 512, partial RoPE); hidden 2816, dense MLP
+2112, 128 experts top-8 of width 704, vocab 262,144, final softcap 30.
+Weights are N(0, 0.02) bf16 from the device generator (seed 3), copied to
+the host for the oracle (the generator itself is pinned bit for bit against
+its numpy restatement in test_gpu_model.py).  So every kernel here runs the
+instance the full model's decode step runs (the IT = 11 GEMV walks, the
+router and selection at E = 128 / k = 8, expert down and combine at F = 704,
+the lm_head over 262,144 rows), with the oracle (oracle/twin.py) as the
+reference.
+
+Checks:
+  * ffn_in on the same inputs as the oracle: residual and normalised
+    vectors bit-exact, expert indices bit-exact (the north-star requirement,
+    on the kernel the decode step selects experts with), routing weights
+    within 2 f32 ulps, the dense activation within one bf16 rounding;
+  * ffn_out (dense down, expert down, bf16 running combine and f32 combine)
+    and lm_head (tail, final norm, 262,144 logits, softcap, block argmax)
+    against f64 products;
+  * Engine.generate (batched prefill of a 54-token prompt, then 8 greedy
+    decode graphs) against the oracle run on the same token history: every
+    generated token is the oracle's greedy choice or a declared near tie
+    (top-two oracle logits within TIE), and the teacher-forced agreement
+    rate is printed;
+  * the decode runner fed that history: logits corr >= 0.9999, max |d| <=
+    LOGIT_TOL, per-layer expert sets;
+  * PrefillRunner at 256 tokens: last-row logits and both layers' K/V
+    against the oracle's dense-MoE prefill;
+  * prefill rows do not depend on the prompt length: the first 256 rows of
+    a 2,048-token prefill equal a 256-token prefill's (cache and logits);
+  * BatchEngine with 8 sequences of different lengths against the batch-1
+    runner fed the same tokens.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gemma4_mi import model as gm
+from gemma4_mi import ops
+from gemma4_mi.batch import BatchEngine
+from gemma4_mi.config import FULL, SLIDING, gemma4_26b_a4b_config
+from gemma4_mi.engine import Engine
+from gemma4_mi.weights import init_random_params
+from oracle import twin
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TIE = 2e-3         # declared near tie: the oracle's top two logits within this
+LOGIT_TOL = 2e-3   # logits are ~N(0, 0.02); a bf16 ulp at 0.1 is 4.9e-4
+P, N_DEC, MAX_LEN = 54, 8, 1024
+
+
+def _cfg():
+    return gemma4_26b_a4b_config().replace(num_hidden_layers=2, layer_types=(SLIDING, FULL))
+
+
+@pytest.fixture(scope="module")
+def m26():
+    cfg = _cfg()
+    params = init_random_params(cfg, 3, device=DEV)
+    torch.cuda.synchronize()
+    cpu = {k: v.cpu() for k, v in params.items()}
+    # the oracle holds the tied embedding in f64 once (same values; its
+    # einsums would otherwise convert the 262,144 x 2816 table every call)
+    po = dict(cpu)
+    po["embed"] = cpu["embed"].double()
+    return cfg, params, cpu, po
+
+
+def _bits(t):
+    return t.contiguous().view(torch.int16).cpu()
+
+
+def _rnd(shape, g, std):
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+def _check_near_ties(got_tok, exp_logits, what):
+    """Each got_tok[s] is the argmax of exp_logits[s] or within TIE of its max."""
+    agree = 0
+    for s, t in enumerate(got_tok):
+        row = exp_logits[s]
+        best = int(np.argmax(row))
+        if t == best:
+            agree += 1
+            continue
+        gap = float(row[best] - row[t])
+        print(f"{what}: step {s} token {t} vs oracle {best}, oracle logit gap {gap:.3e}")
+        assert gap <= TIE, f"{what}: step {s} is not a near tie ({gap:.3e})"
+    print(f"{what}: teacher-forced agreement {agree}/{len(got_tok)}")
+    return agree
+
+
+# ---------------------------------------------------------------- kernels on oracle inputs
+@pytest.mark.parametrize("layer", [0, 1])
+def test_ffn_in_selects_the_oracle_experts(m26, layer):
+    cfg, params, cpu, _ = m26
+    H, E, k, eps = cfg.hidden_size, cfg.num_experts, cfg.top_k_experts, cfg.rms_norm_eps
+    lp = twin.layer_params(cpu, layer)
+    dl = {n: params[f"layers.{layer}.{n}"] for n in lp}
+    g = torch.Generator().manual_seed(100 + layer)
+    x1d = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    xed = torch.empty_like(x1d)
+    act = torch.empty(cfg.intermediate_size, dtype=torch.bfloat16, device=DEV)
+    scores = torch.empty(E, dtype=torch.float32, device=DEV)
+    tw = torch.empty(k, dtype=torch.float32, device=DEV)
+    ti = torch.empty(k, dtype=torch.int32, device=DEV)
+    same_act = []
+    for case in range(4):
+        x, o = _rnd((H,), g, 1.0), _rnd((H,), g, 0.5 if case % 2 else 4.0)
+        ops.ffn_in(x.to(DEV), o.to(DEV), dl["post_attention_layernorm"], dl["pre_feedforward_layernorm"],
+                   dl["pre_feedforward_layernorm_2"], x1d, xed, dl["mlp.gate_proj"], dl["mlp.up_proj"], act,
+                   dl["router.scale"], dl["router.proj"], scores, H, eps,
+                   per_expert_scale=dl["router.per_expert_scale"], k=k, route=(tw, ti))
+        torch.cuda.synchronize()
+        # oracle: model.py:301-304 (x1), 310/315 (norms), 218-220 (gated MLP), 224-232 (router)
+        x1 = twin.rb(twin.f32(x) + twin.f32(twin.rms_norm(o, lp["post_attention_layernorm"], eps)))
+        xm = twin.rms_norm(x1, lp["pre_feedforward_layernorm"], eps)
+        xe = twin.rms_norm(x1, lp["pre_feedforward_layernorm_2"], eps)
+        gg = twin.ein("h,ih->i", xm, lp["mlp.gate_proj"])
+        uu = twin.ein("h,ih->i", xm, lp["mlp.up_proj"])
+        a_ref = twin.rb(twin.f32(twin.gelu(gg)) * twin.f32(uu))
+        w_ref, i_ref = twin.router(cfg, lp, xe[None])
+        assert torch.equal(_bits(x1d), _bits(x1)), "x1"
+        assert torch.equal(_bits(xed), _bits(xe)), "xe"
+        assert ti.cpu().tolist() == i_ref[0].tolist(), (case, ti.cpu().tolist(), i_ref[0].tolist())
+        ulp = np.spacing(np.abs(w_ref[0].numpy()).astype(np.float32))
+        assert np.all(np.abs(tw.cpu().numpy() - w_ref[0].numpy()) <= 2 * ulp), case
+        # the activation: gate and up are f32 dots rounded to bf16 (the oracle's
+        # are f64 dots), so a rounding may flip; bound it by the f32 dot's error
+        ga = act.cpu().double()
+        same_act.append((ga == a_ref.double()).double().mean().item())
+        assert torch.allclose(ga, a_ref.double(), rtol=2.0 ** -6, atol=1e-4), case
+    print(f"layer {layer}: activation bit-identical fraction {np.mean(same_act):.4f}")
+    assert np.mean(same_act) >= 0.98
+
+
+@pytest.mark.parametrize("combine", ["bf16_running", "f32"])
+def test_ffn_out_at_26b_shapes(m26, combine):
+    cfg, params, cpu, _ = m26
+    H, I, F, k = cfg.hidden_size, cfg.intermediate_size, cfg.moe_intermediate_size, cfg.top_k_experts
+    lp = twin.layer_params(cpu, 0)
+    g = torch.Generator().manual_seed(7 if combine == "f32" else 8)
+    act_mlp = _rnd((I,), g, 0.05)
+    act_moe = _rnd((k, F), g, 0.05)
+    top_i = torch.randperm(cfg.num_experts, generator=g)[:k].to(torch.int32)
+    mlp_d = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    moe_d = torch.empty_like(mlp_d)
+    ops.ffn_out(act_mlp.to(DEV), params["layers.0.mlp.down_proj"], mlp_d, act_moe.to(DEV).reshape(-1),
+                params["layers.0.experts.down_proj"], top_i.to(DEV), k, combine, moe_d, H)
+    torch.cuda.synchronize()
+    down = lp["mlp.down_proj"].double()
+    mlp_ref = down @ act_mlp.double()
+    assert (mlp_d.cpu().double() - mlp_ref).abs().max().item() <= mlp_ref.abs().max().item() * 2.0 ** -7
+    assert (mlp_d.cpu() == twin.rb(mlp_ref)).float().mean().item() >= 0.98
+    parts = [lp["experts.down_proj"][int(e)].double() @ act_moe[s].double() for s, e in enumerate(top_i)]
+    if combine == "bf16_running":  # model.py:289-293: bf16 running sum in slot order
+        acc = twin.rb(parts[0])
+        for p in parts[1:]:
+            acc = twin.rb(twin.f32(acc) + twin.f32(twin.rb(p)))
+        ref = acc.double()
+    else:  # model.py:250: one contraction over the experts
+        ref = twin.rb(sum(parts)).double()
+    got = moe_d.cpu().double()
+    same = (got == ref).double().mean().item()
+    print(f"{combine}: moe_out bit-identical {same:.4f}, max|d| {(got - ref).abs().max().item():.3e}")
+    assert (got - ref).abs().max().item() <= ref.abs().max().item() * 2.0 ** -6
+    assert same >= 0.95
+
+
+def test_lm_head_over_262144_rows(m26):
+    cfg, params, cpu, po = m26
+    H, eps = cfg.hidden_size, cfg.rms_norm_eps
+    lp = twin.layer_params(cpu, 1)
+    dl = {n: params[f"layers.1.{n}"] for n in lp}
+    g = torch.Generator().manual_seed(11)
+    x1, mlp, mo = _rnd((H,), g, 1.0), _rnd((H,), g, 2.0), _rnd((H,), g, 0.5)
+    V = cfg.vocab_size
+    logits = torch.empty(V, dtype=torch.float32, device=DEV)
+    nb = ops.lm_head_blocks(V)
+    bv, bi = torch.empty(nb, dtype=torch.float32, device=DEV), torch.empty(nb, dtype=torch.int32, device=DEV)
+    tok = torch.zeros(1, dtype=torch.int32, device=DEV)
+    ops.lm_head(x1.to(DEV), mlp.to(DEV), mo.to(DEV), dl["post_feedforward_layernorm_1"],
+                dl["post_feedforward_layernorm_2"], dl["post_feedforward_layernorm"], dl["layer_scalar"],
+                params["norm"], params["embed"], cfg.final_logit_softcapping, eps, logits, bv, bi)
+    ops.argmax_finalize(bv, bi, tok)
+    torch.cuda.synchronize()
+    # oracle: the layer tail (model.py:312-322), final norm (373), lm_head + softcap (381-385)
+    h1 = twin.rms_norm(mlp, lp["post_feedforward_layernorm_1"], eps)
+    h2 = twin.rms_norm(mo, lp["post_feedforward_layernorm_2"], eps)
+    hs = twin.rms_norm(twin.rb(twin.f32(h1) + twin.f32(h2)), lp["post_feedforward_layernorm"], eps)
+    x = twin.rb(twin.f32(twin.rb(twin.f32(x1) + twin.f32(hs))) * twin.f32(lp["layer_scalar"]))
+    xn = twin.rms_norm(x, cpu["norm"], eps)
+    raw = twin.f32(twin.rb(po["embed"] @ xn.double()))
+    cap = np.float32(cfg.final_logit_softcapping)
+    ref = (torch.tanh(raw / cap) * cap).numpy()
+    got = logits.cpu().numpy()
+    # equal up to the softcap's f32 tanh (a few f32 ulps); a flipped bf16
+    # rounding of the f32-accumulated dot moves a logit by one bf16 ulp
+    same = np.mean(np.abs(got - ref) <= 4 * np.spacing(np.abs(ref)))
+    err = np.abs(got - ref).max()
+    print(f"lm_head: {same:.5f} of 262,144 logits equal, max|d| {err:.3e}, token {int(tok.item())}")
+    assert same >= 0.99 and err <= 2.0 ** -7 * np.abs(ref).max()
+    assert int(tok.item()) == int(np.argmax(got))  # first index of the maximum of the kernel's logits
+    best = int(np.argmax(ref))
+    assert int(tok.item()) == best or ref[best] - ref[int(tok.item())] <= TIE
+
+
+# ---------------------------------------------------------------- whole model
+@pytest.fixture(scope="module")
+def gen26(m26):
+    """Engine.generate on a 54-token prompt (8 greedy decode tokens after the
+    first), then the oracle on the same token history."""
+    cfg, params, cpu, po = m26
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, size=P).tolist()
+    eng = Engine(None, MAX_LEN, 1, cfg=cfg, params=params, device=DEV)
+    ev = list(eng.generate(prompt, max_new_tokens=N_DEC + 1, temperature=0.0, stop_ids=()))
+    gen_g = [e["token"] for e in ev]
+    assert [e["kind"] for e in ev] == ["prefill"] + ["decode"] * N_DEC
+    trace = []
+    logits_o, gen_o = twin.prefill_then_decode(cfg, po, prompt, N_DEC, MAX_LEN, trace=trace, all_logits=False,
+                                               prefill_dense="selected", forced=gen_g)
+    del eng
+    torch.cuda.empty_cache()
+    return prompt, gen_g, logits_o.numpy(), gen_o, trace
+
+
+def test_engine_generate_greedy_matches_oracle(m26, gen26):
+    prompt, gen_g, logits_o, gen_o, _ = gen26
+    print(f"engine {gen_g}\noracle {gen_o}")
+    _check_near_ties(gen_g, logits_o, "Engine.generate")
+
+
+def test_decode_runner_logits_match_oracle(m26, gen26):
+    cfg, params, cpu, po = m26
+    prompt, gen_g, logits_o, gen_o, trace = gen26
+    cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
+    r = gm.DecodeRunner(cfg, params, cache, device=DEV)
+    pr = gm.PrefillRunner(cfg, params, cache, 256, device=DEV, rope=r.rope)
+    pr.run(torch.tensor(prompt, dtype=torch.int32, device=DEV), P)
+    r.pos.fill_(P - 1)
+    r.head(*pr.last_row(P))
+    rows, routes = [r.logits.cpu().clone()], []
+    for s in range(N_DEC):
+        r.set_state(gen_g[s], P + s)
+        r.launch("bf16_running", advance=False)
+        rows.append(r.logits.cpu().clone())
+        routes.append(r.top_i.cpu().clone())
+    torch.cuda.synchronize()
+    got = torch.stack(rows).numpy()
+    err = np.abs(got - logits_o)
+    corr = np.corrcoef(got.ravel(), logits_o.ravel())[0, 1]
+    print(f"26B-shaped decode logits: max|d|={err.max():.3e} corr={corr:.7f}")
+    assert corr >= 0.9999 and err.max() <= LOGIT_TOL
+    _check_near_ties([int(np.argmax(x)) for x in got], logits_o, "decode runner")
+    # routing of the decode steps: trace = [prefill layers, then per step layers 0..L-1]
+    L = cfg.num_hidden_layers
+    same = []
+    for s in range(N_DEC):
+        for layer in range(L):
+            o = trace[L + s * L + layer][1][0, 0].tolist()
+            gsel = routes[s][layer].tolist()
+            same.append(set(o) == set(gsel))
+            if set(o) != set(gsel):
+                print(f"step {s} layer {layer}: gpu {gsel} oracle {o}")
+    print(f"decode expert sets identical: {np.mean(same):.3f}")
+    assert np.mean(same) >= 0.9
+
+
+def test_batched_prefill_256_matches_oracle(m26):
+    cfg, params, cpu, po = m26
+    n = 256
+    prompt = np.random.default_rng(4).integers(0, cfg.vocab_size, size=n)
+    cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
+    r = gm.DecodeRunner(cfg, params, cache, device=DEV)
+    pr = gm.PrefillRunner(cfg, params, cache, n, device=DEV, rope=r.rope)
+    pr.run(torch.tensor(prompt, dtype=torch.int32, device=DEV), n)
+    r.pos.fill_(n - 1)
+    r.head(*pr.last_row(n))
+    torch.cuda.synchronize()
+    oc = twin.init_cache(cfg, 1, n)
+    lg, oc = twin.forward(cfg, po, prompt[None], np.arange(n), oc, 0, twin.prefill_masks(cfg, n, n), n, "selected",
+                          n - 1)
+    got, exp = r.logits.cpu().numpy(), lg[0, 0].numpy()
+    err = np.abs(got - exp)
+    corr = np.corrcoef(got, exp)[0, 1]
+    print(f"prefill 256, last row: max|d|={err.max():.3e} corr={corr:.7f}")
+    assert corr >= 0.9999 and err.max() <= LOGIT_TOL
+    best = int(np.argmax(exp))
+    assert int(r.tok.item()) == best or exp[best] - exp[int(r.tok.item())] <= TIE
+    for i in range(cfg.num_hidden_layers):
+        for j, kind in enumerate(("k", "v")):
+            o = oc[kind][i][0, :n].float().numpy().ravel()
+            gk = gm.cache_positions(cache, i, upto=n)[j].float().cpu().numpy().ravel()
+            same, c = np.mean(gk == o), np.corrcoef(gk, o)[0, 1]
+            print(f"layer {i} {kind}: identical {same:.4f} corr {c:.7f}")
+            assert c >= 0.9999, (i, kind, c)
+            if i == 0:
+                assert same >= 0.99, (i, kind, same)
+
+
+def test_prefill_rows_do_not_depend_on_prompt_length(m26):
+    """Row t of the causal prefill depends only on tokens <= t: the first 256
+    rows of a 2,048-token prefill (cache of both layers, and the head applied
+    to row 255) equal those of a 256-token prefill of the same tokens, bit for
+    bit."""
+    cfg, params, *_ = m26
+    toks = torch.tensor(np.random.default_rng(5).integers(0, cfg.vocab_size, size=2048), dtype=torch.int32,
+                        device=DEV)
+    out = []
+    for n in (2048, 256):
+        cache = gm.init_cache(cfg, None, 1, 2048, device=DEV)
+        r = gm.DecodeRunner(cfg, params, cache, device=DEV)
+        pr = gm.PrefillRunner(cfg, params, cache, n, device=DEV, rope=r.rope)
+        pr.run(toks, n)
+        r.pos.fill_(255)
+        r.head(pr.x1[255], pr.mlp_out[255], pr.moe_out[255])
+        torch.cuda.synchronize()
+        kv = [gm.cache_positions(cache, i, upto=256)[j].cpu() for i in range(2) for j in range(2)]
+        out.append((kv, r.logits.cpu().clone()))
+        del r, pr, cache
+    for a, b in zip(out[0][0], out[1][0]):
+        assert torch.equal(_bits(a), _bits(b))
+    assert torch.equal(out[0][1], out[1][1])
+
+
+def test_batch_engine_matches_batch1_runner(m26):
+    """Eight sequences of different lengths decode together (skinny MFMA
+    GEMMs, per-row attention positions, per-pair experts, batched head);
+    each row's logits at every step against the batch-1 decode runner fed the
+    same tokens: corr >= 0.9999, max |d| <= LOGIT_TOL, and each batch token
+    is the batch-1 runner's greedy choice or a near tie of it."""
+    cfg, params, *_ = m26
+    lens = (20, 33, 54, 70, 91, 128, 150, 200)
+    prompts = [np.random.default_rng(40 + i).integers(0, cfg.vocab_size, size=n).tolist()
+               for i, n in enumerate(lens)]
+    n_steps = 5
+    eng = BatchEngine(cfg, params, batch=8, max_len=512, device=DEV)
+    for b, p in enumerate(prompts):
+        eng.add(b, p)
+    blog = []
+    for _ in range(n_steps):
+        eng.step()
+        blog.append(eng.runner.logits_bf.float().cpu().clone())
+    torch.cuda.synchronize()
+    hist = eng.runner.hist.cpu()
+    cap = np.float32(cfg.final_logit_softcapping)
+    for b, p in enumerate(prompts):
+        n = len(p)
+        toks = hist[b, n:n + n_steps + 1].tolist()
+        cache = gm.init_cache(cfg, None, 1, 512, device=DEV)
+        r = gm.DecodeRunner(cfg, params, cache, device=DEV)
+        pr = gm.PrefillRunner(cfg, params, cache, 256, device=DEV, rope=r.rope)
+        pr.run(torch.tensor(p, dtype=torch.int32, device=DEV), n)
+        r.pos.fill_(n - 1)
+        r.head(*pr.last_row(n))
+        first = int(r.tok.item())
+        exp_rows = []
+        for s in range(n_steps):
+            r.set_state(toks[s], n + s)
+            r.launch("bf16_running", advance=False)
+            exp_rows.append(r.logits.cpu().clone())
+        torch.cuda.synchronize()
+        exp = torch.stack(exp_rows).numpy()
+        got = np.stack([(torch.tanh(blog[s][b] / cap) * cap).numpy() for s in range(n_steps)])
+        err = np.abs(got - exp)
+        corr = np.corrcoef(got.ravel(), exp.ravel())[0, 1]
+        print(f"row {b} ({n} tokens): max|d| {err.max():.3e} corr {corr:.7f} first {toks[0]} vs {first}")
+        assert toks[0] == first
+        assert corr >= 0.9999 and err.max() <= LOGIT_TOL
+        _check_near_ties(toks[1:], exp, f"batch row {b}")
+        del r, pr, cache

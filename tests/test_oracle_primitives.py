@@ -263,6 +263,39 @@ def test_sparse_moe_matches_dense_moe():
     assert (a - b).abs().max().item() <= 4 * 2.0 ** -8 * b.abs().max().item()
 
 
+def test_dense_moe_on_selected_experts_equals_all_experts():
+    """The dense-MoE contraction restricted to the selected (token, expert)
+    pairs (moe_dense_selected, what the 26B-shaped parity tests run) equals
+    the all-experts contraction of model.py:241-250 bit for bit: the masked
+    experts add exact zeros, and only the f64 summation order differs before
+    the single rounding.  Also at 64 tokens with routing ties."""
+    for n_tok, seed in ((6, 3), (64, 8)):
+        cfg, lp, flat = _router_inputs(n_tok, seed)
+        full, w1, i1 = twin.moe(cfg, lp, flat, dense=True, return_route=True)
+        sel, w2, i2 = twin.moe(cfg, lp, flat, dense="selected", return_route=True)
+        assert torch.equal(i1, i2) and torch.equal(w1, w2)
+        assert torch.equal(full.view(torch.int16), sel.view(torch.int16))
+    with pytest.raises(ValueError):
+        twin.moe(cfg, lp, flat, dense="all")
+
+
+def test_teacher_forced_decode_feeds_the_given_tokens():
+    """prefill_then_decode with `forced` feeds the given tokens; fed the
+    oracle's own greedy stream it reproduces the free-running logits, and
+    all_logits=False returns the last prompt row only."""
+    cfg = tiny_parity_config()
+    params = twin.random_params(cfg, 0)
+    prompt = np.random.default_rng(3).integers(0, cfg.vocab_size, size=12)
+    lg, gen = twin.prefill_then_decode(cfg, params, prompt, 3, 32)
+    lg2, gen2 = twin.prefill_then_decode(cfg, params, prompt, 3, 32, all_logits=False, prefill_dense="selected",
+                                         forced=gen)
+    assert lg.shape[0] == 12 + 3 and lg2.shape[0] == 1 + 3
+    assert torch.equal(lg[11:], lg2) and gen2 == gen
+    other = [(t + 1) % cfg.vocab_size for t in gen]
+    lg3, _ = twin.prefill_then_decode(cfg, params, prompt, 3, 32, all_logits=False, forced=other)
+    assert torch.equal(lg3[0], lg2[0]) and not torch.equal(lg3[1], lg2[1])
+
+
 def test_moe_against_brute_force_selected_experts():
     """Routing weight applied before down (model.py:271), f64 brute force over
     the selected experts only."""
