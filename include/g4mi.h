@@ -375,6 +375,27 @@ int64_t g4mi_argmax_rows_workspace_bytes(int64_t B);
 int g4mi_argmax_rows(const uint16_t* logits, int64_t B, int64_t V, float softcap, float* logits_f32, int32_t* tok,
                      int32_t* pos, int32_t* hist, int64_t hist_len, void* ws, int64_t ws_bytes, void* stream);
 
+/* ---------------------------------------------------------------- model primitives
+ * The reference model's standalone primitives (model.py:42-78), with the
+ * rounding recipe of the fused kernels.  Tensor dtype codes: 0 = bf16,
+ * 1 = f32 (the output has x's dtype).
+ *   g4mi_rms_norm:    out[r, :] = cast(f32(x) * r * f32(w)), r = 1/sqrt(mean(x^2) + eps)
+ *                     with the sum of squares exact (model.py:42-47); w may be NULL.
+ *   g4mi_gelu_tanh:   tanh-approximation GELU in f32, one rounding (model.py:50-51).
+ *   g4mi_rope_tables: cos/sin [T, 2*half] f32 of f32(pos) * inv_freq[j] with
+ *                     the halves duplicated (model.py:64-67).
+ *   g4mi_apply_rope:  x [B, T, inner, D] (inner = the head axes) with cos/sin
+ *                     [T, D] cast to x's dtype: x*c + rotate_half(x)*s, each
+ *                     product and the sum rounded to x's dtype (model.py:70-78);
+ *                     out must not alias x. */
+int g4mi_rms_norm(const void* x, int32_t x_f32, const void* w, int32_t w_f32, int64_t rows, int64_t dim, float eps,
+                  void* out, void* stream);
+int g4mi_gelu_tanh(const void* x, int32_t x_f32, int64_t n, void* out, void* stream);
+int g4mi_rope_tables(const int32_t* positions, int64_t T, const float* inv_freq, int64_t half, float* cos_out,
+                     float* sin_out, void* stream);
+int g4mi_apply_rope(const void* x, int32_t x_f32, const float* rope_cos, const float* rope_sin, int64_t B, int64_t T,
+                    int64_t inner, int64_t D, void* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

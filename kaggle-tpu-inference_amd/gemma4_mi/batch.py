@@ -200,7 +200,7 @@ class BatchEngine:
         self.cache = M.init_cache(cfg, None, batch, max_len, device=self.device, num_pages=pool_pages)
         self.pool = PagePool(self.cache)
         self.runner = BatchDecodeRunner(cfg, params, self.cache, device=self.device)
-        self._head = M.DecodeRunner(cfg, params, self.cache, device=self.device, hist_len=8)
+        self._head = M.HeadRunner(cfg, params, self.device)
         self._prefill: M.PrefillRunner | None = None
         self._prompt = torch.zeros(max_len, dtype=torch.int32, device=self.device)
         self.pos_host = [0] * batch

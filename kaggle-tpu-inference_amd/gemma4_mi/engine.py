@@ -58,8 +58,8 @@ class Engine:
     def __init__(self, model_dir: str | None, max_len: int = 4096, batch: int = 1, top_k: int = 64, progress=None,
                  *, cfg: TextConfig | None = None, params: dict | None = None, device: str = "cuda:0",
                  prefill: str = "batched"):
-        if batch != 1:
-            raise ValueError("this engine decodes one sequence (batch=1)")
+        if batch < 1:
+            raise ValueError("batch must be >= 1")
         if not 1 <= top_k <= 64:
             raise ValueError("top_k must be in [1, 64]")
         if prefill not in ("batched", "stepwise"):
@@ -93,6 +93,8 @@ class Engine:
         self._pos_host = 0
         self._host_tok = torch.zeros(self.max_len + 1, dtype=torch.int32, pin_memory=True)
         self._prefill_runner: M.PrefillRunner | None = None
+        # positions written per cache row since the last reset_cache()
+        self._dirty = [0] * batch
 
     @classmethod
     def random(cls, cfg: TextConfig, seed: int = 3, max_len: int = 4096, top_k: int = 64, device: str = "cuda:0",
@@ -135,6 +137,8 @@ class Engine:
         r.tok.copy_(saved_tok)
         r.pos.copy_(saved_pos)
         r.hist.copy_(hist_save)
+        # the warm step wrote K/V at the scratch position: clear that page again
+        self._zero_pages(0, self.max_len - 1, self.max_len)
         torch.cuda.synchronize(self.device)
         self._graphs[key] = g
         return g
@@ -168,7 +172,18 @@ class Engine:
             n = int(_scalar(prompt_len))
             if not 1 <= n <= min(t, self.max_len):
                 raise ValueError(f"prompt_len {n} outside [1, {min(t, self.max_len)}]")
-            toks = torch.as_tensor(tokens).reshape(-1)[:n].to(torch.int32)
+            rows = torch.as_tensor(tokens)
+            rows = rows.reshape(1, -1) if rows.ndim < 2 else rows.reshape(rows.shape[0], -1)
+            if rows.shape[0] > self.batch or rows.shape[1] < n:
+                raise ValueError(f"tokens {tuple(rows.shape)} for batch {self.batch} and prompt_len {n}")
+            # rows 1.. (engine.py:60-67 runs every row of tokens [B, t]) fill
+            # their own cache rows; the token comes from row 0, as there
+            for b in range(1, rows.shape[0]):
+                pb = self._prefill_for(n)
+                self._prompt[:n].copy_(rows[b, :n].to(torch.int32))
+                pb.run(self._prompt, n, seq=b)
+                self._dirty[b] = max(self._dirty[b], n)
+            toks = rows[0, :n].to(torch.int32)
             self._prompt[:n].copy_(toks)
             greedy = self._set_sampling(key, temperature, top_p)
             r.hist[:n].copy_(self._prompt[:n])
@@ -186,6 +201,7 @@ class Engine:
                     feed.replay()
                 self._graph("head", greedy).replay()
             self._pos_host = n
+            self._dirty[0] = max(self._dirty[0], n)
             return r.hist[n:n + 1].view(1, 1), cache, torch.tensor(n, dtype=torch.int32)
 
         return fn
@@ -209,6 +225,7 @@ class Engine:
             greedy = self._set_sampling(key, temperature, top_p)
             self._graph("decode", greedy).replay()
             self._pos_host = p + 1
+            self._dirty[0] = max(self._dirty[0], p + 1)
             return r.hist[p + 1:p + 2].view(1, 1), cache, torch.tensor(p + 1, dtype=torch.int32)
 
         return fn
@@ -221,15 +238,29 @@ class Engine:
 
     def decode_fn(self):
         """fn(params, token[1,1] int32, cache, pos, key, temperature, top_p)
-        -> (tok [1,1] int32, cache, pos + 1) (engine.py:71-83)."""
+        -> (tok [1,1] int32, cache, pos + 1) (engine.py:71-83).  Decodes cache
+        row 0 (the reference's engine samples logits[0, 0] and keeps one
+        scalar position, engine.py:74-81)."""
         return self._build_decode()
 
     # ---------------------------------------------------------------- helpers
-    def reset_cache(self):
-        """Zeroes the K/V pools in place (engine.py:96-97 builds a new zero cache;
-        the captured graphs keep these buffers)."""
+    def _zero_pages(self, b: int, lo: int, hi: int) -> None:
+        """Zeroes the pages of cache row b that hold positions [lo, hi)."""
+        page, mp = self.cache["page_size"], self.cache["page_table"].shape[1]
+        p0, p1 = b * mp + lo // page, b * mp + (hi + page - 1) // page
         for t in self.cache["k"] + self.cache["v"]:
-            t.zero_()
+            t[p0:p1].zero_()
+
+    def reset_cache(self):
+        """A zero cache again (engine.py:96-97 builds a new one; here the
+        captured graphs keep these buffers, so they are cleared in place).
+        Only the pages written since the last reset are zeroed: no kernel
+        reads a position before the current request writes it, and a full
+        clear of a 32K cache would move 7.4 GB per request."""
+        for b, d in enumerate(self._dirty):
+            if d:
+                self._zero_pages(b, 0, d)
+            self._dirty[b] = 0
         self._runner.hist.zero_()
         self._pos_host = 0
 
@@ -239,7 +270,7 @@ class Engine:
     def compile_all(self, bucket: int = PREFILL_BUCKET) -> dict[str, float]:
         """Captures the step graphs and times one decode step (engine.py:102-140)."""
         out = {}
-        toks = torch.zeros((1, bucket), dtype=torch.int32)
+        toks = torch.zeros((self.batch, bucket), dtype=torch.int32)
         t0 = time.perf_counter()
         if self.prefill_mode == "batched":
             # prompts of more than 16 rows run their dense products through the

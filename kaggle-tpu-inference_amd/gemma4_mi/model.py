@@ -15,6 +15,71 @@ from .config import FULL, SLIDING, TextConfig
 NEG_INF = -1e30
 
 
+# --------------------------------------------------------------------- primitives
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """model.py:42-47 on a device tensor (bf16 or f32), through the library's
+    row kernel: f32 normalisation with an exact sum of squares, optional
+    weight (Gemma-4 multiplies by w, not 1 + w), cast back to x's dtype."""
+    from . import ops
+
+    return ops.rms_norm(x, weight, eps)
+
+
+def gelu(x: torch.Tensor) -> torch.Tensor:
+    """model.py:50-51: tanh-approximation GELU, computed in f32, x's dtype."""
+    from . import ops
+
+    return ops.gelu(x)
+
+
+def rope_tables(positions, inv_freq) -> tuple[torch.Tensor, torch.Tensor]:
+    """model.py:64-67: (cos, sin) f32 [T, D] of f32(pos) * inv_freq, halves
+    duplicated, on the GPU (positions may be a host list or array)."""
+    from . import ops
+
+    pos = torch.as_tensor(positions)
+    if not pos.is_cuda:
+        pos = pos.to("cuda")
+    return ops.rope_tables(pos, torch.as_tensor(inv_freq))
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """model.py:70-78: x [B, T, ..., D]; cos/sin [T, D] cast to x's dtype;
+    x * c + rotate_half(x) * s with each op rounded to x's dtype."""
+    from . import ops
+
+    return ops.apply_rope(x, cos, sin)
+
+
+class Mesh:
+    """One-device stand-in for the reference's jax Mesh (model.py:159-161):
+    the same attributes callers read (devices, axis_names, shape, size) and a
+    no-op context manager, so `with mesh:` blocks run unchanged.  This build
+    runs the model on one GPU; there is no tensor-parallel axis to shard."""
+
+    def __init__(self, device: torch.device):
+        import numpy as np
+
+        self.devices = np.array([device], dtype=object)
+        self.axis_names = ("tp",)
+        self.shape = {"tp": 1}
+        self.size = 1
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        return False
+
+    def __repr__(self) -> str:
+        return f"Mesh(devices={list(self.devices)}, axis_names={self.axis_names})"
+
+
+def make_mesh() -> Mesh:
+    """model.py:159-161: the mesh over the visible devices; here one GPU."""
+    return Mesh(torch.device("cuda", 0))
+
+
 # --------------------------------------------------------------------- layout
 def param_shapes(cfg: TextConfig) -> dict[str, tuple[int, ...]]:
     """Canonical shapes of every parameter by flat name (model.py:84-117).
@@ -167,6 +232,44 @@ def decode_masks(cfg: TextConfig, max_len: int, pos) -> dict:
             "pos": p}
 
 
+# --------------------------------------------------------------------- sampling
+def fold_in(key, data: int):
+    """The per-step key of engine.py:66 and engine.py:80 (jax.random.fold_in):
+    here the pair (seed, step).  sample() with it draws the uniform at
+    Philox counter `step`, which is what the engine's decode step at
+    position `step` draws (and step 0 after a prefill)."""
+    seed = key[0] if isinstance(key, tuple) else int(key)
+    return (int(seed), int(data))
+
+
+def sample(logits: torch.Tensor, key, temperature, top_k: int, top_p) -> torch.Tensor:
+    """model.py:414-424 on a device logits row [V] f32 -> int32 scalar (device).
+
+    temperature <= 0: argmax, the first index of the maximum.  Otherwise the
+    top_k of logits / max(T, 1e-6), softmax, the nucleus cut (exclusive
+    prefix sum < top_p), renormalisation and one draw.  `key` is an integer
+    seed or a (seed, step) pair from fold_in; the uniform comes from this
+    library's Philox4x32-10 stream, not JAX's threefry, so stochastic draws
+    match the reference in distribution, not bit for bit."""
+    from . import ops
+
+    lg = logits.reshape(-1)
+    if lg.dtype != torch.float32 or not lg.is_contiguous():
+        lg = lg.float().contiguous()
+    dev = lg.device
+    t = float(temperature.item()) if isinstance(temperature, torch.Tensor) else float(temperature)
+    p = float(top_p.item()) if isinstance(top_p, torch.Tensor) else float(top_p)
+    seed, step = key if isinstance(key, tuple) else (int(key), None)
+    params = ops.sample_params(t, p, seed, dev)
+    tok = torch.zeros(1, dtype=torch.int32, device=dev)
+    if step is None:
+        ops.sample(lg, int(top_k), params, tok, counter_mode=0)
+    else:
+        ctr = torch.tensor([step], dtype=torch.int32, device=dev)
+        ops.sample(lg, int(top_k), params, tok, counter_mode=1, pos=ctr)
+    return tok.reshape(())
+
+
 # --------------------------------------------------------------------- decode step
 class DecodeRunner:
     """Launches one batch-1 token step of the model on the current stream.
@@ -233,8 +336,6 @@ class DecodeRunner:
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
         self.sample_ws = torch.zeros(ops.sample_workspace_bytes(cfg.vocab_size), dtype=torch.uint8, device=dev)
         self.ffn_ws = torch.zeros(int(ops._lib.lib().g4mi_ffn_in_workspace_bytes()), dtype=torch.uint8, device=dev)
-        self.ffn_out_ws = torch.zeros(int(ops._lib.lib().g4mi_ffn_out_workspace_bytes()), dtype=torch.uint8,
-                                      device=dev)
 
     def _splits(self, lt: str) -> int:
         cfg = self.cfg
@@ -326,6 +427,14 @@ class DecodeRunner:
         self.tok.fill_(int(token))
         self.pos.fill_(int(pos))
 
+    def set_sequence(self, b: int) -> None:
+        """Steps launched from now on use page-table row b of the cache (the
+        runner's own buffers are shared).  Not for a runner whose steps are
+        captured in graphs: a graph keeps the row it was captured with."""
+        if not 0 <= b < self.cache["page_table"].shape[0]:
+            raise ValueError(f"sequence {b} outside the cache's {self.cache['page_table'].shape[0]} rows")
+        self.page_table = self.cache["page_table"][b:b + 1]
+
 
 class PrefillRunner:
     """Batched prefill of n prompt tokens at positions 0..n-1 (model.py:333-386
@@ -383,12 +492,16 @@ class PrefillRunner:
                              self.max_len, dev),
         }
 
-    def run(self, tokens: torch.Tensor, n: int, seq: int = 0) -> None:
+    def run(self, tokens: torch.Tensor, n: int, seq: int = 0, p0: int = 0) -> None:
         """Runs the layers for tokens[:n] (device int32) of sequence `seq`
-        (its page-table row) on the current stream."""
+        (its page-table row) at positions p0 .. p0 + n - 1 on the current
+        stream.  With p0 > 0 (a continued prefill) the rows also attend the
+        positions < p0 already in the cache."""
         ops, cfg, p = self.ops, self.cfg, self.params
         if not 1 <= n <= self.capacity:
             raise ValueError(f"{n} prompt tokens outside [1, {self.capacity}]")
+        if not 0 <= p0 <= self.max_len - n:
+            raise ValueError(f"positions {p0}..{p0 + n - 1} outside the cache (max_len {self.max_len})")
         H, eps, NH = cfg.hidden_size, cfg.rms_norm_eps, cfg.num_attention_heads
         moe = cfg.enable_moe_block
         L = cfg.num_hidden_layers
@@ -396,7 +509,7 @@ class PrefillRunner:
         mlp_out = self.mlp_out[:n]
         xe = self.xe[:n] if moe else None
         moe_out = self.moe_out[:n] if moe else None
-        pos = self.pos[:n]
+        pos = self.pos[:n] if p0 == 0 else self.pos[:n] + p0
         page_row = self.cache["page_table"][seq]
         ops.rows_embed(tokens[:n], p["embed"], self.layers[0]["input_layernorm"], eps, x, xn)
         for i, lt in enumerate(cfg.layer_types):
@@ -414,8 +527,8 @@ class PrefillRunner:
                           self.cache["k"][i], self.cache["v"][i], page_row, pos, self.max_len, eps)
             ctx = self.ctx[: n * NH * d].view(n, NH, d)
             window = cfg.sliding_window if lt == SLIDING else 0
-            qh = ops.q_norm_rope(q.view(n, NH, d), lp["q_norm"], cos, sin, 0, eps)
-            ops.prefill_attention(qh, self.cache["k"][i], self.cache["v"][i], page_row, 0, window,
+            qh = ops.q_norm_rope(q.view(n, NH, d), lp["q_norm"], cos, sin, p0, eps)
+            ops.prefill_attention(qh, self.cache["k"][i], self.cache["v"][i], page_row, p0, window,
                                   cfg.attn_logit_softcapping, ctx=ctx)
             ops.prefill_gemm(ctx.view(n, NH * d), lp["o_proj"].reshape(H, NH * d), o)
             ops.rows_post_attn(x, o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
@@ -440,51 +553,147 @@ class PrefillRunner:
         return (self.x1[n - 1], self.mlp_out[n - 1], None if self.moe_out is None else self.moe_out[n - 1])
 
 
+class HeadRunner:
+    """The head of one row on its own: the last layer's tail and the final
+    norm (model.py:317-322, 373), lm_head and the final softcap
+    (model.py:381-385), then the greedy argmax or the sampler
+    (model.py:414-424).  For callers that need the head of a prefill row
+    without a decode step's buffers; tok/pos/hist are its own unless given."""
+
+    def __init__(self, cfg: TextConfig, params: dict, device="cuda", tok=None, pos=None, hist=None,
+                 hist_len: int = 8):
+        from . import ops
+
+        self.ops, self.cfg, self.params = ops, cfg, params
+        dev = torch.device(device)
+        z = lambda n, dt: torch.zeros(n, dtype=dt, device=dev)  # noqa: E731
+        self.logits = z(cfg.vocab_size, torch.float32)
+        nb = ops.lm_head_blocks(cfg.vocab_size)
+        self.blk_val, self.blk_idx = z(nb, torch.float32), z(nb, torch.int32)
+        self.tok = tok if tok is not None else z(1, torch.int32)
+        self.pos = pos if pos is not None else z(1, torch.int32)
+        self.hist = hist if hist is not None else z(hist_len, torch.int32)
+        self.sample_ws = None
+        self.last = {k[len(f"layers.{cfg.num_hidden_layers - 1}."):]: v for k, v in params.items()
+                     if k.startswith(f"layers.{cfg.num_hidden_layers - 1}.")}
+
+    def logits_of(self, x1, mlp_out, moe_out, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Softcapped f32 logits [V] of one row's tail inputs, into `out`."""
+        cfg, pl = self.cfg, self.last
+        out = self.logits if out is None else out
+        self.ops.lm_head(x1, mlp_out, moe_out, pl.get("post_feedforward_layernorm_1"),
+                         pl.get("post_feedforward_layernorm_2"), pl["post_feedforward_layernorm"],
+                         pl["layer_scalar"], self.params["norm"], self.params["embed"], cfg.final_logit_softcapping,
+                         cfg.rms_norm_eps, out, self.blk_val, self.blk_idx)
+        return out
+
+    def head(self, x1, mlp_out, moe_out, sampler=None) -> None:
+        """logits_of, then the next token: the token after position `pos`
+        goes to tok and hist[pos + 1], pos += 1."""
+        self.logits_of(x1, mlp_out, moe_out)
+        if sampler is not None:
+            params, top_k, counter_mode = sampler
+            if self.sample_ws is None:
+                self.sample_ws = torch.zeros(self.ops.sample_workspace_bytes(self.cfg.vocab_size), dtype=torch.uint8,
+                                             device=self.logits.device)
+            self.ops.sample(self.logits, top_k, params, self.tok, counter_mode, self.pos, self.hist,
+                            ws=self.sample_ws)
+        else:
+            self.ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos, self.hist)
+
+
 _RUNNERS: dict = {}
+
+
+def _runners_for(cfg: TextConfig, params: dict, cache: dict) -> dict:
+    """The runners that forward() uses for this (params, cache) pair, built on
+    first use: the decode runner, the head and the batched prefill."""
+    key = (id(params), id(cache["k"][0]))
+    rs = _RUNNERS.get(key)
+    if rs is None or rs["decode"].params is not params or rs["decode"].cache is not cache:
+        _RUNNERS.clear()
+        dev = cache["k"][0].device
+        r = DecodeRunner(cfg, params, cache, device=dev)
+        rs = {"decode": r, "head": HeadRunner(cfg, params, dev), "prefill": None}
+        _RUNNERS[key] = rs
+    return rs
 
 
 def runner_for(cfg: TextConfig, params: dict, cache: dict) -> DecodeRunner:
     """The DecodeRunner bound to this (params, cache) pair, built on first use."""
-    key = (id(params), id(cache["k"][0]))
-    r = _RUNNERS.get(key)
-    if r is None or r.params is not params or r.cache is not cache:
-        r = DecodeRunner(cfg, params, cache, device=cache["k"][0].device)
-        _RUNNERS.clear()
-        _RUNNERS[key] = r
-    return r
+    return _runners_for(cfg, params, cache)["decode"]
 
 
 def forward(cfg: TextConfig, mesh, params: dict, tokens, positions, cache: dict, write_at, masks: dict, kv_len: int,
             dense_moe: bool, last_index=None):
-    """Logits for `tokens` [1, T] at `positions` (model.py:333-386); returns
-    (logits f32 [1, T or 1, V], cache).  The cache is updated in place (the
-    reference donates it) and returned.
+    """Logits for `tokens` [B, T] at `positions` [T] (model.py:333-386): every
+    row b uses row b of the cache at the same positions, as the reference's
+    batched forward does.  Returns (logits f32 [B, T or 1, V], cache); the
+    cache is updated in place (the reference donates it) and returned.
 
-    Tokens are processed one position at a time with the decode kernels: row t
-    of the reference's causal prefill attends exactly the cached positions
-    <= t, so this equals the T x T masked prefill.  dense_moe selects the
-    dense-MoE contraction (one f32 sum over the experts, model.py:241-250)
-    instead of the decode path's bf16 running sum.  Padded prefill positions
-    (>= the masks' prompt_len) are skipped: the reference never attends them
-    and only last_index (< prompt_len) is read back."""
-    tok = torch.as_tensor(tokens).reshape(-1).tolist()
-    pos = torch.as_tensor(positions).reshape(-1).tolist()
-    if len(pos) != len(tok):
-        raise ValueError("tokens and positions differ in length")
-    n = len(tok)
+    A multi-token call with the dense-MoE combine over consecutive positions
+    (the engine's prefill, model.py:241-250 and 392-399) runs the batched
+    prefill: MFMA GEMMs, the selected-expert grouped GEMMs and MFMA prefill
+    attention, then the head of each requested row.  Single-token calls (the
+    decode step, model.py:262-294) and any other call run the decode kernels
+    one position at a time; row t of the reference's causal prefill attends
+    exactly the cached positions <= t, so both equal the T x T masked form.
+    dense_moe selects the dense-MoE f32 combine instead of the decode path's
+    bf16 running sum.  Rows at or past the masks' prompt_len (the
+    reference's bucket padding) are neither computed nor written to the
+    cache: the reference never attends them and reads back only last_index
+    (< prompt_len); their logits are returned as zeros.  kv_len is not
+    needed: the kernels read only each row's attended positions."""
+    tok = torch.as_tensor(tokens)
+    if tok.ndim == 1:
+        tok = tok[None]
+    if tok.ndim != 2:
+        raise ValueError(f"tokens must be [B, T], got {tuple(tok.shape)}")
+    B, T = tok.shape
+    pos = [int(v) for v in torch.as_tensor(positions).reshape(-1).tolist()]
+    if len(pos) != T:
+        raise ValueError(f"{len(pos)} positions for {T} tokens")
+    if B > cache["page_table"].shape[0]:
+        raise ValueError(f"{B} token rows for a cache of {cache['page_table'].shape[0]} sequences")
+    if T and int(torch.as_tensor(write_at).item() if isinstance(write_at, torch.Tensor) else write_at) != pos[0]:
+        raise ValueError("write_at must equal positions[0] (the cache rows are written at the token positions)")
+    n = T
     if isinstance(masks, dict) and "prompt_len" in masks:
         n = min(n, int(masks["prompt_len"]))
-    r = runner_for(cfg, params, cache)
-    combine = "f32" if dense_moe else "bf16_running"
-    keep = range(n) if last_index is None else [int(last_index)]
-    out = torch.empty((1, len(keep), cfg.vocab_size), dtype=torch.float32, device=r.device)
-    j = 0
+    rs = _runners_for(cfg, params, cache)
+    r, hr = rs["decode"], rs["head"]
     for t in range(n):
         if not 0 <= pos[t] < r.max_len:
             raise ValueError(f"position {pos[t]} outside the cache (max_len {r.max_len})")
-        r.set_state(tok[t], pos[t])
-        r.launch(combine, advance=False)
-        if last_index is None or t == int(last_index):
-            out[0, j].copy_(r.logits)
-            j += 1
+    if last_index is not None and not 0 <= int(last_index) < max(n, 1):
+        raise ValueError(f"last_index {int(last_index)} outside the {n} computed rows")
+    keep = list(range(n)) if last_index is None else [int(last_index)]
+    out = torch.zeros((B, T if last_index is None else 1, cfg.vocab_size), dtype=torch.float32, device=r.device)
+    consecutive = all(pos[t] == pos[0] + t for t in range(n))
+    if n > 1 and dense_moe and consecutive:
+        pr = rs["prefill"]
+        if pr is None or pr.capacity < n:
+            rs["prefill"] = None
+            pr = rs["prefill"] = PrefillRunner(cfg, params, cache, min(r.max_len, max(n, 256)), device=r.device,
+                                               rope=r.rope)
+        tok_dev = tok.to(device=r.device, dtype=torch.int32)
+        for b in range(B):
+            pr.run(tok_dev[b].contiguous(), n, seq=b, p0=pos[0])
+            for j, t in enumerate(keep):
+                hr.logits_of(pr.x1[t], pr.mlp_out[t], None if pr.moe_out is None else pr.moe_out[t], out=out[b, j])
+        return out, cache
+    combine = "f32" if dense_moe else "bf16_running"
+    tok_host = tok.tolist()
+    try:
+        for b in range(B):
+            r.set_sequence(b)
+            j = 0
+            for t in range(n):
+                r.set_state(tok_host[b][t], pos[t])
+                r.launch(combine, advance=False)
+                if last_index is None or t == int(last_index):
+                    out[b, j].copy_(r.logits)
+                    j += 1
+    finally:
+        r.set_sequence(0)
     return out, cache

@@ -671,3 +671,74 @@ def argmax_rows(logits_bf16, softcap, tok, pos=None, hist=None, logits_f32=None)
     ws = WORKSPACE.get(logits_bf16.device, "argmax_rows", int(_lib.lib().g4mi_argmax_rows_workspace_bytes(B)))
     _lib.call("g4mi_argmax_rows", _ptr(logits_bf16), B, V, float(softcap or 0.0), _ptr(logits_f32), _ptr(tok),
               _ptr(pos), _ptr(hist), hist_len, _ptr(ws), ws.numel(), stream_handle(logits_bf16.device))
+
+
+# ------------------------------------------------------------------------- model primitives
+def _dtype_code(t: torch.Tensor, name: str) -> int:
+    if t.dtype == torch.bfloat16:
+        return 0
+    if t.dtype == torch.float32:
+        return 1
+    raise TypeError(f"{name}: bf16 or f32 expected, got {t.dtype}")
+
+
+def _on_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name}: a device tensor is expected (the kernels have no CPU path)")
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor | None, eps: float) -> torch.Tensor:
+    """model.py:42-47 over the last axis of x (bf16 or f32) -> x's dtype."""
+    _on_device(x, "rms_norm x")
+    x = x.contiguous()
+    dim = x.shape[-1]
+    w_code = 0
+    if weight is not None:
+        weight = weight.contiguous()
+        w_code = _dtype_code(weight, "rms_norm weight")
+        if weight.numel() != dim:
+            raise ValueError(f"rms_norm: weight has {weight.numel()} elements, x's last axis {dim}")
+    out = torch.empty_like(x)
+    _lib.call("g4mi_rms_norm", _ptr(x), _dtype_code(x, "rms_norm x"), _ptr(weight), w_code, x.numel() // max(dim, 1),
+              dim, float(eps), _ptr(out), stream_handle(x.device))
+    return out
+
+
+def gelu(x: torch.Tensor) -> torch.Tensor:
+    """model.py:50-51: tanh-approximation GELU, x's dtype."""
+    _on_device(x, "gelu x")
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    _lib.call("g4mi_gelu_tanh", _ptr(x), _dtype_code(x, "gelu x"), x.numel(), _ptr(out), stream_handle(x.device))
+    return out
+
+
+def rope_tables(positions: torch.Tensor, inv_freq: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """model.py:64-67: (cos, sin) f32 [T, 2 * len(inv_freq)] on positions' device."""
+    _on_device(positions, "rope_tables positions")
+    pos = positions.reshape(-1).to(torch.int32).contiguous()
+    inv = inv_freq.to(device=pos.device, dtype=torch.float32).contiguous()
+    T, half = pos.numel(), inv.numel()
+    cos = torch.empty((T, 2 * half), dtype=torch.float32, device=pos.device)
+    sin = torch.empty_like(cos)
+    _lib.call("g4mi_rope_tables", _ptr(pos), T, _ptr(inv), half, _ptr(cos), _ptr(sin), stream_handle(pos.device))
+    return cos, sin
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """model.py:70-78: x [B, T, ..., D]; cos/sin [T, D] broadcast over B and
+    the head axes."""
+    _on_device(x, "apply_rope x")
+    if x.ndim < 3:
+        raise ValueError("apply_rope: x must be [B, T, ..., D]")
+    x = x.contiguous()
+    B, T, D = x.shape[0], x.shape[1], x.shape[-1]
+    inner = x.numel() // max(B * T * D, 1)
+    c = cos.to(device=x.device, dtype=torch.float32).reshape(-1, D).contiguous()
+    s = sin.to(device=x.device, dtype=torch.float32).reshape(-1, D).contiguous()
+    if c.shape[0] != T or s.shape[0] != T:
+        raise ValueError(f"apply_rope: tables hold {c.shape[0]} positions, x {T}")
+    out = torch.empty_like(x)
+    _lib.call("g4mi_apply_rope", _ptr(x), _dtype_code(x, "apply_rope x"), _ptr(c), _ptr(s), B, T, inner, D, _ptr(out),
+              stream_handle(x.device))
+    return out

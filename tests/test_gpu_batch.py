@@ -4,11 +4,11 @@
 Three prompts of 40, 77 and 128 tokens (rng 0, 1, 2) share one page pool; a
 fourth row repeats the last prompt.  Each sequence is prefilled into its own
 pages, then all advance together for 12 greedy tokens.  Each sequence's
-tokens are checked against the oracle run on that prompt alone
-(oracle.twin.prefill_then_decode): the first token must match and the first
-divergence, if any, may not come before step 8 (the batched path's GEMMs
-accumulate in another order than the single-sequence GEMVs and the oracle's
-f64, so a near tie late in the stream may resolve the other way).
+tokens are checked against the oracle run on that prompt alone, teacher
+forced on the GPU's tokens (oracle.twin.prefill_then_decode): every token is
+the oracle's greedy choice or a declared near tie (top-two oracle logits
+within 2e-3; the batched path's GEMMs accumulate in another order than the
+single-sequence GEMVs and the oracle's f64).
 """
 
 import numpy as np
@@ -18,6 +18,7 @@ import torch
 from gemma4_mi.batch import BatchEngine
 from gemma4_mi.config import tiny_parity_config
 from gemma4_mi.weights import init_random_params
+from greedy_check import check_stream
 from oracle import twin
 
 pytestmark = pytest.mark.gpu
@@ -35,18 +36,15 @@ def test_batched_decode_matches_single_sequence_oracle():
     used = sum(len(o) for o in eng.pool.owned)
     assert used == sum((n + 12 + 63) // 64 for n in list(lens) + [lens[-1]])
     for b, pr in enumerate(prompts):
-        _, exp = twin.prefill_then_decode(cfg, params_cpu, pr, 11, 256)
-        div = next((i for i, (x, y) in enumerate(zip(got[b], exp)) if x != y), None)
-        print(f"sequence {b} ({len(pr)} tokens): gpu {got[b][:6]} oracle {list(exp[:6])}, first divergence {div}")
-        assert got[b][0] == exp[0]
-        assert div is None or div >= 8
+        print(f"sequence {b} ({len(pr)} tokens): gpu {got[b][:6]}")
+        check_stream(cfg, params_cpu, pr, got[b], 256, what=f"sequence {b}")
 
 
 def test_batched_decode_above_eight_rows_uses_grouped_experts():
     """Ten rows (the grouped expert path, each selected expert read once per
     step): rows holding the same prompt produce the same tokens, and each
-    distinct prompt's tokens follow the single-sequence oracle (first token
-    equal, no divergence before step 8)."""
+    distinct prompt's tokens follow the single-sequence oracle (greedy
+    choices or declared near ties)."""
     cfg = tiny_parity_config()
     params = init_random_params(cfg, 0, device=DEV)
     params_cpu = twin.random_params(cfg, 0)
@@ -59,9 +57,7 @@ def test_batched_decode_above_eight_rows_uses_grouped_experts():
     for b in range(10):
         assert got[b] == got[b % 3], b
     for i, pr in enumerate(base):
-        _, exp = twin.prefill_then_decode(cfg, params_cpu, pr, 9, 192)
-        div = next((j for j, (x, y) in enumerate(zip(got[i], exp)) if x != y), None)
-        assert got[i][0] == exp[0] and (div is None or div >= 8), (i, div)
+        check_stream(cfg, params_cpu, pr, got[i], 192, what=f"prompt {i}")
 
 
 def test_batched_rows_are_independent():

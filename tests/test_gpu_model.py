@@ -22,6 +22,7 @@ import torch
 from gemma4_mi import model as gm
 from gemma4_mi.config import tiny_parity_config
 from gemma4_mi.weights import init_random_params
+from greedy_check import check_stream
 from oracle import twin
 
 pytestmark = pytest.mark.gpu
@@ -152,8 +153,10 @@ def test_batched_prefill_matches_oracle(c1):
 
 
 def test_free_running_greedy(c1):
-    """The device-resident loop (argmax feeds the next step) against the oracle's
-    free-running greedy tokens; reports the first divergence."""
+    """The device-resident loop (argmax feeds the next step): every token is
+    the oracle's greedy choice on the same history or a declared near tie
+    (the oracle is run teacher-forced on the GPU's tokens); the first
+    divergence from the oracle's own free-running stream is printed."""
     cfg, params_cpu, params, prompt, logits_o, gen_o, _ = c1
     cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
     r = gm.runner_for(cfg, params, cache)
@@ -168,8 +171,7 @@ def test_free_running_greedy(c1):
     gen_g = r.hist[P: P + N_DEC + 1].cpu().tolist()
     div = next((i for i, (a, b) in enumerate(zip(gen_g, gen_o)) if a != b), None)
     print(f"free-running greedy: first divergence at step {div}; gpu {gen_g[:8]} oracle {gen_o[:8]}")
-    assert gen_g[0] == gen_o[0]
-    assert div is None or div >= 8
+    check_stream(cfg, params_cpu, prompt, gen_g, MAX_LEN, TIE, "free-running greedy")
 
 
 def test_long_context_prefill_then_decode():

@@ -198,3 +198,21 @@ def test_page_pool_allocates_and_releases_pages():
     assert len(pool.owned[0]) == 4 and len(set(pt[0].tolist())) == 4
     with pytest.raises(ValueError):
         pool.ensure(1, 257)
+
+
+def test_make_mesh_is_a_one_device_stand_in():
+    """model.py:159-161 callers read mesh.devices.size (engine.py:39) and use
+    the mesh as a context manager (tests/test_parity.py:88-90)."""
+    from gemma4_mi import model as M
+
+    mesh = M.make_mesh()
+    assert int(mesh.devices.size) == 1 and mesh.axis_names == ("tp",) and mesh.size == 1
+    with mesh as m:
+        assert m is mesh
+
+
+def test_fold_in_keys():
+    from gemma4_mi import model as M
+
+    assert M.fold_in(7, 3) == (7, 3)
+    assert M.fold_in((7, 99), 5) == (7, 5)
