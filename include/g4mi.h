@@ -143,6 +143,30 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
                           int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx, void* ws,
                           int64_t ws_bytes, void* stream);
 
+/* g4mi_decode_attention without a workspace argument.  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * split-K scratch lives in a file-scope device array of
+ * G4MI_NOALLOC_ATTENTION_SCRATCH_BYTES per GPU, loaded with the library and
+ * held until the process ends; its address is looked up once per device on
+ * the first call made with that device current.  A call whose
+ * g4mi_decode_attention_workspace_bytes() exceeds that size is rejected with
+ * G4MI_EWORKSPACE (nothing is launched); the 26B-A4B decode step at 32,768
+ * positions needs 6.6 MiB.  Each call first zeroes its arrival counters with
+ * a fill kernel on `stream`, then runs the same kernels as
+ * g4mi_decode_attention.  Every call on one GPU shares that GPU's array:
+ * calls that may overlap on one GPU (other streams, other host threads) race
+ * and give wrong results; order them on one stream.  Nothing is allocated or
+ * freed. */
+#define G4MI_NOALLOC_ATTENTION_SCRATCH_BYTES (16ll << 20)
+int g4mi_decode_attention_noalloc(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                  const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                                  const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                                  const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B,
+                                  int64_t NH, int64_t KV, int64_t D, int64_t page_size, int64_t window,
+                                  float softcap, float eps, int32_t append, int64_t lmax, int64_t n_split_max,
+                                  uint16_t* ctx, void* stream);
+
 /* Cache append of T tokens of one sequence (model.py:202-206, the
  * dynamic_update_slice of model.py:205-206): k = rope(rms_norm(k_raw, k_norm)),
  * v = rms_norm(v_raw) written at positions pos[T] through page_table_row. */

@@ -25,6 +25,8 @@
 // Device-side positions and page indices are range-checked: an out-of-range
 // position attends to nothing (ctx = 0, no cache write) and an out-of-range
 // page entry is skipped, so bad inputs cannot address outside the buffers.
+#include <mutex>
+
 #include "capi_util.h"
 #include "common.h"
 
@@ -779,6 +781,57 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
 
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
 
+// Zeroes n words (the arrival counters of a call that brings no workspace of
+// its own, see g4mi_decode_attention_noalloc).
+__global__ __launch_bounds__(256) void zero_words_kernel(unsigned int* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) p[i] = 0u;
+}
+
+// ------------------------------------------------------------------ no-allocation scratch
+// The workspace of g4mi_decode_attention_noalloc: a file-scope device array,
+// one copy per GPU, held until the process ends.  Its device address is
+// looked up once per device (hipGetSymbolAddress, with that device current)
+// and only that address is handed to kernels.
+constexpr int64_t kNoAllocScratchBytes = G4MI_NOALLOC_ATTENTION_SCRATCH_BYTES;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+static int scratch_address(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_error("decode_attention_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return (int)e;
+  }
+  G4MI_REQUIRE(dev >= 0 && dev < kMaxDevices, G4MI_EUNSUPPORTED, "decode_attention_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      set_error("decode_attention_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(e));
+      return e != hipSuccess ? (int)e : G4MI_EINVAL;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+// Argument checks and launches shared by the two decode attention entry
+// points.  With clear_counters the workspace's arrival counters are zeroed
+// first by a fill kernel on the same stream (a shared scratch may hold
+// another call's data where this call's counters sit).
+static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                                 const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                                 const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B,
+                                 int64_t NH, int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap,
+                                 float eps, int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx,
+                                 void* ws, int64_t ws_bytes, bool clear_counters, void* stream);
+
 }  // namespace g4mi
 
 using namespace g4mi;
@@ -803,6 +856,45 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
                           int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap, float eps,
                           int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx, void* ws,
                           int64_t ws_bytes, void* stream) {
+  return decode_attention_impl(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, num_pages,
+                               page_table, max_pages, pos, B, NH, KV, D, page_size, window, softcap, eps, append,
+                               lmax, n_split_max, ctx, ws, ws_bytes, false, stream);
+}
+
+int g4mi_decode_attention_noalloc(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                  const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                                  const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                                  const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B,
+                                  int64_t NH, int64_t KV, int64_t D, int64_t page_size, int64_t window,
+                                  float softcap, float eps, int32_t append, int64_t lmax, int64_t n_split_max,
+                                  uint16_t* ctx, void* stream) {
+  G4MI_REQUIRE(B >= 1 && NH >= 1 && D >= 1 && lmax >= 1 && n_split_max >= 1, G4MI_EINVAL,
+               "decode_attention_noalloc: bad B/NH/D/lmax/n_split_max");
+  G4MI_REQUIRE(B <= 65535 && NH <= 65535 && D <= 512 && lmax <= (1 << 20) && n_split_max <= 4096, G4MI_EINVAL,
+               "decode_attention_noalloc: B/NH/D/lmax/n_split_max out of range");
+  const int64_t need = g4mi_decode_attention_workspace_bytes(B, NH, D, lmax, n_split_max);
+  G4MI_REQUIRE(need <= kNoAllocScratchBytes, G4MI_EWORKSPACE,
+               "decode_attention_noalloc: this call needs %lld bytes of scratch, more than the %lld held per device",
+               (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_address(&ws);
+  if (rc != 0) return rc;
+  return decode_attention_impl(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, num_pages,
+                               page_table, max_pages, pos, B, NH, KV, D, page_size, window, softcap, eps, append,
+                               lmax, n_split_max, ctx, ws, kNoAllocScratchBytes, true, stream);
+}
+
+}  // extern "C"
+
+namespace g4mi {
+
+static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, const uint16_t* v_raw,
+                                 const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* rope_cos,
+                                 const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,
+                                 const int32_t* page_table, int64_t max_pages, const int32_t* pos, int64_t B,
+                                 int64_t NH, int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap,
+                                 float eps, int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx,
+                                 void* ws, int64_t ws_bytes, bool clear_counters, void* stream) {
   G4MI_REQUIRE(q_raw && q_norm && rope_cos && rope_sin && k_pages && v_pages && page_table && pos && ctx && ws,
                G4MI_EINVAL, "decode_attention: null pointer argument");
   G4MI_REQUIRE(!append || (k_raw && k_norm), G4MI_EINVAL, "decode_attention: append needs k_raw and k_norm");
@@ -837,6 +929,10 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
   w.part = (float*)((char*)w.stats + al256(2 * B * NH * n_split_max * 4));
   w.group = (float*)((char*)w.part + al256(B * n_split_max * NH * D * 4));
   hipStream_t st = as_stream(stream);
+  if (clear_counters) {
+    const int64_t words = B * NH * (kMaxGroups + 1);
+    hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, w.counters, words);
+  }
   dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
 #define G4MI_ATT(DD, GG)                                                                                         \
   if (D == DD && G == GG)                                                                                        \
@@ -849,6 +945,10 @@ int g4mi_decode_attention(const uint16_t* q_raw, const uint16_t* k_raw, const ui
 #undef G4MI_ATT
   return check_launch("decode_attention");
 }
+
+}  // namespace g4mi
+
+extern "C" {
 
 int g4mi_kv_append(const uint16_t* k_raw, const uint16_t* v_raw, const uint16_t* k_norm, const uint16_t* rope_cos,
                    const uint16_t* rope_sin, uint16_t* k_pages, uint16_t* v_pages, int64_t num_pages,

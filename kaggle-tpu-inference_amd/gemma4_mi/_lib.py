@@ -105,6 +105,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _int,
         [_p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f32, _i32, _p, _p, _p, _p, _i64, _p],
     ),
+    "g4mi_decode_attention_noalloc": (
+        _int,
+        [_p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _f32,
+         _i32, _i64, _i64, _p, _p],
+    ),
     "g4mi_rms_norm": (_int, [_p, _i32, _p, _i32, _i64, _i64, _f32, _p, _p]),
     "g4mi_gelu_tanh": (_int, [_p, _i32, _i64, _p, _p]),
     "g4mi_rope_tables": (_int, [_p, _i64, _p, _i64, _p, _p, _p]),

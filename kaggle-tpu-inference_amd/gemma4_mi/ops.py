@@ -742,3 +742,20 @@ def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.T
     _lib.call("g4mi_apply_rope", _ptr(x), _dtype_code(x, "apply_rope x"), _ptr(c), _ptr(s), B, T, inner, D, _ptr(out),
               stream_handle(x.device))
     return out
+
+
+def decode_attention_noalloc(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table,
+                             pos, window, softcap, eps, lmax, n_split_max, ctx, append=True):
+    """decode_attention through g4mi_decode_attention_noalloc: the same
+    kernels with the split-K scratch in the library's per-device array (no
+    workspace argument, nothing allocated here: ctx is the caller's)."""
+    b, nh, d = q_raw.shape
+    num_pages, kv, page, _ = k_pages.shape
+    _need(ctx, BF16, "ctx", (b, nh, d))
+    _need(pos, torch.int32, "pos", (b,))
+    _need(page_table, torch.int32, "page_table")
+    _lib.call("g4mi_decode_attention_noalloc", _ptr(q_raw), _ptr(k_raw), _ptr(v_raw), _ptr(q_norm), _ptr(k_norm),
+              _ptr(rope_cos), _ptr(rope_sin), _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table),
+              page_table.shape[1], _ptr(pos), b, nh, kv, d, page, int(window), float(softcap or 0.0), float(eps),
+              1 if append else 0, int(lmax), int(n_split_max), _ptr(ctx), stream_handle(q_raw.device))
+    return ctx
