@@ -246,13 +246,18 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   // selection are this kernel's longest chain
   const int rblocks = (int)gridDim.x - a.dense_blocks;
   const bool dense = (int)blockIdx.x >= rblocks;
-  // prologue operands first (see layer_in), then the weight rows
+  // prologue operands first (see layer_in), then the weight rows.  Every
+  // load is unconditional (a valid stand-in pointer where an operand is
+  // absent): under a branch the compiler waits for the load inside it,
+  // before the weight rows below are requested.  The per-expert scale the
+  // selection multiplies in comes first: the selection is the kernel's tail.
+  const float pes_t = bf2f(((a.pes != nullptr) ? a.pes : a.x)[min(tid, max(a.E, 1) - 1)]);
   Vec x, o, wpa, wf, rsc;
   vload(o, a.o, NCH);
   vload(x, a.x, NCH);
   vload(wpa, a.w_pa, NCH);
   vload(wf, dense ? a.w_pf : a.w_pf2, NCH);
-  if (!dense) vload(rsc, a.r_scale, NCH);
+  vload(rsc, (!dense && a.r_scale != nullptr) ? a.r_scale : a.w_pa, NCH);
   // dense: this block owns tasks (one (gate, up) row pair each) [t0, tend),
   // wave w takes t0+w, t0+w+4, ...; router blocks own 8 expert rows each.
   const int t0 = ((int)blockIdx.x - rblocks) * a.tasks_per_block;
@@ -333,7 +338,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     const float sv = (t < a.E) ? __hip_atomic_load(a.scores + min(t, a.E - 1), __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT)
                                : -INFINITY;
-    block_select_values(sv, a.pes, a.E, a.K, L);
+    block_select_values_pes(sv, pes_t, a.E, a.K, L);
     if (t < a.K) {
       a.top_w[t] = L.topw[t];
       a.top_i[t] = L.topi[t];

@@ -24,9 +24,22 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned int)v, CTRL, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned int)(v >> 32), CTRL, 0xF, 0xF, false);
+  return ((unsigned long long)(unsigned int)hi << 32) | (unsigned int)lo;
+}
+__device__ __forceinline__ unsigned long long max_u64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+
 // Selection shared state (LDS) of one 256-thread block.
 struct SelectLds {
-  unsigned long long key[kMaxE];
+  alignas(16) unsigned long long key[kMaxE];  // candidate keys, compacted
+  unsigned long long rowmax[16];
+  unsigned long long thresh;
+  int wcnt[4];
   float pes[kMaxE];
   int rank_part[256];
   float topp[kMaxK];
@@ -44,12 +57,14 @@ struct SelectLds {
 //
 // Ranking: probabilities are >= 0, so their f32 bit patterns order like the
 // values; key = (bits(p) << 32) | ~index makes every key distinct and orders
-// ties by lower index, so rank(t) = #{e : key[e] > key[t]}.  The E*E key
-// comparisons are spread over all 256 threads (256/E threads per expert).
-// `s` is thread t's score (t < E), -inf for t >= E.
-__device__ void block_select_values(float s, const uint16_t* __restrict__ pes, int E, int K, SelectLds& L) {
+// ties by lower index, so rank(t) = #{e : key[e] > key[t]}; only the keys
+// that can be among the K largest are ranked (see below).
+// `s` is thread t's score (t < E), -inf for t >= E; `pes_t` is thread t's
+// per_expert_scale value (requested early by callers on a latency-bound
+// path: a global load here would put its round trip on the critical path).
+__device__ void block_select_values_pes(float s, float pes_t, int E, int K, SelectLds& L) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
-  if (t < E) L.pes[t] = bf2f(pes[t]);
+  if (t < E) L.pes[t] = pes_t;
   const float wm = wave_max(s);
   if (lane == 0) L.redf[w] = wm;
   __syncthreads();
@@ -60,31 +75,47 @@ __device__ void block_select_values(float s, const uint16_t* __restrict__ pes, i
   __syncthreads();
   const float total = (float)(L.redd[0] + L.redd[1] + L.redd[2] + L.redd[3]);
   const float p = (t < E) ? ex / total : 0.0f;
-  if (t < E) L.key[t] = ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)(~t);
+  // Ranking by key = (bits(p) << 32) | ~index (distinct; ties go to the
+  // lower index).  Only keys >= T can be among the K largest, where T is the
+  // K-th largest of the 16-lane row maxima (K distinct keys are >= T) or 0
+  // with fewer than K rows; those candidates are compacted into LDS and
+  // ranked among themselves, which gives their global ranks, since every
+  // key above a top-K key is >= T as well.
+  const unsigned long long key = (t < E) ? ((unsigned long long)__float_as_uint(p) << 32) | (unsigned)(~t) : 0ull;
+  unsigned long long rm = key;
+  rm = max_u64(rm, dpp_u64<kDppXor1>(rm));
+  rm = max_u64(rm, dpp_u64<kDppXor2>(rm));
+  rm = max_u64(rm, dpp_u64<kDppHalfMirror>(rm));
+  rm = max_u64(rm, dpp_u64<kDppMirror>(rm));
+  if ((lane & 15) == 0) L.rowmax[t >> 4] = rm;
   __syncthreads();
-  const int parts = max(1, 256 / E);
-  const int chunk = (E + parts - 1) / parts;
-  const int part = t / E, et = t - part * E;
-  if (part < parts) {
-    const unsigned long long mine = L.key[et];
-    const int e0 = part * chunk, e1 = min(E, e0 + chunk);
-    int r0 = 0, r1 = 0;
-    int e = e0;
-#pragma unroll 4
-    for (; e + 1 < e1; e += 2) {
-      r0 += L.key[e] > mine;
-      r1 += L.key[e + 1] > mine;
-    }
-    if (e < e1) r0 += L.key[e] > mine;
-    L.rank_part[t] = r0 + r1;
+  const int nrows = (E + 15) / 16;
+  if (nrows < K) {
+    if (t == 0) L.thresh = 1ull;  // every real key (nonzero) is a candidate
+  } else if (t < nrows) {
+    const unsigned long long mine = L.rowmax[t];
+    int r = 0;
+    for (int q = 0; q < nrows; ++q) r += (L.rowmax[q] > mine) ? 1 : 0;
+    if (r == K - 1) L.thresh = mine;
   }
   __syncthreads();
-  if (t < E) {
+  const bool cand = key >= L.thresh && t < E;
+  const unsigned long long bal = __ballot(cand);
+  const int before = __builtin_amdgcn_mbcnt_hi((unsigned)(bal >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)bal, 0));
+  if (lane == 0) L.wcnt[w] = __popcll(bal);
+  __syncthreads();
+  int off = 0;
+  for (int q = 0; q < w; ++q) off += L.wcnt[q];
+  const int C = L.wcnt[0] + L.wcnt[1] + L.wcnt[2] + L.wcnt[3];
+  if (cand) L.key[off + before] = key;
+  __syncthreads();
+  if (t < C) {
+    const unsigned long long mine = L.key[t];
     int rank = 0;
-    for (int q = 0; q < parts; ++q) rank += L.rank_part[q * E + t];
+    for (int j = 0; j < C; ++j) rank += (L.key[j] > mine) ? 1 : 0;
     if (rank < K) {
-      L.topp[rank] = p;
-      L.topi[rank] = t;
+      L.topp[rank] = __uint_as_float((unsigned int)(mine >> 32));
+      L.topi[rank] = (int)(~(unsigned int)mine);
     }
   }
   __syncthreads();
@@ -94,6 +125,12 @@ __device__ void block_select_values(float s, const uint16_t* __restrict__ pes, i
     if (t < K) L.topw[t] = (L.topp[t] / sk) * L.pes[L.topi[t]];
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void block_select_values(float s, const uint16_t* __restrict__ pes, int E, int K,
+                                                    SelectLds& L) {
+  const int t = threadIdx.x;
+  block_select_values_pes(s, (t < E) ? bf2f(pes[t]) : 0.0f, E, K, L);
 }
 
 __device__ __forceinline__ void block_select(const float* __restrict__ srow, const uint16_t* __restrict__ pes, int E,
