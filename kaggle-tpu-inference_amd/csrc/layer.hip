@@ -399,6 +399,15 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
 #pragma unroll
     for (int i = 0; i < DIT; ++i) wd[i] = ld_stream(drow + min(lane + 64 * i, ich - 1));
   }
+  // this lane group's slot activations (written by the previous kernel):
+  // requested with the weight rows, not after them
+  u32x4 am[FIT];
+  {
+    const u32x4* avm = (const u32x4*)((a.act_moe != nullptr ? a.act_moe : a.act_mlp) +
+                                      (size_t)(a.act_moe != nullptr ? min(g, max(a.K, 1) - 1) : 0) * F);
+#pragma unroll
+    for (int i = 0; i < FIT; ++i) am[i] = ld16(avm + (a.act_moe != nullptr ? l8 + 8 * i : 0));
+  }
   const int e = (g < a.K && ei >= 0 && ei < a.E) ? ei : -1;
   u32x4 we[FIT];
   if (a.e_down != nullptr) {
@@ -422,9 +431,8 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
     if (a.e_down != nullptr) {
       float part = 0.0f;
       if (e >= 0) {
-        const u32x4* avm = (const u32x4*)(a.act_moe + (size_t)g * F);
 #pragma unroll
-        for (int i = 0; i < FIT; ++i) part = dot8(we[i], ld16(avm + l8 + 8 * i), part);
+        for (int i = 0; i < FIT; ++i) part = dot8(we[i], am[i], part);
       }
       part = group_sum<8>(part);
       float run = 0.0f;
