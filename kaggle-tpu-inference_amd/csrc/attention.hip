@@ -75,22 +75,25 @@ __device__ __forceinline__ long long page_off_lds(const AttnDims& a, const int* 
   return ((((long long)page * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
 }
 
-// Requests the page-table entries of pages [first, first + 2*256) of one
-// sequence (clamped to the row) into registers; stage_store() writes them to
-// LDS before the block's next barrier.  A split spans at most kChunkMax + 1
-// pages.
+// Requests the page-table entries of pages [first, first + 512) of one
+// sequence (clamped to the row) into registers of an NT-thread block;
+// stage_store() writes them to LDS before the block's next barrier.  A split
+// spans at most kChunkMax + 1 pages.
+template <int NT = 256>
 struct PtStage {
-  int v[2];
+  int v[512 / NT];
 };
-__device__ __forceinline__ PtStage stage_load(const AttnDims& a, const int32_t* pt_row, int first) {
-  PtStage s;
+template <int NT = 256>
+__device__ __forceinline__ PtStage<NT> stage_load(const AttnDims& a, const int32_t* pt_row, int first) {
+  PtStage<NT> s;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) s.v[r] = pt_row[min(first + (int)threadIdx.x + 256 * r, a.max_pages - 1)];
+  for (int r = 0; r < 512 / NT; ++r) s.v[r] = pt_row[min(first + (int)threadIdx.x + NT * r, a.max_pages - 1)];
   return s;
 }
-__device__ __forceinline__ void stage_store(const PtStage& s, int* ptl) {
+template <int NT = 256>
+__device__ __forceinline__ void stage_store(const PtStage<NT>& s, int* ptl) {
 #pragma unroll
-  for (int r = 0; r < 2; ++r) ptl[threadIdx.x + 256 * r] = s.v[r];
+  for (int r = 0; r < 512 / NT; ++r) ptl[threadIdx.x + NT * r] = s.v[r];
 }
 
 __device__ __forceinline__ float wave_max_bfly(float m) {
@@ -149,17 +152,22 @@ __device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const 
 // 16-position tiles w, w+4, ... of the split; the next tile's K loads are in
 // flight while the current one is multiplied.  ONE: the launch guarantees
 // at most kChunkMin positions per split (one tile per wave), so there is
-// nothing to prefetch.
-template <int D, int G, bool ONE>
-__global__ __launch_bounds__(256) void attn_qk_kernel(
+// nothing to prefetch.  NW = 8 (long ranges): 8 waves, and every tile a wave
+// owns (tiles w and w + 8 of a split's 16 at most) is requested before the
+// prologue, so a whole split's K rows are in flight at once.
+template <int D, int G, bool ONE, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
     AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
     const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
     const uint16_t* __restrict__ rope_cos, const uint16_t* __restrict__ rope_sin, uint16_t* __restrict__ k_pages,
     uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table, const int32_t* __restrict__ pos_arr,
     int append, float* __restrict__ ws_scores, float* __restrict__ ws_stats) {
   constexpr int PL = D / 64;
-  constexpr int GW = (G + 3) / 4;
+  constexpr int NT = NW * 64;
+  constexpr int GW = (G + NW - 1) / NW;
   constexpr int KS = D / 32;  // MFMA steps along the head dimension
+  constexpr int TPW = (NW == 8 && !ONE) ? kChunkMax / 16 / NW : 1;  // tiles requested up front per wave
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   __shared__ __align__(16) uint16_t qa[16 * D];
   __shared__ __align__(16) uint16_t kn16[D];
   __shared__ float knew[D];
@@ -185,7 +193,7 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   const int kg = lane >> 4, col = lane & 15;
   const int ntiles = (npos + 15) >> 4;
   const int first = start / a.page;
-  const PtStage pts = stage_load(a, pt_row, first);
+  const PtStage<NT> pts = stage_load<NT>(a, pt_row, first);
   auto load_tile = [&](int t, u32x4* bf, long long& off) {
     const int jc = min(t * 16 + col, npos - 1);
     off = page_off_lds(a, ptl, first, start + jc, kv);
@@ -193,8 +201,12 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
 #pragma unroll
     for (int s = 0; s < KS; ++s) bf[s] = ld16((const u32x4*)(kp + 32 * s));
   };
-  const int jc0 = min(min(wave, ntiles - 1) * 16 + col, npos - 1);
-  const int pe0 = pt_row[(start + jc0) / a.page];
+  int jc0[TPW], pe0[TPW];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    jc0[tt] = min(min(wave + NW * tt, ntiles - 1) * 16 + col, npos - 1);
+    pe0[tt] = pt_row[(start + jc0[tt]) / a.page];
+  }
 
   // Prologue: wave w owns q heads w, w+4 (G <= 8); with the append, waves 2
   // and 3 also own the new K and V rows.
@@ -204,7 +216,7 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
   float qx[GW][PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
 #pragma unroll
   for (int u = 0; u < GW; ++u)
-    load_slice<PL>(q_raw + ((size_t)b * a.NH + kv * G + min(wave + 4 * u, G - 1)) * D + so, qx[u]);
+    load_slice<PL>(q_raw + ((size_t)b * a.NH + kv * G + min(wave + NW * u, G - 1)) * D + so, qx[u]);
   load_slice<PL>(q_norm + so, qw);
   load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
   load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
@@ -214,20 +226,22 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
     load_slice<PL>((wave == 2 ? kr : vr) + so, kvx);
     load_slice<PL>((mine ? k_norm : q_norm) + so, kw);
   }
-  u32x4 bcur[KS];
-  long long ocur;
-  {
-    const bool valid = pe0 >= 0 && pe0 < a.num_pages;
-    ocur = valid ? ((((long long)pe0 * a.KV + kv) * a.page) + ((start + jc0) % a.page)) * (long long)D : -1ll;
-    const uint16_t* kp = k_pages + max(ocur, 0ll) + 8 * kg;
+  u32x4 bt[TPW][KS];
+  long long ot[TPW];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) bcur[s] = ld16((const u32x4*)(kp + 32 * s));
+  for (int tt = 0; tt < TPW; ++tt) {
+    const bool valid = pe0[tt] >= 0 && pe0[tt] < a.num_pages;
+    ot[tt] = valid ? ((((long long)pe0[tt] * a.KV + kv) * a.page) + ((start + jc0[tt]) % a.page)) * (long long)D
+                   : -1ll;
+    const uint16_t* kp = k_pages + max(ot[tt], 0ll) + 8 * kg;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bt[tt][s] = ld16((const u32x4*)(kp + 32 * s));
   }
   // padding rows G..15 of the A operand are zero
-  for (int c = tid; c < (16 - G) * D / 8; c += 256) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
+  for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
-    const int g = wave + 4 * u;
+    const int g = wave + NW * u;
     if (g < G) {
       norm_rope_slice<D>(qx[u], qw, cs, sn, a.eps, true);
 #pragma unroll
@@ -243,12 +257,12 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
       if (wave == 2) kn16[so + i] = f2bf(kvx[i]);
     }
   }
-  stage_store(pts, ptl);
+  stage_store<NT>(pts, ptl);
   __syncthreads();
   if (mine) {
     const long long off = page_off_lds(a, ptl, first, pos, kv);
     if (off >= 0)
-      for (int d = tid; d < D; d += 256) {
+      for (int d = tid; d < D; d += NT) {
         k_pages[off + d] = f2bf(knew[d]);
         v_pages[off + d] = f2bf(vnew[d]);
       }
@@ -282,8 +296,16 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
     }
   };
   if constexpr (ONE) {
-    if (wave < ntiles) score_tile(wave, bcur, ocur);
+    if (wave < ntiles) score_tile(wave, bt[0], ot[0]);
+  } else if constexpr (NW == 8) {
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt)
+      if (wave + NW * tt < ntiles) score_tile(wave + NW * tt, bt[tt], ot[tt]);
   } else {
+    u32x4 bcur[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) bcur[s] = bt[0][s];
+    long long ocur = ot[0];
     for (int t = wave; t < ntiles; t += 4) {
       u32x4 bnext[KS];
       long long onext;
@@ -297,11 +319,11 @@ __global__ __launch_bounds__(256) void attn_qk_kernel(
     }
   }
   __syncthreads();
-  // the split's max and sum of exp per head: wave w owns heads w, w+4, so
+  // the split's max and sum of exp per head: wave w owns heads w, w+NW, so
   // the heads reduce in parallel and no further barrier is needed
 #pragma unroll
   for (int u = 0; u < GW; ++u) {
-    const int g = wave + 4 * u;
+    const int g = wave + NW * u;
     if (g < G) {
       float m = -INFINITY;
       for (int j = lane; j < npos; j += 64) m = fmaxf(m, sc[g][j]);
@@ -342,7 +364,7 @@ constexpr int kMaxGroups = kMaxSplits / kGroup;
 // loads (the sources were written by other blocks of this kernel).  All loads
 // of a half (8 sources) are issued before the first add, so a half costs one
 // round trip.
-template <int E4, int N4>
+template <int E4, int N4, int NT = 256>
 __device__ __forceinline__ void ordered_sum(__amdgpu_buffer_rsrc_t rs, uint32_t base, uint32_t stride, int n,
                                             float4* sum) {
 #pragma unroll
@@ -355,7 +377,7 @@ __device__ __forceinline__ void ordered_sum(__amdgpu_buffer_rsrc_t rs, uint32_t 
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int r = 0; r < E4; ++r) {
-          const int e4 = min((int)threadIdx.x + 256 * r, N4 - 1);
+          const int e4 = min((int)threadIdx.x + NT * r, N4 - 1);
           v[i][r] = coherent_load4(rs, base + (uint32_t)min(h0 + i, n - 1) * stride + 16u * (uint32_t)e4);
         }
 #pragma unroll
@@ -372,11 +394,11 @@ __device__ __forceinline__ void ordered_sum(__amdgpu_buffer_rsrc_t rs, uint32_t 
   }
 }
 
-template <int E4, int N4>
+template <int E4, int N4, int NT = 256>
 __device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
 #pragma unroll
   for (int r = 0; r < E4; ++r) {
-    const int e4 = threadIdx.x + 256 * r;
+    const int e4 = threadIdx.x + NT * r;
     if (e4 < N4) {
       uint2 w;
       w.x = pack2(sum[r].x, sum[r].y);
@@ -387,21 +409,25 @@ __device__ __forceinline__ void store_bf16x4(uint16_t* out, const float4* sum) {
 }
 
 // Merged softmax statistics of the splits of every head of a KV head into
-// mg/sg (LDS): wave w owns heads w, w+4; lanes stride the splits.
+// mg/sg (LDS): wave w owns heads w, w+NW; lanes stride the splits.  The
+// score and statistics pointers of the pv kernels are not __restrict__: with
+// it the compiler may sink their loads past the V rows (and past an asm
+// memory barrier) to where they are used, and the in-order vmcnt wait for
+// them then waits for every V row in flight.
 // load_split_stats requests every head's split statistics (unconditional
 // loads from clamped indices; issue it before any load that waits on a
 // page-table entry), reduce_split_stats merges them.  R.n_eff >= 1.
-template <int G>
+template <int G, int NW = 4>
 struct SplitStats {
-  float m[(G + 3) / 4][kMaxSplits / 64], l[(G + 3) / 4][kMaxSplits / 64];
+  float m[(G + NW - 1) / NW][kMaxSplits / 64], l[(G + NW - 1) / NW][kMaxSplits / 64];
 };
-template <int G>
-__device__ __forceinline__ SplitStats<G> load_split_stats(const AttnDims& a, const Range& R, int kv, int b,
-                                                          int wave, int lane, const float* __restrict__ ws_stats) {
-  SplitStats<G> st;
+template <int G, int NW = 4>
+__device__ __forceinline__ SplitStats<G, NW> load_split_stats(const AttnDims& a, const Range& R, int kv, int b,
+                                                              int wave, int lane, const float* ws_stats) {
+  SplitStats<G, NW> st;
 #pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) {
-    const int h = kv * G + min(wave + 4 * u, G - 1);
+  for (int u = 0; u < (G + NW - 1) / NW; ++u) {
+    const int h = kv * G + min(wave + NW * u, G - 1);
     const float* sm = ws_stats + ((size_t)b * a.NH + h) * a.n_split_max;
     const float* sl = ws_stats + ((size_t)(a.B + b) * a.NH + h) * a.n_split_max;
 #pragma unroll
@@ -413,13 +439,13 @@ __device__ __forceinline__ SplitStats<G> load_split_stats(const AttnDims& a, con
   }
   return st;
 }
-template <int G>
-__device__ __forceinline__ void reduce_split_stats(SplitStats<G>& st, const Range& R, int wave, int lane, float* mg,
+template <int G, int NW = 4>
+__device__ __forceinline__ void reduce_split_stats(SplitStats<G, NW>& st, const Range& R, int wave, int lane, float* mg,
                                                    float* sg) {
   constexpr int Q = kMaxSplits / 64;
 #pragma unroll
-  for (int u = 0; u < (G + 3) / 4; ++u) {
-    const int g = wave + 4 * u;
+  for (int u = 0; u < (G + NW - 1) / NW; ++u) {
+    const int g = wave + NW * u;
     if (g < G) {
       float m = -INFINITY;
 #pragma unroll
@@ -452,16 +478,17 @@ __device__ __forceinline__ void reduce_split_stats(SplitStats<G>& st, const Rang
 constexpr int kShortLen = 512;
 constexpr int kSliceD = 32;
 
-template <int D, int G>
+template <int D, int G, int NW = 4>
 __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int kv, int b,
                                          const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
-                                         const float* __restrict__ ws_scores, const float* __restrict__ ws_stats,
+                                         const float* ws_scores, const float* ws_stats,
                                          uint16_t* __restrict__ ctx, float* pr, float* red, float* mg, float* sg) {
+  constexpr int NT = NW * 64;
   constexpr int LPS = kSliceD / 8;
   constexpr int PPW = 64 / LPS;
-  constexpr int PPB = 4 * PPW;
+  constexpr int PPB = NW * PPW;
   constexpr int NST = kShortLen / PPB;       // V steps per lane at most
-  constexpr int SPT = G * kShortLen / 256;   // scores per thread at most
+  constexpr int SPT = G * kShortLen / NT;    // scores per thread at most
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int slot = lane % PPW, sub = lane / PPW;  // the positions of a step are consecutive lanes
   const int d0 = blockIdx.x * kSliceD + sub * 8;
@@ -478,10 +505,11 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
   float sreg[SPT];
 #pragma unroll
   for (int r = 0; r < SPT; ++r) {
-    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
+    const int idx = tid + NT * r, g = idx / kShortLen, j = idx % kShortLen;
     sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + min(j, len - 1)];
   }
-  SplitStats<G> sst = load_split_stats<G>(a, R, kv, b, wave, lane, ws_stats);
+  SplitStats<G, NW> sst = load_split_stats<G, NW>(a, R, kv, b, wave, lane, ws_stats);
+  asm volatile("" ::: "memory");  // the loads above stay ahead of the V rows in issue order
   u32x4 vv[NST];
   bool ok[NST];
 #pragma unroll
@@ -493,12 +521,12 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
     vv[st] = ld16((const u32x4*)(v_pages + off + d0));
     ok[st] = (st < nst) && (j < len) && valid;
   }
-  reduce_split_stats<G>(sst, R, wave, lane, mg, sg);
+  reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
   __syncthreads();
   // normalised probabilities, rounded to bf16 (model.py:212), zero past len
 #pragma unroll
   for (int r = 0; r < SPT; ++r) {
-    const int idx = tid + 256 * r, g = idx / kShortLen, j = idx % kShortLen;
+    const int idx = tid + NT * r, g = idx / kShortLen, j = idx % kShortLen;
     const float sv = sreg[r];
     if (j < len) pr[g * kShortLen + j] = (sv == -INFINITY) ? 0.0f : rbf(expf(sv - mg[g]) / sg[g]);
   }
@@ -534,29 +562,138 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
       for (int i = 0; i < 8; ++i) red[(wave * G + g) * kSliceD + sub * 8 + i] = acc[g][i];
   }
   __syncthreads();
-  for (int e = tid; e < G * kSliceD; e += 256) {
+  for (int e = tid; e < G * kSliceD; e += NT) {
     const int g = e / kSliceD, dd = e % kSliceD;
-    const float v = ((red[g * kSliceD + dd] + red[(G + g) * kSliceD + dd]) + red[(2 * G + g) * kSliceD + dd]) +
-                    red[(3 * G + g) * kSliceD + dd];
+    float v = red[g * kSliceD + dd];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[(w * G + g) * kSliceD + dd];  // in wave order
     ctx[((size_t)b * a.NH + kv * G + g) * D + blockIdx.x * kSliceD + dd] = f2bf(v);
   }
 }
 
+// pv_long8: the long-range body for 8 waves (NW = 8).  Wave w owns the
+// head dims [w*D/8, (w+1)*D/8): DW/8 lanes per position, PPV positions per
+// wave step, and every step's V row slice of the split is requested at once
+// (at most kChunkMax / PPV steps), so a whole split's V rows are in flight
+// together; then the pairs of steps are dotted with the bf16 probabilities
+// as in the 4-wave body.  Writes the wave's partial sums to v_out (per head,
+// 8 dims per lane, summed over the PPV positions of a step).
 template <int D, int G>
-__global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
+__device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int split, int kv, int b,
+                                         const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
+                                         const float* ws_scores, const float* ws_stats,
+                                         float* lds_f, float* mg, float* sg, float (*v_out)[8], int& dofs_out,
+                                         int& slot_out) {
+  constexpr int NW = 8, NT = 512;
+  constexpr int DW = D / NW;                    // dims per wave
+  constexpr int LPV = DW / 8;                   // lanes per position
+  constexpr int PPV = 64 / LPV;                 // positions per wave step
+  constexpr int MAXST = kChunkMax / PPV;        // steps per split at most
+  constexpr int RS = (G * kChunkMax + NT - 1) / NT;  // scores per thread
+  static_assert(D % (NW * 8) == 0 && MAXST % 2 == 0, "pv_long8 layout");
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int start = R.lo + split * R.chunk;
+  const int end = min(R.lo + R.len, start + R.chunk);
+  const int npos = end - start;
+  const int slot = lane % PPV, sub = lane / PPV;
+  const int dofs = wave * DW + sub * 8;
+  // the split's scores, the split statistics, then every V row of the split
+  float sreg[RS];
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int idx = tid + NT * r, g = min(idx / kChunkMax, G - 1), j = idx % kChunkMax;
+    sreg[r] = ws_scores[((size_t)b * a.NH + kv * G + g) * a.lmax + (start - R.lo) + min(j, npos - 1)];
+  }
+  SplitStats<G, NW> sst = load_split_stats<G, NW>(a, R, kv, b, wave, lane, ws_stats);
+  const int nsteps = (npos + PPV - 1) / PPV;
+  int pg[MAXST];
+#pragma unroll
+  for (int st = 0; st < MAXST; ++st) pg[st] = pt_row[(start + min(st * PPV + slot, npos - 1)) / a.page];
+  // keep the small loads above ahead of the V rows in issue order: vmcnt
+  // waits are in order, and a statistics load moved after the rows would
+  // wait for the whole split's V
+  asm volatile("" ::: "memory");
+  u32x4 vv[MAXST];
+  bool ok[MAXST];
+#pragma unroll
+  for (int st = 0; st < MAXST; ++st) {
+    const int j = st * PPV + slot;
+    const int p = start + min(j, npos - 1);
+    const bool valid = pg[st] >= 0 && pg[st] < a.num_pages;
+    const long long off = ((((long long)(valid ? pg[st] : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+    vv[st] = ld16((const u32x4*)(v_pages + off + dofs));
+    ok[st] = (st < nsteps) && (j < npos) && valid;
+  }
+  reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
+  __syncthreads();
+  // normalised probabilities, rounded to bf16 (model.py:212), as bf16 pairs:
+  // the positions of wave steps 2q and 2q + 1 at lane slot `sl` share word
+  // q * PPV + sl (zero past npos)
+  uint16_t* pr16 = reinterpret_cast<uint16_t*>(lds_f);
+#pragma unroll
+  for (int r = 0; r < RS; ++r) {
+    const int idx = tid + NT * r, g = idx / kChunkMax, j = idx % kChunkMax;
+    if (idx < G * kChunkMax) {
+      const float sv = sreg[r];
+      const float pv = (j < npos && sv != -INFINITY) ? rbf(expf(sv - mg[g]) / sg[g]) : 0.0f;
+      const int step = j / PPV, sl = j % PPV;
+      pr16[g * kChunkMax + ((step >> 1) * PPV + sl) * 2 + (step & 1)] = f2bf(pv);
+    }
+  }
+  __syncthreads();
+  const uint32_t* pr32 = reinterpret_cast<const uint32_t*>(lds_f);
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < MAXST; u += 2) {
+    if (u < nsteps) {
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      const u32x4 va = ok[u] ? vv[u] : z, vb = ok[u + 1] ? vv[u + 1] : z;
+      uint32_t vp[8];
+      vp[0] = __builtin_amdgcn_perm(vb.x, va.x, 0x05040100u);
+      vp[1] = __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u);
+      vp[2] = __builtin_amdgcn_perm(vb.y, va.y, 0x05040100u);
+      vp[3] = __builtin_amdgcn_perm(vb.y, va.y, 0x07060302u);
+      vp[4] = __builtin_amdgcn_perm(vb.z, va.z, 0x05040100u);
+      vp[5] = __builtin_amdgcn_perm(vb.z, va.z, 0x07060302u);
+      vp[6] = __builtin_amdgcn_perm(vb.w, va.w, 0x05040100u);
+      vp[7] = __builtin_amdgcn_perm(vb.w, va.w, 0x07060302u);
+      const int pi = (u >> 1) * PPV + slot;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t pp = pr32[g * (kChunkMax / 2) + pi];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[g][i] = dot2bf(vp[i], pp, acc[g][i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v_out[g][i] = group_sum<PPV>(acc[g][i]);
+  dofs_out = dofs;
+  slot_out = slot;
+}
+
+template <int D, int G, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
                                                       const int32_t* __restrict__ page_table,
                                                       const int32_t* __restrict__ pos_arr,
-                                                      const float* __restrict__ ws_scores,
-                                                      const float* __restrict__ ws_stats, float* ws_part,
+                                                      const float* ws_scores,
+                                                      const float* ws_stats, float* ws_part,
                                                       float* ws_group, unsigned int* counters,
                                                       uint16_t* __restrict__ ctx) {
   constexpr int LPV = D / 32;
   constexpr int PPV = 64 / LPV;
   constexpr int UB = 8;                        // wave steps of V loads in flight
   constexpr int RS = G * kChunkMax / 256;      // scores per thread
-  constexpr int E4 = (G * D / 4 + 255) / 256;  // reduced float4s per thread
-  constexpr int kLdsF = (G * kShortLen + 4 * G * kSliceD > G * kChunkMax) ? G * kShortLen + 4 * G * kSliceD
-                                                                          : G * kChunkMax;
+  constexpr int NT = NW * 64;
+  constexpr int E4 = (G * D / 4 + NT - 1) / NT;  // reduced float4s per thread
+  constexpr int kLdsF = (G * kShortLen + NW * G * kSliceD > G * kChunkMax) ? G * kShortLen + NW * G * kSliceD
+                                                                           : G * kChunkMax;
   __shared__ float lds_f[kLdsF];
   __shared__ float mg[G], sg[G];
   __shared__ int flag;
@@ -567,15 +704,33 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   const Range R = attn_range(a, pos);
   if (R.n_eff > 0 && R.len <= kShortLen) {  // grid.x >= D / kSliceD (see launch_attn)
     if (split < D / kSliceD)
-      pv_short<D, G>(a, R, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, ctx, lds_f,
-                     lds_f + G * kShortLen, mg, sg);
+      pv_short<D, G, NW>(a, R, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, ctx,
+                         lds_f, lds_f + G * kShortLen, mg, sg);
     return;
   }
   if (split >= R.n_eff) {
     if (R.n_eff == 0 && split == 0)  // nothing attended: ctx = 0
-      for (int e = tid; e < G * D; e += 256) ctx[(size_t)b * a.NH * D + (size_t)kv * G * D + e] = 0;
+      for (int e = tid; e < G * D; e += NT) ctx[(size_t)b * a.NH * D + (size_t)kv * G * D + e] = 0;
     return;
   }
+  const size_t hd = (size_t)kv * G * D;  // offset of this KV head's group in [NH, D]
+  const uint32_t sstride = (uint32_t)(a.NH * D * 4);  // bytes per split partial
+  const __amdgpu_buffer_rsrc_t rpart = buffer_rsrc(ws_part, (uint32_t)(a.B * a.n_split_max) * sstride);
+  const uint32_t pbase = (uint32_t)(((size_t)b * a.n_split_max + split) * sstride + hd * 4);
+  if constexpr (NW == 8) {
+    float v[G][8];
+    int dofs, slot;
+    pv_long8<D, G>(a, R, split, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, lds_f, mg,
+                   sg, v, dofs, slot);
+    if (slot == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        const uint32_t o = pbase + (uint32_t)(g * D + dofs) * 4;
+        coherent_store4(rpart, o, make_float4(v[g][0], v[g][1], v[g][2], v[g][3]));
+        coherent_store4(rpart, o + 16, make_float4(v[g][4], v[g][5], v[g][6], v[g][7]));
+      }
+    }
+  } else {
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
@@ -614,6 +769,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
     }
   };
   SplitStats<G> sst = load_split_stats<G>(a, R, kv, b, wave, lane, ws_stats);
+  asm volatile("" ::: "memory");  // the loads above stay ahead of the V rows in issue order
   u32x4 vcur[UB];
   bool okcur[UB];
   vload(0, vcur, okcur, false);
@@ -675,10 +831,6 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
       }
     }
   }
-  const size_t hd = (size_t)kv * G * D;  // offset of this KV head's group in [NH, D]
-  const uint32_t sstride = (uint32_t)(a.NH * D * 4);  // bytes per split partial
-  const __amdgpu_buffer_rsrc_t rpart = buffer_rsrc(ws_part, (uint32_t)(a.B * a.n_split_max) * sstride);
-  const uint32_t pbase = (uint32_t)(((size_t)b * a.n_split_max + split) * sstride + hd * 4);
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     float v[8];
@@ -690,6 +842,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
       coherent_store4(rpart, o + 16, make_float4(v[4], v[5], v[6], v[7]));
     }
   }
+  }  // NW == 4
 
   // two-level ordered reduction of the partials
   const int grp = split / kGroup;
@@ -698,23 +851,23 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnDims a, const uint16_t
   unsigned int* cnt = counters + ((size_t)b * a.KV + kv) * (kMaxGroups + 1);
   if (!arrive_last(cnt + 1 + grp, (unsigned)gsz, &flag)) return;
   float4 sum[E4];
-  ordered_sum<E4, G * D / 4>(rpart, (uint32_t)(((size_t)b * a.n_split_max + grp * kGroup) * sstride + hd * 4),
+  ordered_sum<E4, G * D / 4, NT>(rpart, (uint32_t)(((size_t)b * a.n_split_max + grp * kGroup) * sstride + hd * 4),
                              sstride, gsz, sum);
   uint16_t* out = ctx + (size_t)b * a.NH * D + hd;
   if (ngroups == 1) {
-    store_bf16x4<E4, G * D / 4>(out, sum);
+    store_bf16x4<E4, G * D / 4, NT>(out, sum);
     return;
   }
   const __amdgpu_buffer_rsrc_t rgrp = buffer_rsrc(ws_group, (uint32_t)(a.B * kMaxGroups) * sstride);
   const uint32_t gbase = (uint32_t)((size_t)b * kMaxGroups * sstride + hd * 4);
 #pragma unroll
   for (int r = 0; r < E4; ++r) {
-    const int e4 = threadIdx.x + 256 * r;
+    const int e4 = threadIdx.x + NT * r;
     if (e4 < G * D / 4) coherent_store4(rgrp, gbase + (uint32_t)grp * sstride + 16u * (uint32_t)e4, sum[r]);
   }
   if (!arrive_last(cnt, (unsigned)ngroups, &flag)) return;
-  ordered_sum<E4, G * D / 4>(rgrp, gbase, sstride, ngroups, sum);
-  store_bf16x4<E4, G * D / 4>(out, sum);
+  ordered_sum<E4, G * D / 4, NT>(rgrp, gbase, sstride, ngroups, sum);
+  store_bf16x4<E4, G * D / 4, NT>(out, sum);
 }
 
 // ------------------------------------------------------------------ append
@@ -766,17 +919,23 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
                         const uint16_t* v_raw, const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* cs,
                         const uint16_t* sn, uint16_t* kp, uint16_t* vp, const int32_t* pt, const int32_t* pos,
                         int append, const AttnWs& w, uint16_t* ctx) {
-  // every split holds at most kChunkMin positions when the longest range does
+  // every split holds at most kChunkMin positions when the longest range
+  // does: one K tile per wave, 4 waves.  Longer ranges (up to kChunkMax
+  // positions per split) run 8 waves per block with every K tile and V row
+  // of a split requested at once.
   const int span = (a.window > 0 && a.window < a.lmax) ? a.window : a.lmax;
-  if (span <= kChunkMin * a.n_split_max)
+  const dim3 pgrid(max(grid.x, (unsigned)(D / kSliceD)), grid.y, grid.z);  // short ranges use D / kSliceD blocks
+  if (span <= kChunkMin * a.n_split_max) {
     hipLaunchKernelGGL((attn_qk_kernel<D, G, true>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm,
                        cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
-  else
-    hipLaunchKernelGGL((attn_qk_kernel<D, G, false>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm,
-                       cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
-  const dim3 pgrid(max(grid.x, (unsigned)(D / kSliceD)), grid.y, grid.z);  // short ranges use D / kSliceD blocks
-  hipLaunchKernelGGL((attn_pv_kernel<D, G>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
-                     w.group, w.counters, ctx);
+    hipLaunchKernelGGL((attn_pv_kernel<D, G>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
+                       w.group, w.counters, ctx);
+  } else {
+    hipLaunchKernelGGL((attn_qk_kernel<D, G, false, 8>), grid, dim3(512), 0, st, a, q_raw, k_raw, v_raw, q_norm,
+                       k_norm, cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
+    hipLaunchKernelGGL((attn_pv_kernel<D, G, 8>), pgrid, dim3(512), 0, st, a, vp, pt, pos, w.scores, w.stats,
+                       w.part, w.group, w.counters, ctx);
+  }
 }
 
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }

@@ -150,6 +150,12 @@ def test_full_layer_shape_both_sides_of_the_short_range_limit():
     _run_case(5, 16, 2, 512, 2048, 64, [300, 510, 511, 512, 1500], 0, 0.0, True, 1e6, 0.25, 31)
 
 
+def test_one_query_head_per_kv_head_long_splits():
+    """G = 1 (as many query heads as KV heads) on the 8-wave path for ranges
+    of more than 64 positions per split: more threads than score slots."""
+    _run_case(2, 2, 2, 64, 2048, 64, [1800, 700], 0, 0.0, False, 1e4, 1.0, 33)
+
+
 def test_sliding_layer_shape_decode_positions():
     """26B sliding-layer shape (16 q / 8 KV heads, head_dim 256, window
     1024) at decode positions from the first token to a full window."""
