@@ -16,6 +16,9 @@ Workloads (--workload):
              N(0, 0.02), seed 3, 47 GiB in HBM; a 32,768-position cache; a
              54-token uniform-random prompt, then greedy batch-1 decode:
              warm-up steps + timed steps = 768 tokens.  value = decode tok/s.
+             config.filled_cache_decode: the same engine after every cache
+             page is filled with N(0,1), 64 timed steps at positions
+             32,703-32,766 (full layers attending ~32.7K positions).
   moe_block  the isolated MoE decode block: hidden 2816, router 2816x128,
              128 experts top-8 of width 704, bf16, seed 1, batch --batch
              (1, 4 or 8).  One HIP graph holds up to 64 consecutive steps, each
@@ -241,27 +244,32 @@ def run_moe_block(args) -> dict:
 
 def run_attention(args) -> dict:
     """Isolated decode attention, one query token at position 32,767 (seed 2),
-    RoPE and softcap 50, over a paged bf16 cache (64-position pages) filled
+    RoPE and softcap 50, over paged bf16 caches (64-position pages) filled
     with N(0, 1):
       (a) sliding layer: 16 q / 8 KV heads, head_dim 256, window 1024;
       (b) full layer: 16 q / 2 KV heads, head_dim 512, k==v, 32,768 cached
           positions (K and V rows stored separately, as the decode step does).
     Each case is the decode step's call (append of the new K/V row, then the
     split qk and pv kernels), --steps launches captured in HIP graphs and
-    timed with HIP events.  Algorithmic bytes per launch: the attended K and V
-    rows, 2 * positions * KV * D * 2 B.  value = (b)'s GB/s."""
+    timed with HIP events.  Consecutive launches rotate over `caches`
+    independent caches in one page pool (one page table each) holding at
+    least 512 MiB of attended rows together, twice the 256 MB Infinity
+    Cache, so every launch streams its K/V rows from HBM as a decode step
+    does (a step visits 29 other layers between two visits of one cache).
+    Algorithmic bytes per launch: the attended K and V rows,
+    2 * positions * KV * D * 2 B.  value = (b)'s GB/s."""
     import torch
     from gemma4_mi import model as gm
     from gemma4_mi import ops
     from gemma4_mi.weights import tensor_key
 
     dev, seed, lmax, page, pos = "cuda:0", 2, 32768, 64, 32767
+    rotate_bytes = 512 << 20
     cases = {
         "sliding": dict(NH=16, KV=8, D=256, window=1024, k_eq_v=False, theta=1e4, partial=1.0),
         "full": dict(NH=16, KV=2, D=512, window=0, k_eq_v=True, theta=1e6, partial=0.25),
     }
     steps = args.steps
-    G = _chunk(steps)
     out = {}
     for name, c in cases.items():
         NH, KV, D = c["NH"], c["KV"], c["D"]
@@ -275,29 +283,37 @@ def run_attention(args) -> dict:
         v_raw = None if c["k_eq_v"] else gen((1, KV, D), "v")
         q_norm, k_norm = gen((D,), "q_norm", 0.5), gen((D,), "k_norm", 0.5)
         cos, sin = gm.rope_table(D, c["theta"], c["partial"], lmax, dev)
-        pages = lmax // page
-        kp, vp = gen((pages, KV, page, D), "cache_k"), gen((pages, KV, page, D), "cache_v")
-        pt = torch.arange(pages, dtype=torch.int32, device=dev).view(1, pages)
-        p_t = torch.tensor([pos], dtype=torch.int32, device=dev)
         span = min(pos + 1, c["window"]) if c["window"] else pos + 1
+        nbytes = 2 * span * KV * D * 2
+        n_caches = -(-rotate_bytes // nbytes)
+        max_pages = lmax // page
+        lo_page = (pos + 1 - span) // page  # first attended page
+        per = max_pages - lo_page           # pages each cache holds (the attended ones)
+        kp, vp = gen((n_caches * per, KV, page, D), "cache_k"), gen((n_caches * per, KV, page, D), "cache_v")
+        pts = torch.full((n_caches, max_pages), -1, dtype=torch.int32, device=dev)
+        pts[:, lo_page:] = torch.arange(n_caches * per, dtype=torch.int32, device=dev).view(n_caches, per)
+        p_t = torch.tensor([pos], dtype=torch.int32, device=dev)
         ns = gm.decode_splits(KV, span)  # the decode step's split count for this layer
         ctx = torch.empty((1, NH, D), dtype=torch.bfloat16, device=dev)
         ws = torch.zeros(int(ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, NH, D, lmax, ns)),
                          dtype=torch.uint8, device=dev)
+        G = max(n_caches, (_chunk(steps) // n_caches) * n_caches)  # launches per graph, a multiple of n_caches
 
-        def call():
-            ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, pt, p_t, c["window"], 50.0,
-                                 1e-6, lmax, n_split_max=ns, append=True, ctx=ctx, ws=ws)
+        def call(i):
+            ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, pts[i % n_caches:][:1], p_t,
+                                 c["window"], 50.0, 1e-6, lmax, n_split_max=ns, append=True, ctx=ctx, ws=ws)
 
-        g = _capture(lambda: [call() for _ in range(G)])
-        _time_graph(g, max(1, args.warmup // G))
-        us = _time_graph(g, steps // G) / steps * 1e3
-        nbytes = 2 * span * KV * D * 2
+        g = _capture(lambda: [call(i) for i in range(G)])
+        _time_graph(g, max(1, -(-args.warmup // G)))
+        reps = max(1, steps // G)
+        us = _time_graph(g, reps) / (reps * G) * 1e3
         out[name] = {"heads": NH, "kv_heads": KV, "head_dim": D, "window": c["window"], "k_eq_v": c["k_eq_v"],
-                     "positions_attended": span, "splits": ns, "us_per_launch": us, "bytes_per_launch": nbytes,
-                     "gbs": nbytes / (us * 1e-6) / 1e9}
-        _log(f"attention {name}: {us:.2f} us, {out[name]['gbs']:.0f} GB/s")
-        del kp, vp
+                     "positions_attended": span, "splits": ns, "caches_rotated": n_caches,
+                     "rotated_bytes": n_caches * nbytes, "launches_timed": reps * G, "us_per_launch": us,
+                     "bytes_per_launch": nbytes, "gbs": nbytes / (us * 1e-6) / 1e9}
+        _log(f"attention {name}: {us:.2f} us, {out[name]['gbs']:.0f} GB/s over {n_caches} caches")
+        del kp, vp, g
+        torch.cuda.empty_cache()
     full = out["full"]
     return {
         "metric": "isolated decode attention GB/s (full layer, 32K positions)",
@@ -305,11 +321,12 @@ def run_attention(args) -> dict:
         "unit": "GB/s",
         "ms_per_step": full["us_per_launch"] * 1e-3,
         "dtype": "bf16",
-        "config": {"workload": "isolated decode attention at position 32767, softcap 50, seed 2", **out,
-                   "launch": "HIP graph"},
+        "config": {"workload": "isolated decode attention at position 32767, softcap 50, seed 2, "
+                               "caches rotated per launch (>= 512 MiB)", **out, "launch": "HIP graph"},
         "roofline": {
             "kernel": "attn_qk + attn_pv (full layer, 32K positions)", "bound": "hbm", "achieved": full["gbs"],
-            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": full["gbs"] / HBM_PEAK_GBS, "traffic": None,
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": full["gbs"] / HBM_PEAK_GBS,
+            "traffic": _measured_traffic("attn_qk_kernel+attn_pv_kernel<512>", "attention_32k_traffic.txt"),
             "bytes_per_launch": full["bytes_per_launch"], "avg_launch_us": full["us_per_launch"],
         },
     }
@@ -385,6 +402,48 @@ def _e2e_decode(args) -> dict:
     bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
     return {"cfg": cfg, "params": eng.params, "cache": eng.cache, "engine": eng, "ms": ms, "ttft": ttft,
             "first": first, "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt}
+
+
+def _filled_decode(res, steps: int = 64, warm: int = 4) -> dict:
+    """The same engine decoding at the end of a filled cache: every K/V page
+    of every layer is overwritten with N(0, 1) bf16 (a synthetic 32K-token
+    history), the position is set to max_len - steps - warm - 1, and `steps`
+    greedy steps are timed after `warm` untimed ones, so the full layers
+    attend ~32,700 positions and the sliding layers their whole window."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi import ops
+    from gemma4_mi.weights import decode_bytes, tensor_key
+
+    eng, cfg = res["engine"], res["cfg"]
+    max_len = eng.max_len
+    for i, (k, v) in enumerate(zip(eng.cache["k"], eng.cache["v"])):
+        ops.fill_normal_(k, tensor_key(5, f"bench.filled.k.{i}"), 1.0)
+        ops.fill_normal_(v, tensor_key(5, f"bench.filled.v.{i}"), 1.0)
+    eng._dirty[0] = max_len  # reset_cache clears the whole row
+    p_start = max_len - steps - warm - 1
+    dec = eng.decode_fn()
+    tok = torch.tensor([[res["tokens"][-1]]], dtype=torch.int32)
+    pos = p_start
+    for _ in range(warm):
+        tok, cache, pos = dec(eng.params, tok, eng.cache, pos, 3, 0.0, 1.0)
+    torch.cuda.synchronize()
+    p0 = int(pos)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        tok, cache, pos = dec(eng.params, tok, eng.cache, pos, 3, 0.0, 1.0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    p1 = int(pos)
+    bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
+    gbs = bytes_tok / (ms * 1e-3) / 1e9
+    _log(f"filled-cache decode at positions {p0}-{p1 - 1}: {ms:.3f} ms/token, {gbs:.0f} GB/s")
+    return {"positions_timed": [p0, p1], "steps": steps, "warmup": warm, "ms_per_token": ms, "tok_s": 1000.0 / ms,
+            "bytes_per_token": bytes_tok, "e2e_hbm_gbs": gbs, "e2e_frac_of_roofline": gbs / HBM_PEAK_GBS,
+            "cache_fill": "N(0,1) bf16 in every K/V page of every layer (seed 5)"}
 
 
 def _gateup_timing(cfg, params, n: int, steps: int) -> tuple[float, float]:
@@ -468,10 +527,11 @@ def _cpu_decode_baseline(res, budget_s: float, max_steps: int) -> dict:
     }
 
 
-def _measured_traffic(kernel: str) -> float | None:
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter
-    summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated), or None."""
-    path = os.path.join(ROOT, "profiles", "moe_gateup_26b_a4b_traffic.txt")
+def _measured_traffic(kernel: str, summary: str = "moe_gateup_26b_a4b_traffic.txt") -> float | None:
+    """HBM bytes per launch of `kernel` from a committed rocprofv3 counter
+    summary under profiles/ (FETCH_SIZE / WRITE_SIZE, copy-calibrated), or
+    None."""
+    path = os.path.join(ROOT, "profiles", summary)
     try:
         kv = dict(line.split(":", 1) for line in open(path) if ":" in line and not line.startswith("#"))
     except OSError:
@@ -518,6 +578,8 @@ def run_decode(args) -> dict:
     }
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_decode_baseline(res, args.cpu_seconds, 8)
+    # after the CPU baseline, which reads the prompt's cache rows
+    out["config"]["filled_cache_decode"] = _filled_decode(res)
     return out
 
 
