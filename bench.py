@@ -506,12 +506,13 @@ def _cpu_decode_baseline(res, budget_s: float, max_steps: int) -> dict:
     _log(f"cpu baseline: state copied to host in {time.perf_counter() - t0:.1f}s")
     tok, pos = res["first"], p
     done, t_start, el = 0, None, 0.0
+    oracle_tokens = []
     while done < max_steps:
-        ts = time.perf_counter()
         lg, ocache = twin.forward(cfg, cpu_params, np.array([[tok]]), np.array([pos]), ocache, pos,
                                   twin.decode_masks(cfg, max_len, pos), max_len, False, None, precise=False,
                                   inplace=True)
         tok, pos = twin.greedy(lg[0, 0]), pos + 1
+        oracle_tokens.append(int(tok))
         if t_start is None:  # first step is the warm-up
             t_start = time.perf_counter()
             continue
@@ -519,8 +520,15 @@ def _cpu_decode_baseline(res, budget_s: float, max_steps: int) -> dict:
         el = time.perf_counter() - t_start
         if el >= budget_s:
             break
+    # the GPU's greedy tokens after the same first token (res["tokens"][0] is that token)
+    gpu_tokens = res["tokens"][1:1 + len(oracle_tokens)]
+    same = 0
+    while same < min(len(gpu_tokens), len(oracle_tokens)) and gpu_tokens[same] == oracle_tokens[same]:
+        same += 1
     return {
         "value": done / el if el > 0 else None, "unit": "tok/s", "cores": threads, "kind": "port",
+        "tokens_compared": len(oracle_tokens), "tokens_identical_prefix": same,
+        "oracle_tokens": oracle_tokens, "gpu_tokens": gpu_tokens,
         "sample": f"{done} batch-1 decode steps (after 1 warm-up) of the 26B-A4B-shaped model from position {p + 1}, "
                   f"attending the whole {max_len}-position cache as the reference's decode does; torch-CPU oracle "
                   f"with bf16 GEMMs on {threads} threads of {_cpu_name()}",

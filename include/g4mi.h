@@ -304,20 +304,6 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes,
                    void* stream);
 
-/* The unfused dense products of the batched prefill through the ROCm library
- * GEMM (rocBLAS, bf16 in, f32 accumulate, atomics disallowed so the result
- * does not depend on scheduling): C[M,N] = A[M,K] . B[N,K]^T, row-major with
- * strides lda, ldb, ldc; bf16 output, or f32 with f32_out.  One rocBLAS
- * handle per device, created on first use; calls on one device from several
- * host threads must not overlap.  The XLA dots of model.py:197-221 at T > 1. */
-int g4mi_gemm_bf16_library(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
-                           int64_t K, int32_t f32_out, void* c, int64_t ldc, void* stream);
-
-/* act = bf16(bf16(gelu_tanh(g)) * u) over n bf16 elements (n % 8 == 0): the
- * gated MLP activation (model.py:220) on gate and up products already
- * rounded to bf16, after two g4mi_gemm_bf16_library calls. */
-int g4mi_gated_act(const uint16_t* g, const uint16_t* u, int64_t n, uint16_t* act, void* stream);
-
 /* Several products that share A in one skinny launch: C_s = A . B_s^T for
  * the nseg <= 4 segments, B_s [n[s], K] (row stride K), C_s [M, n[s]] bf16
  * (row stride n[s]); M <= 16, every n[s] a multiple of 16, K % 64 == 0.

@@ -70,8 +70,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> str:
         objs = list(ex.map(lambda s: _compile(s, hipcc, verbose), srcs))
     out = os.path.join(OUT_DIR, LIB_NAME)
     tmp = out + ".tmp"
-    # rocBLAS: the library GEMM for the unfused prefill products (csrc/blas.hip)
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, "-lrocblas"]
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

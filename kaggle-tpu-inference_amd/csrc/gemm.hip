@@ -3,10 +3,10 @@
 // C[m, n] = sum_k A[m, k] * B[n, k]: activations A [M, K] and weights B [N, K]
 // are both row-major with K contiguous, as every projection of the model is
 // stored (model.py:84-117), so both operands stream 16-byte rows.  bf16 in,
-// f32 accumulate.  One block computes a BM x BN tile with 4 waves (2 x 2);
-// a wave holds (BM/2) x (BN/2) of f32 accumulators as 16 x 16 MFMA tiles.
-// K advances 32 at a time through double-buffered LDS tiles: the next step's
-// global loads are in flight while the current step multiplies.
+// f32 accumulate.  More than 16 rows: a tile kernel (4 waves, 128 x 128 or
+// 64 x 128 tiles) fed by direct global->LDS loads through 2 or 3 LDS stages
+// (see gemm_kernel); up to 16 rows: a skinny kernel that splits K over the
+// waves of a block (gemm_skinny_kernel).
 //
 // MFMA operand layout (16x16x32 bf16): lane l holds A[l%16][8(l/16)..+7] and
 // B[l%16][8(l/16)..+7] (both rows of their K-contiguous tiles) and receives
@@ -19,13 +19,14 @@
 //  * split-K: blockIdx.z takes K slice z and writes f32 partials, summed in
 //    slice order by gemm_reduce_kernel (deterministic);
 //  * epilogues: bf16 store, f32 store, or the gated activation of a (gate, up)
-//    pair: the tile's first BN/2 B rows come from b, the last BN/2 from
-//    b + pair_offset at the same row index, and output column n0/2 + j gets
+//    pair: the tile's first BN/2 B rows are gate rows n0 + j of b, the last
+//    BN/2 the up rows at b + pair_offset, and output column n0 + j gets
 //    bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w_row)) (model.py:220,
 //    model.py:246-247 and 269-271 with the routing weight w_row of the row).
 #include <stdlib.h>
 
 #include <type_traits>
+#include <utility>
 
 #include "capi_util.h"
 #include "common.h"
@@ -65,201 +66,354 @@ struct GemmArgs {
   void* seg_c[kMaxSeg];
 };
 
-constexpr int kBK = 64;  // K per pipeline step
-constexpr int kPad = 8;  // LDS row padding (elements): rows of 144 bytes
+constexpr int kBK = 64;  // K per pipeline stage
 
-template <int BM, int BN, int EP>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmArgs g) {
-  constexpr int WM = BM / 2, WN = BN / 2;   // wave tile
-  constexpr int FM = WM / 16, FN = WN / 16; // MFMA fragments per wave
-  constexpr int LDT = kBK + kPad;
-  constexpr int CPR = kBK / 8;              // 16-byte chunks per tile row
-  constexpr int ACH = BM * CPR / 256;       // A chunks per thread per step
-  constexpr int BCH = BN * CPR / 256;
-  static_assert(ACH >= 1 && BCH >= 1, "tile too small for 256 threads");
-  // one LDS block: the double-buffered A and B tiles, reused by the gated
-  // epilogue's exchange
-  __shared__ __align__(16) uint16_t smem[2 * BM * LDT + 2 * BN * LDT];
-  // A tile of buffer `buf` at smem + buf*BM*LDT, B tile at smem + 2*BM*LDT + buf*BN*LDT
-  constexpr int SB0 = 2 * BM * LDT;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+// ---- tile GEMM (M > 16 rows)
+// A block computes a BM x BN tile (BM, BN in {64, 128, ...}) with 4 waves
+// (2 x 2), each a (BM/2) x (BN/2) patch of 16 x 16 MFMA accumulators.  K
+// advances kBK = 64 per stage through ST LDS stages (separate __shared__
+// arrays), filled by direct global->LDS loads (global_load_lds_dwordx4: 64
+// lanes x 16 bytes = 1 KB per instruction, written contiguously in lane
+// order).  Each tile row is 8 slots of 16 bytes; slot (r, p) holds k-chunk
+// p ^ sw(r), sw(r) = (r & 7) ^ ((r >> 3) & 1), so the fragment reads (16
+// rows x one chunk per ds_read_b128) hit distinct banks for 8 or 16 lanes
+// per cycle.  Stage step ks:
+//   phase A: the MFMAs of k-half 0 with the reads of k-half 1 in between;
+//   wait for those reads and for step ks+1's DMA, barrier (step ks+1's stage
+//   landed in every wave; stage ks read by every wave);
+//   phase B: the MFMAs of k-half 1 with the reads of step ks+1's k-half 0
+//   and the DMA of step ks+ST (into stage ks % ST) in between.
+// The DMA is inline asm (M0 = LDS address): the compiler sees no LDS
+// writer, so it does not wait for every outstanding DMA before its own LDS
+// reads (which it would for the builtin); the fragment reads are ordinary
+// LDS loads whose waits and registers the compiler tracks, and the DMA waits
+// are explicit (wait_vm_barrier).  sched_barrier pins the interleave; every
+// loop over fragments is a static_for and every lambda always_inline, so
+// the accumulators and fragments stay in registers.  ST = 2 stages let two
+// blocks share a CU (OCC = 2), so one block's barrier overlaps the other's
+// MFMAs; ST = 3 (one block per CU) covers more latency when there are fewer
+// tiles than CUs.
+
+// f(integral_constant<int, i>) for i = 0 .. N-1
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Waits until at most N of this wave's vector memory operations (the DMA of
+// later steps) are outstanding and its LDS reads are done, then the barrier.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Tile of block `bid` of a 1-D grid: consecutive ids go to the 8 XCDs in
+// turn (each XCD has its own L2), so XCD x takes the x-th contiguous run of
+// the tile order.  Plain tiling: groups of 8 row tiles, column tiles inner
+// (a group's A and B tiles are shared in the XCD's L2).  Grouped tiles
+// (tile list order, column tiles inner): a run covers whole tiles, so an A
+// tile is read once per XCD and the tiles of one group are neighbours.
+// Returns false for ids past the live tile count.
+__device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles_col, int& tx, int& ty, bool grouped) {
+  const int nb = mtiles * ntiles_col;
+  const int per = (nb + 7) / 8;
+  const int id = (bid % 8) * per + bid / 8;
+  if (id >= nb) return false;
+  if (grouped) {
+    tx = id / ntiles_col;
+    ty = id % ntiles_col;
+  } else {
+    constexpr int G = 8;
+    const int grp = id / (G * ntiles_col), fx = grp * G, gs = min(mtiles - fx, G);
+    tx = fx + (id % (G * ntiles_col)) % gs;
+    ty = (id % (G * ntiles_col)) / gs;
+  }
+  return true;
+}
+
+template <int BM, int BN, int ST, int OCC, int EP>
+__global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
+  constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
+  constexpr int FM = WM / 16, FN = WN / 16;  // MFMA fragments per wave
+  constexpr int AI = BM / 32, BI = BN / 32;  // DMA instructions per wave per stage
+  constexpr int NL = AI + BI;
+  constexpr int SB = (BM + BN) * 128;        // stage bytes
+  constexpr int NF = FM + FN, NM = FM * FN;
+  static_assert(ST == 2 || ST == 3, "2 or 3 stages");
+  static_assert(AI >= 1 && BI >= 1, "tile too small for 256 threads");
+  __shared__ __align__(1024) uint8_t st0[SB];
+  __shared__ __align__(1024) uint8_t st1[SB];
+  __shared__ __align__(1024) uint8_t st2[ST == 3 ? SB : 16];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
+  constexpr int NCOL = (EP == kEpGated) ? BN / 2 : BN;  // output columns per tile
+  const int ncol_tiles = (g.N + NCOL - 1) / NCOL;
 
   // ---- this block's tile
-  int group = 0, m0, m1;
+  int group = 0, m0, m1, tx, ty;
   if (g.tiles != nullptr) {
-    if ((int)blockIdx.x >= g.ntiles[0]) return;
-    const GemmTile t = g.tiles[blockIdx.x];
+    if (!tile_of(blockIdx.x, g.ntiles[0], ncol_tiles, tx, ty, true)) return;
+    const GemmTile t = g.tiles[tx];
     group = t.group;
     m0 = t.m0;
     m1 = t.m1;
   } else {
-    m0 = blockIdx.x * BM;
+    if (!tile_of(blockIdx.x, (g.M + BM - 1) / BM, ncol_tiles, tx, ty, false)) return;
+    m0 = tx * BM;
     m1 = min(g.M, m0 + BM);
   }
-  const int n0 = blockIdx.y * (EP == kEpGated ? BN / 2 : BN);  // first output column
-  const uint16_t* bbase = g.b + (size_t)group * g.b_group_stride;
+  const int n0 = ty * NCOL;  // first output column
+  const char* abase = (const char*)g.a;
+  const char* bbase = (const char*)(g.b + (size_t)group * g.b_group_stride);
   const int kslices = g.k_slices;
   const int ksteps_all = g.K / kBK;
   const int ks0 = (ksteps_all * (int)blockIdx.z) / kslices;
   const int ks1 = (ksteps_all * ((int)blockIdx.z + 1)) / kslices;
+  const int nks = ks1 - ks0;
 
-  // ---- global source rows of the chunks this thread copies (fixed over K)
-  const u32x4* asrc[ACH];
-  const u32x4* bsrc[BCH];
-  int adst[ACH], bdst[BCH];
+  // ---- DMA sources: instruction j of this wave fills tile rows
+  // (wave*AI + j)*8 + lane/8, slot lane%8 (chunk (lane%8) ^ sw(row)).  Rows
+  // past the tile repeat its last row (not stored).
+  const char* asrc[AI];
+  const char* bsrc[BI];
 #pragma unroll
-  for (int q = 0; q < ACH; ++q) {
-    const int c = tid + 256 * q;  // chunk: row c/CPR, 8 elements at (c%CPR)*8
-    const int r = c / CPR, kc = (c % CPR) * 8;
+  for (int j = 0; j < AI; ++j) {
+    const int r = (wave * AI + j) * 8 + (lane >> 3);
+    const int cc = (lane & 7) ^ ((r & 7) ^ ((r >> 3) & 1));
     const int m = min(m0 + r, max(m1 - 1, m0));
     const int src = (g.a_rows != nullptr) ? g.a_rows[m] : m;
-    asrc[q] = (const u32x4*)(g.a + (size_t)src * g.lda + kc);
-    adst[q] = r * LDT + kc;
+    asrc[j] = abase + ((int64_t)src * g.lda + cc * 8) * 2;
   }
 #pragma unroll
-  for (int q = 0; q < BCH; ++q) {
-    const int c = tid + 256 * q;
-    const int r = c / CPR, kc = (c % CPR) * 8;
-    const uint16_t* row;
+  for (int j = 0; j < BI; ++j) {
+    const int r = (wave * BI + j) * 8 + (lane >> 3);
+    const int cc = (lane & 7) ^ ((r & 7) ^ ((r >> 3) & 1));
+    int64_t row;
     if constexpr (EP == kEpGated) {
       const int half = r >= BN / 2;
-      const int n = min(n0 + (r - half * (BN / 2)), g.N - 1);
-      row = bbase + (half ? g.pair_offset : 0) + (size_t)n * g.ldb;
+      row = (half ? g.pair_offset : 0) + (int64_t)min(n0 + (r - half * (BN / 2)), g.N - 1) * g.ldb;
     } else {
-      const int n = min(n0 + r, g.N - 1);
-      row = bbase + (size_t)n * g.ldb;
+      row = (int64_t)min(n0 + r, g.N - 1) * g.ldb;
     }
-    bsrc[q] = (const u32x4*)(row + kc);
-    bdst[q] = r * LDT + kc;
+    bsrc[j] = bbase + (row + cc * 8) * 2;
+  }
+  // fragment reads: lane l takes row (l%16) of a 16-row block, chunk
+  // 4*half + l/16 of the stage's 8 (byte offsets within a stage)
+  const int swl = (lane & 7) ^ ((lane >> 3) & 1);
+  uint32_t fa[2], fb[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int cch = (4 * kk + (lane >> 4)) ^ swl;
+    fa[kk] = (uint32_t)(((wm * WM + (lane & 15)) * 8 + cch) * 16);
+    fb[kk] = (uint32_t)(BM * 128 + ((wn * WN + (lane & 15)) * 8 + cch) * 16);
   }
 
   f32x4 acc[FM][FN];
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  static_for<NM>([&](auto ic) __attribute__((always_inline)) { acc[decltype(ic)::value / FN][decltype(ic)::value % FN] = f32x4{0.0f, 0.0f, 0.0f, 0.0f}; });
 
-  // Pipeline: tile j's global loads go to register stage j%2 two steps
-  // before it is multiplied; at step k the block multiplies LDS buffer k%2,
-  // stores register stage (k+1)%2 (tile k+1) into the other buffer and has
-  // tile k+2's loads in flight, so two steps of MFMA work cover each load.
-  u32x4 ra[2][ACH], rb[2][BCH];
-  auto gload = [&](int ks, u32x4* a_, u32x4* b_) {
-#pragma unroll
-    for (int q = 0; q < ACH; ++q) a_[q] = ld16(asrc[q] + ks * CPR);
-#pragma unroll
-    for (int q = 0; q < BCH; ++q) b_[q] = ld_stream(bsrc[q] + ks * CPR);
+  auto sbase = [&](auto sc) __attribute__((always_inline)) -> uint8_t* {
+    constexpr int S = decltype(sc)::value;
+    if constexpr (S == 0) return st0;
+    else if constexpr (S == 1) return st1;
+    else return st2;
   };
-  auto lstore = [&](int buf, const u32x4* a_, const u32x4* b_) {
-#pragma unroll
-    for (int q = 0; q < ACH; ++q) *(u32x4*)(smem + buf * BM * LDT + adst[q]) = a_[q];
-#pragma unroll
-    for (int q = 0; q < BCH; ++q) *(u32x4*)(smem + SB0 + buf * BN * LDT + bdst[q]) = b_[q];
-  };
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
-  auto compute = [&](int buf) {
-#pragma unroll
-    for (int kk = 0; kk < kBK / 32; ++kk) {
-      u32x4 af[FM], bf[FN];
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *(const u32x4*)(smem + buf * BM * LDT + (wm * WM + i * 16 + fr) * LDT + 32 * kk + fk);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        bf[j] = *(const u32x4*)(smem + SB0 + buf * BN * LDT + (wn * WN + j * 16 + fr) * LDT + 32 * kk + fk);
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
-                                                              __builtin_bit_cast(bf16x8, bf[j]), acc[i][j], 0, 0,
-                                                              0);
+  // DMA instruction q (< NL) of step ks into stage sc: 64 lanes x 16 bytes
+  // from their global addresses to LDS[l, l + 1024) in lane order (M0 = l).
+  // Inline asm: it has no register result, and the compiler, which does not
+  // see an LDS writer, does not wait for it before its own LDS reads; the
+  // waits are the explicit vmcnt waits below.
+  auto issue1 = [&](int ks, auto sc, auto qc) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    uint8_t* s = sbase(sc);
+    const uint32_t kb = (uint32_t)ks * kBK * 2u;
+    const char* gp;
+    uint32_t l;
+    if constexpr (q < AI) {
+      gp = asrc[q] + kb;
+      l = (uint32_t)(uintptr_t)(s + (wave * AI + q) * 1024);
+    } else {
+      gp = bsrc[q - AI] + kb;
+      l = (uint32_t)(uintptr_t)(s + BM * 128 + (wave * BI + q - AI) * 1024);
     }
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :
+                 : "v"(gp), "s"(__builtin_amdgcn_readfirstlane(l))
+                 : "memory", "m0");
   };
-  // one pipeline step on buffer BUF (register stages are compile-time)
-  auto step = [&](int ks, auto bufc) {
-    constexpr int BUF = decltype(bufc)::value;
-    if (ks + 2 < ks1) gload(ks + 2, ra[BUF], rb[BUF]);
-    compute(BUF);
-    if (ks + 1 < ks1) lstore(BUF ^ 1, ra[BUF ^ 1], rb[BUF ^ 1]);
-    __syncthreads();
+  struct Frag {
+    u32x4 a[FM], b[FN];
   };
-  if (ks0 < ks1) {
-    gload(ks0, ra[0], rb[0]);
-    if (ks0 + 1 < ks1) gload(ks0 + 1, ra[1], rb[1]);
-    lstore(0, ra[0], rb[0]);
-    __syncthreads();
-    int ks = ks0;
-    for (; ks + 1 < ks1; ks += 2) {
-      step(ks, std::integral_constant<int, 0>{});
-      step(ks + 1, std::integral_constant<int, 1>{});
+  // fragment read q (< NF) of k-half kk of stage sc (an ordinary LDS load:
+  // the compiler waits for it before the MFMA that uses it)
+  auto read1 = [&](Frag& f, auto sc, int kk, auto qc) __attribute__((always_inline)) {
+    constexpr int q = decltype(qc)::value;
+    const uint8_t* s = sbase(sc);
+    if constexpr (q < FM) f.a[q] = *(const u32x4*)(s + fa[kk] + q * 16 * 128);
+    else f.b[q - FM] = *(const u32x4*)(s + fb[kk] + (q - FM) * 16 * 128);
+  };
+  // 16-row fragments of this wave that hold rows of the tile (a grouped
+  // tile may be short): the MFMAs of the others are skipped (wave-uniform)
+  const int vfrag = min(FM, max(0, (m1 - (m0 + wm * WM) + 15) / 16));
+  auto mfma1 = [&](const Frag& f, auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value / FN, j = decltype(ic)::value % FN;
+    if (i == 0 || i < vfrag)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, f.a[i]),
+                                                          __builtin_bit_cast(bf16x8, f.b[j]), acc[i][j], 0, 0, 0);
+  };
+  using I = std::integral_constant<int, 0>;
+  Frag f0, f1;
+  // step t (relative to ks0) on stage S = t % ST; f0 holds its k-half 0
+  // fragments (requested).  STD: not one of the last steps (every check true).
+  auto step = [&](int t, auto sc, auto steady) __attribute__((always_inline)) {
+    constexpr int S = decltype(sc)::value;
+    constexpr bool STD = decltype(steady)::value;
+    using SN = std::integral_constant<int, (S + 1) % ST>;
+    static_for<NM>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int idx = decltype(ic)::value;
+      mfma1(f0, ic);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (idx % 2 == 0 && idx / 2 < NF) read1(f1, sc, 1, std::integral_constant<int, idx / 2>{});
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<NF>([&](auto qc) __attribute__((always_inline)) {  // reads beyond the interleave slots
+      if constexpr (decltype(qc)::value >= NM / 2) read1(f1, sc, 1, qc);
+    });
+    // this wave's LDS reads done; DMA still allowed in flight: steps t+2 ..
+    // t+ST-1 (those that exist)
+    if constexpr (STD) {
+      wait_vm_barrier<(ST - 2) * NL>();
+    } else {
+      if (ST == 3 && t + 2 < nks) wait_vm_barrier<NL>();
+      else wait_vm_barrier<0>();
     }
-    if (ks < ks1) step(ks, std::integral_constant<int, 0>{});
+    const bool nxt = STD || t + 1 < nks, dma = STD || t + ST < nks;
+    static_for<NM>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int idx = decltype(ic)::value;
+      mfma1(f1, ic);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (idx % 2 == 0 && idx / 2 < NF) {
+        if (nxt) read1(f0, SN{}, 0, std::integral_constant<int, idx / 2>{});
+      }
+      if constexpr (idx % 2 == 1 && idx / 2 < NL) {
+        if (dma) issue1(ks0 + t + ST, sc, std::integral_constant<int, idx / 2>{});
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    });
+    static_for<NF>([&](auto qc) __attribute__((always_inline)) {
+      if constexpr (decltype(qc)::value >= NM / 2) {
+        if (nxt) read1(f0, SN{}, 0, qc);
+      }
+    });
+    static_for<NL>([&](auto qc) __attribute__((always_inline)) {
+      if constexpr (decltype(qc)::value >= NM / 2) {
+        if (dma) issue1(ks0 + t + ST, sc, qc);
+      }
+    });
+  };
+  using YES = std::integral_constant<bool, true>;
+  using NO = std::integral_constant<bool, false>;
+  if (nks > 0) {
+    // prologue: the DMA of steps 0 .. ST-1, then wait for step 0's
+    static_for<ST>([&](auto sc) __attribute__((always_inline)) {
+      if (decltype(sc)::value < nks) static_for<NL>([&](auto qc) __attribute__((always_inline)) { issue1(ks0 + decltype(sc)::value, sc, qc); });
+    });
+    const int later = min(ST, nks) - 1;  // steps issued after step 0
+    if (ST == 3 && later == 2) wait_vm_barrier<2 * NL>();
+    else if (later >= 1) wait_vm_barrier<NL>();
+    else wait_vm_barrier<0>();
+    static_for<NF>([&](auto qc) __attribute__((always_inline)) { read1(f0, I{}, 0, qc); });
+    int t = 0;
+    for (; t + 2 * ST - 1 < nks; t += ST)  // steady state: every check of the step holds
+      static_for<ST>([&](auto sc) __attribute__((always_inline)) { step(t + decltype(sc)::value, sc, YES{}); });
+    // fewer than 2*ST - 1 steps remain, on stages 0, 1, ..
+    static_for<2 * ST - 1>([&](auto u) __attribute__((always_inline)) {
+      constexpr int U = decltype(u)::value;
+      if (t + U < nks) step(t + U, std::integral_constant<int, U % ST>{}, NO{});
+    });
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 
   // ---- epilogue.  Fragment (i, j), register q: row wm*WM + 16i + 4(l/16) + q,
   // column wn*WN + 16j + (l%16) of the tile.
   const int er = 4 * (lane >> 4), ec = lane & 15;
   if (kslices > 1) {
     float* p = g.partial + (size_t)blockIdx.z * g.M * g.N;
-#pragma unroll
-    for (int i = 0; i < FM; ++i)
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = m0 + wm * WM + 16 * i + er + q, n = n0 + wn * WN + 16 * j + ec;
-          if (m < m1 && n < g.N) p[(size_t)m * g.N + n] = acc[i][j][q];
-        }
-    return;
-  }
-  if constexpr (EP == kEpGated) {
-    // up (wn = 1) to LDS, then the gate waves combine
-    __syncthreads();
-    float* su = (float*)smem;  // BM x WN f32
-    static_assert((size_t)BM * (BN / 2) * 4 <= sizeof(smem), "exchange buffer too small");
-    if (wn == 1) {
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) su[(wm * WM + 16 * i + er + q) * WN + 16 * j + ec] = acc[i][j][q];
-    }
-    __syncthreads();
-    if (wn == 0) {
-      uint16_t* c = (uint16_t*)g.c;
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const int r = wm * WM + 16 * i + er + q, col = 16 * j + ec;
-            const int m = m0 + r, n = n0 + col;
-            if (m < m1 && n < g.N) {
-              const float gt = rbf(acc[i][j][q]), up = rbf(su[r * WN + col]);
-              float a = rbf(rbf(gelu_tanh(gt)) * up);
-              if (g.row_scale != nullptr) a = rbf(a * rbf(g.row_scale[m]));
-              c[(size_t)m * g.ldc + n] = f2bf(a);
-            }
-          }
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < FM; ++i)
-#pragma unroll
-    for (int j = 0; j < FN; ++j)
+    static_for<NM>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value / FN, j = decltype(ic)::value % FN;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = m0 + wm * WM + 16 * i + er + q, n = n0 + wn * WN + 16 * j + ec;
-        if (m < m1 && n < g.N) {
-          if constexpr (EP == kEpF32) ((float*)g.c)[(size_t)m * g.ldc + n] = acc[i][j][q];
-          else ((uint16_t*)g.c)[(size_t)m * g.ldc + n] = f2bf(acc[i][j][q]);
-        }
+        if (m < m1 && n < g.N) p[(size_t)m * g.N + n] = acc[i][j][q];
       }
+    });
+    return;
+  }
+  if constexpr (EP == kEpGated) {
+    // gate (wn = 0) and up (wn = 1) products rounded to bf16, and the rows'
+    // bf16 scales, to LDS (every wave is past its last stage read: the
+    // barrier orders the exchange after them); then all 256 threads take 8
+    // consecutive output columns at a time and store them as 16 bytes
+    constexpr int HC = BN / 2;                       // output columns of the tile
+    uint16_t* sgate = (uint16_t*)st0;                // [BM][HC] bf16
+    uint16_t* sup = (uint16_t*)st1;                  // [BM][HC] bf16
+    float* sw = (float*)(st0 + BM * HC * 2);         // [BM] row scales
+    static_assert(BM * HC * 2 + BM * 4 <= SB, "exchange buffer too small");
+    __syncthreads();
+    static_for<NM>([&](auto ic) __attribute__((always_inline)) {
+      constexpr int i = decltype(ic)::value / FN, j = decltype(ic)::value % FN;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        (wn ? sup : sgate)[(wm * WM + 16 * i + er + q) * HC + 16 * j + ec] = f2bf(acc[i][j][q]);
+    });
+    for (int r = tid; r < BM; r += 256) {
+      const int m = min(m0 + r, m1 - 1);
+      sw[r] = (g.row_scale != nullptr) ? rbf(g.row_scale[m]) : 1.0f;
+    }
+    __syncthreads();
+    uint16_t* c = (uint16_t*)g.c;
+    const bool vec = (((uintptr_t)c | (uintptr_t)(g.ldc * 2)) & 15u) == 0;
+    for (int e = tid; e < BM * (HC / 8); e += 256) {
+      const int r = e / (HC / 8), c8 = (e % (HC / 8)) * 8;
+      const int m = m0 + r, n = n0 + c8;
+      if (m >= m1 || n >= g.N) continue;
+      const u32x4 gv = *(const u32x4*)(sgate + r * HC + c8), uv = *(const u32x4*)(sup + r * HC + c8);
+      const float wr = sw[r];
+      uint32_t o[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        float a0 = rbf(rbf(gelu_tanh(bf_lo(gv[h]))) * bf_lo(uv[h]));
+        float a1 = rbf(rbf(gelu_tanh(bf_hi(gv[h]))) * bf_hi(uv[h]));
+        if (g.row_scale != nullptr) {
+          a0 = rbf(a0 * wr);
+          a1 = rbf(a1 * wr);
+        }
+        o[h] = pack2(a0, a1);
+      }
+      uint16_t* dst = c + (size_t)m * g.ldc + n;
+      if (vec && n + 8 <= g.N) {
+        *(u32x4*)dst = u32x4{o[0], o[1], o[2], o[3]};
+      } else {
+        for (int h = 0; h < 8 && n + h < g.N; ++h) dst[h] = (uint16_t)(o[h / 2] >> (16 * (h & 1)));
+      }
+    }
+    return;
+  }
+  static_for<NM>([&](auto ic) __attribute__((always_inline)) {
+    constexpr int i = decltype(ic)::value / FN, j = decltype(ic)::value % FN;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = m0 + wm * WM + 16 * i + er + q, n = n0 + wn * WN + 16 * j + ec;
+      if (m < m1 && n < g.N) {
+        if constexpr (EP == kEpF32) ((float*)g.c)[(size_t)m * g.ldc + n] = acc[i][j][q];
+        else ((uint16_t*)g.c)[(size_t)m * g.ldc + n] = f2bf(acc[i][j][q]);
+      }
+    }
+  });
 }
 
 // ---- skinny GEMM (M <= 16 rows: batched decode, short prompts)
@@ -385,11 +539,14 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
   else ((uint16_t*)c)[m * ldc + n] = f2bf(s);
 }
 
-template <int BM, int BN, int EP>
-static void launch(const GemmArgs& g, int mtiles, hipStream_t st) {
-  const int ncols = (EP == kEpGated) ? BN / 2 : BN;
-  dim3 grid((unsigned)mtiles, (unsigned)((g.N + ncols - 1) / ncols), (unsigned)g.k_slices);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, EP>), grid, dim3(256), 0, st, g);
+// 1-D grid of tiles x column tiles (rounded up to a multiple of the 8 XCDs;
+// ids past the live count exit), blockIdx.z = K slice.
+template <int BM, int BN, int ST, int OCC, int EP>
+static void launch(const GemmArgs& g, int64_t mtiles, hipStream_t st) {
+  const int ncol = (EP == kEpGated) ? BN / 2 : BN;
+  const int64_t nb = mtiles * ((g.N + ncol - 1) / ncol);
+  dim3 grid((unsigned)(((nb + 7) / 8) * 8), 1, (unsigned)g.k_slices);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, ST, OCC, EP>), grid, dim3(256), 0, st, g);
 }
 
 }  // namespace g4mi
@@ -446,19 +603,28 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
     }
     return check_launch("gemm_bf16 (skinny)");
   }
-  // grouped tiles are up to 128 rows (128-row kernels); small plain M takes 64-row tiles
+  // grouped tiles are up to 128 rows (128-row kernels); small plain M takes
+  // 64-row tiles.  Two blocks per CU (2 stages) for grouped tiles and when
+  // there are more tiles than CUs, else one block per CU with 3 stages.
   const bool small = tiles == nullptr && M <= 64;
   const int64_t mtiles = tiles ? max_tiles : (M + (small ? 63 : 127)) / (small ? 64 : 128);
-  G4MI_REQUIRE(mtiles <= 2147483647, G4MI_EINVAL, "gemm: too many tiles");
+  const int64_t ncol = epilogue == kEpGated ? 64 : 128;
+  const int64_t nblocks = mtiles * ((N + ncol - 1) / ncol) * k_slices;
+  G4MI_REQUIRE(mtiles * ((N + ncol - 1) / ncol) <= 2147483647 - 8, G4MI_EINVAL, "gemm: too many tiles");
+  G4MI_REQUIRE(tiles == nullptr || max_tiles <= 2147483647, G4MI_EINVAL, "gemm: too many tiles");
+  const int ep = (k_slices > 1) ? (int)kEpF32 : epilogue;
+#define G4MI_GEMM(BM, BN, S, O)                                                 \
+  if (ep == kEpGated) launch<BM, BN, S, O, kEpGated>(g, mtiles, st);            \
+  else if (ep == kEpF32) launch<BM, BN, S, O, kEpF32>(g, mtiles, st);           \
+  else launch<BM, BN, S, O, kEpBf16>(g, mtiles, st);
   if (small) {
-    if (epilogue == kEpGated) launch<64, 128, kEpGated>(g, (int)mtiles, st);
-    else if (k_slices > 1 || epilogue == kEpF32) launch<64, 64, kEpF32>(g, (int)mtiles, st);
-    else launch<64, 64, kEpBf16>(g, (int)mtiles, st);
+    G4MI_GEMM(64, 128, 3, 1)
+  } else if (tiles != nullptr || nblocks > 256) {
+    G4MI_GEMM(128, 128, 2, 2)
   } else {
-    if (epilogue == kEpGated) launch<128, 128, kEpGated>(g, (int)mtiles, st);
-    else if (k_slices > 1 || epilogue == kEpF32) launch<128, 128, kEpF32>(g, (int)mtiles, st);
-    else launch<128, 128, kEpBf16>(g, (int)mtiles, st);
+    G4MI_GEMM(128, 128, 3, 1)
   }
+#undef G4MI_GEMM
   if (k_slices > 1) {
     const int64_t mn = M * N;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3((unsigned)((mn + 255) / 256)), dim3(256), 0, st, (const float*)ws,

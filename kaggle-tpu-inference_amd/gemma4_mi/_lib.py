@@ -51,8 +51,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          _i32, _i64, _i64, _p, _p, _i64, _p],
     ),
     "g4mi_gemm_bf16_segments": (_int, [_p, _i64, _i64, _i64, _i32, _p, _p, _p, _p]),
-    "g4mi_gemm_bf16_library": (_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _i32, _p, _i64, _p]),
-    "g4mi_gated_act": (_int, [_p, _p, _i64, _p, _p]),
     "g4mi_moe_decode_grouped": (_int, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p, _i64, _p]),
     "g4mi_layer_in": (
         _int,

@@ -160,7 +160,7 @@ class BatchDecodeRunner:
                                lp.get("pre_feedforward_layernorm_2"), eps, self.x1, self.xm, self.xe)
             gate, up = lp["mlp.gate_proj"], lp["mlp.up_proj"]
             ops.prefill_gemm(self.xm, gate, self.act, epilogue=ops.EP_GATED,
-                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0], up=up)
+                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0])
             ops.prefill_gemm(self.act, lp["mlp.down_proj"], self.mlp_out)
             if moe:
                 ops.moe_router_topk(self.xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],

@@ -536,7 +536,7 @@ class PrefillRunner:
             gate, up = lp["mlp.gate_proj"], lp["mlp.up_proj"]
             act = self.act[:n]
             ops.prefill_gemm(xm, gate, act, epilogue=ops.EP_GATED,
-                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0], up=up)
+                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0])
             ops.prefill_gemm(act, lp["mlp.down_proj"], mlp_out)
             if moe:
                 tw, ti = self.top_w[:n], self.top_i[:n]

@@ -574,52 +574,18 @@ def rows_tail(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, n
               stream_handle(x1.device))
 
 
-def gemm_library(a, b, out=None, f32_out=False):
-    """C = A . B^T through the ROCm library GEMM (rocBLAS): a [M, K], b [N, K]
-    bf16 (row strides from the tensors), out [M, N] bf16 or f32."""
-    M, K = a.shape
-    N = b.shape[0]
-    for t, name in ((a, "a"), (b, "b")):
-        if t.device.type != "cuda" or t.dtype != BF16 or t.stride(1) != 1:
-            raise ValueError(f"gemm_library needs {name} as bf16 row-major device memory")
-    if b.shape[1] != K:
-        raise ValueError("gemm_library: a and b disagree on K")
-    if out is None:
-        out = torch.empty((M, N), dtype=torch.float32 if f32_out else BF16, device=a.device)
-    if out.stride(1) != 1 or tuple(out.shape) != (M, N):
-        raise ValueError("gemm_library needs a row-major out [M, N]")
-    _lib.call("g4mi_gemm_bf16_library", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, 1 if f32_out else 0,
-              _ptr(out), out.stride(0), stream_handle(a.device))
-    return out
-
-
-def gated_act(g, u, act):
-    """act = bf16(bf16(gelu_tanh(g)) * u) elementwise (model.py:220)."""
-    _need(g, BF16, "g")
-    _need(u, BF16, "u", tuple(g.shape))
-    _need(act, BF16, "act", tuple(g.shape))
-    _lib.call("g4mi_gated_act", _ptr(g), _ptr(u), g.numel(), _ptr(act), stream_handle(g.device))
-    return act
-
-
-def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256, up=None):
+def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256):
     """gemm() for the batched prefill: activations a [M, K] times the weight
-    rows w [N, K].  M <= 16 runs the skinny MFMA kernel; larger M the library
-    GEMM, the gated epilogue (gate rows w, up rows `up`, also reachable at w +
-    pair_offset for the MFMA kernels) as two library products and gated_act."""
+    rows w [N, K] on the MFMA kernels (M <= 16: the skinny kernel; more rows:
+    the tile kernel, split over K when there are fewer tiles than `blocks`);
+    the gated epilogue takes the gate rows w and the up rows at w +
+    pair_offset elements."""
     M, K = a.shape
     N = n if n is not None else w.shape[0]
-    if M > 16 and epilogue in (EP_BF16, EP_F32) and out.stride(1) == 1 and w.is_contiguous():
-        return gemm_library(a, w.reshape(-1, K)[:N], out=out, f32_out=epilogue == EP_F32)
-    if M > 16 and epilogue == EP_GATED and up is not None and N % 8 == 0 and out.is_contiguous() and w.is_contiguous():
-        tmp = WORKSPACE.get(a.device, "gated_gu", 2 * M * N * 2).view(BF16)[: 2 * M * N].view(2, M, N)
-        gemm_library(a, w.reshape(-1, K)[:N], out=tmp[0])
-        gemm_library(a, up.reshape(-1, K)[:N], out=tmp[1])
-        return gated_act(tmp[0], tmp[1], out)
     k_slices = 1
     if epilogue != EP_GATED and M > 16:  # M <= 16 runs the skinny kernel (K split inside the block)
         tm = 64 if M <= 64 else 128
-        tiles = ((M + tm - 1) // tm) * ((N + tm - 1) // tm)
+        tiles = ((M + tm - 1) // tm) * ((N + 127) // 128)
         if tiles < blocks:
             k_slices = max(1, min((blocks + tiles - 1) // tiles, K // 128, 16))
     return gemm(a, w, out=out, epilogue=epilogue, pair_offset=pair_offset, n=N, k_slices=k_slices)

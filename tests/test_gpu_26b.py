@@ -29,8 +29,9 @@ Checks:
     LOGIT_TOL, per-layer expert sets;
   * PrefillRunner at 256 tokens: last-row logits and both layers' K/V
     against the oracle's dense-MoE prefill;
-  * prefill rows do not depend on the prompt length: the first 256 rows of
-    a 2,048-token prefill equal a 256-token prefill's (cache and logits);
+  * prefill rows do not depend on later tokens: two 2,048-token prompts that
+    share their first 1,024 tokens give the same first 1,024 rows (cache and
+    the head on row 1,023), bit for bit;
   * BatchEngine with 8 sequences of different lengths against the batch-1
     runner fed the same tokens.
 """
@@ -303,29 +304,36 @@ def test_batched_prefill_256_matches_oracle(m26):
                 assert same >= 0.99, (i, kind, same)
 
 
-def test_prefill_rows_do_not_depend_on_prompt_length(m26):
-    """Row t of the causal prefill depends only on tokens <= t: the first 256
-    rows of a 2,048-token prefill (cache of both layers, and the head applied
-    to row 255) equal those of a 256-token prefill of the same tokens, bit for
-    bit."""
+def test_prefill_prefix_rows_do_not_depend_on_later_tokens(m26):
+    """Row t of the causal prefill depends only on tokens <= t: two
+    2,048-token prompts that agree on their first 1,024 tokens give the same
+    first 1,024 cache rows in both layers, and the same head on row 1,023,
+    bit for bit (the GEMMs, the expert grouping -- whose tiles hold other
+    tokens in the two runs -- and the attention keep rows apart)."""
     cfg, params, *_ = m26
-    toks = torch.tensor(np.random.default_rng(5).integers(0, cfg.vocab_size, size=2048), dtype=torch.int32,
-                        device=DEV)
+    rng = np.random.default_rng(5)
+    base = rng.integers(0, cfg.vocab_size, size=2048)
+    other = base.copy()
+    other[1024:] = rng.integers(0, cfg.vocab_size, size=1024)
     out = []
-    for n in (2048, 256):
+    for toks_np in (base, other):
+        toks = torch.tensor(toks_np, dtype=torch.int32, device=DEV)
         cache = gm.init_cache(cfg, None, 1, 2048, device=DEV)
         r = gm.DecodeRunner(cfg, params, cache, device=DEV)
-        pr = gm.PrefillRunner(cfg, params, cache, n, device=DEV, rope=r.rope)
-        pr.run(toks, n)
-        r.pos.fill_(255)
-        r.head(pr.x1[255], pr.mlp_out[255], pr.moe_out[255])
+        pr = gm.PrefillRunner(cfg, params, cache, 2048, device=DEV, rope=r.rope)
+        pr.run(toks, 2048)
+        r.pos.fill_(1023)
+        r.head(pr.x1[1023], pr.mlp_out[1023], pr.moe_out[1023])
         torch.cuda.synchronize()
-        kv = [gm.cache_positions(cache, i, upto=256)[j].cpu() for i in range(2) for j in range(2)]
-        out.append((kv, r.logits.cpu().clone()))
+        kv = [gm.cache_positions(cache, i, upto=1024)[j].cpu() for i in range(2) for j in range(2)]
+        later = [gm.cache_positions(cache, i, upto=2048)[j][1024:].cpu() for i in range(2) for j in range(2)]
+        out.append((kv, r.logits.cpu().clone(), later))
         del r, pr, cache
     for a, b in zip(out[0][0], out[1][0]):
         assert torch.equal(_bits(a), _bits(b))
     assert torch.equal(out[0][1], out[1][1])
+    # the later rows did change (the prompts differ there)
+    assert not torch.equal(_bits(out[0][2][0]), _bits(out[1][2][0]))
 
 
 def test_batch_engine_matches_batch1_runner(m26):

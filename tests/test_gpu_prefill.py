@@ -10,13 +10,14 @@ GEMM (g4mi_gemm_bf16) against float64 products of the same bf16 operands:
   * the gated epilogue against the same rounding points built from f64 gate
     and up values (model.py:220, 246-247): >= 97% bit-identical, corr >= 0.9999
     (a one-ulp flip of a rounded gate or up moves the product by one ulp).
-Cases: the library GEMM (rocBLAS) the batched prefill uses above 16 rows,
-and its gated path (two products and gated_act); plain 128x128 tiles with
-ragged edges, small M with split-K (the
-slices are summed in order, so split-K equals the one-slice result within
-f32 reassociation), the skinny kernel (M <= 16) alone and with column
-segments (several weight matrices sharing A in one launch), row gather,
-grouped per-expert tiles.
+Cases: the tile kernel at the 2,048-token prefill's product shapes (q/k/v/o
+and the dense MLP of both layer kinds; 2-stage two-blocks-per-CU and
+3-stage one-block-per-CU variants) and through prefill_gemm with the gated
+epilogue on separate gate and up tensors; 128x128 tiles with ragged edges,
+small M (64-row tiles) with split-K (the slices are summed in order, so
+split-K equals the one-slice result within f32 reassociation), the skinny
+kernel (M <= 16) alone and with column segments (several weight matrices
+sharing A in one launch), row gather, grouped per-expert tiles.
 
 MoE prefill (g4mi_moe_prefill) against the oracle's dense path
 (oracle.twin.moe(dense=True): every expert, masked by the routing weights),
@@ -143,31 +144,39 @@ def _close_bf16(got, ref, same_min=0.97):
     assert same >= same_min and corr >= 0.9999, (same, corr)
 
 
-@pytest.mark.parametrize("m,n,k", [(2048, 4096, 2816), (300, 1000, 2112), (17, 2816, 4096)])
-def test_gemm_library_bf16_and_f32(m, n, k):
-    """The library GEMM (rocBLAS, atomics disallowed) that the batched prefill
-    uses above 16 rows, to the same bounds as the MFMA kernel; repeated calls
-    are bit-identical."""
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 2816), (2048, 2048, 2816), (2048, 8192, 2816), (2048, 2816, 4096),
+                                   (2048, 2816, 2112), (2048, 1024, 2816), (54, 4096, 2816)])
+def test_gemm_prefill_shapes(m, n, k):
+    """The products of a 2,048-token (and the 54-token) prefill through
+    prefill_gemm: 512+ tiles run two blocks per CU with 2 LDS stages, fewer
+    one block with 3 stages, 54 rows 64-row tiles split over K; repeated
+    calls are bit-identical."""
     a, b = _rand((m, k), 16), _rand((n, k), 17, 0.02)
     ref, absum = _ref(a, b)
     ad, bd = a.to(DEV), b.to(DEV)
-    out = ops.gemm_library(ad, bd)
+    out = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    ops.prefill_gemm(ad, bd, out)
     _check_bf16(out, ref, absum)
-    assert torch.equal(ops.gemm_library(ad, bd).view(torch.int16), out.view(torch.int16))
-    _check_f32(ops.gemm_library(ad, bd, f32_out=True), ref, absum)
+    again = torch.empty_like(out)
+    ops.prefill_gemm(ad, bd, again)
+    assert torch.equal(again.view(torch.int16), out.view(torch.int16))
+    out32 = torch.empty((m, n), dtype=torch.float32, device=DEV)
+    ops.prefill_gemm(ad, bd, out32, epilogue=ops.EP_F32)
+    _check_f32(out32, ref, absum)
 
 
-@pytest.mark.parametrize("m", [17, 300])
-def test_prefill_gemm_gated_through_library(m):
-    """Above 16 rows prefill_gemm's gated epilogue is two library products and
-    gated_act: the same rounding points as the fused epilogue."""
+@pytest.mark.parametrize("m", [17, 300, 2048])
+def test_prefill_gemm_gated_separate_tensors(m):
+    """The dense MLP's gate/up product as the prefill issues it: gate and up
+    are separate allocations, reached as b and b + pair_offset (a signed
+    element distance) by the fused gated epilogue."""
     h, f = 2816, 2112
     a = _rand((m, h), 18)
     gate, up = _rand((f, h), 19, 0.02), _rand((f, h), 20, 0.02)
     gd, ud = gate.to(DEV), up.to(DEV)
     out = torch.empty((m, f), dtype=torch.bfloat16, device=DEV)
     ops.prefill_gemm(a.to(DEV), gd, out, epilogue=ops.EP_GATED, pair_offset=(ud.data_ptr() - gd.data_ptr()) // 2,
-                     n=f, up=ud)
+                     n=f)
     _close_bf16(out, _gated_ref(a, gate, up, None))
 
 
