@@ -273,28 +273,43 @@ static float bf16_inv_sqrt(int64_t H) {
   return r;
 }
 
-// Many rows (prefill): a block takes kRouterRows token rows and every
-// expert, so each router row is read once per kRouterRows tokens instead of
-// once per token.  Wave w normalises rows 2w and 2w+1 into LDS (wave-level f64
-// reductions, the same rounding steps as router_scores_kernel), then thread t
-// accumulates in f64 the dots of expert e0 + t % 128 with rows 4*(t/128) ..
-// +3, reading the expert's router row 128 bytes at a time.  H <= 4096 (the
-// rows fit 64 KB of LDS).
-constexpr int kRouterRows = 8;
-__global__ __launch_bounds__(256) void router_scores_tile_kernel(const uint16_t* __restrict__ x,
+// Many rows (prefill) on f64 MFMA (v_mfma_f64_16x16x4_f64: lane l supplies
+// A[l%16][l/16] and B[l/16][l%16] and holds D[4r + l/16][l%16], r < 4).  A
+// block takes kRouterMRows = 16 token rows and 64 experts: the rows are
+// normalised into LDS (the same rounding steps as router_scores_kernel),
+// then wave w accumulates the 16 x 16 dots of experts 64*blockIdx.y + 16w ..
+// +15 in f64 (the bf16 x bf16 products are exact; the sum is f64 as in the
+// per-row kernels, in another order).  Per 32-wide k chunk lane l reads 8
+// consecutive k of row l%16 (LDS) and of expert l%16 (router row, 16 bytes)
+// at chunk offset 8*(l/16), and MFMA s of the chunk takes k = 8*(l/16) + s:
+// the four k slots of the MFMA cover the chunk over s = 0..7.  H % 32 == 0,
+// H <= kRouterMaxH.
+constexpr int kRouterMRows = 16;
+constexpr int kRouterMExperts = 64;
+constexpr int kRouterMaxH = 4096;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(256) void router_scores_mfma_kernel(const uint16_t* __restrict__ x,
                                                                  const uint16_t* __restrict__ pre_w,
                                                                  const uint16_t* __restrict__ scale,
                                                                  const uint16_t* __restrict__ proj, int N, int H,
                                                                  int E, float eps, float inv_sqrt_h_bf,
                                                                  float* __restrict__ scores) {
-  extern __shared__ u32x4 xs_rows[];  // kRouterRows x H/8 chunks
+  __shared__ u32x4 xs_rows[kRouterMRows * kRouterMaxH / 8];  // 16 x H/8 chunks
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int CH = H / 8;
-  const int r0 = blockIdx.x * kRouterRows;
+  const int r0 = blockIdx.x * kRouterMRows;
+  const int e0 = blockIdx.y * kRouterMExperts + wave * 16;
   const u32x4* pw = (const u32x4*)pre_w;
   const u32x4* sw = (const u32x4*)scale;
-  for (int rr = 0; rr < 2; ++rr) {
-    const int r = wave * 2 + rr;
+  // this wave's first router rows, requested before the normalisation
+  const int er = min(e0 + (lane & 15), E - 1);
+  const u32x4* wrow = (const u32x4*)(proj + (size_t)er * H) + (lane >> 4);
+  constexpr int PF = 8;  // router chunks in flight per lane
+  u32x4 wq[PF];
+#pragma unroll
+  for (int u = 0; u < PF; ++u) wq[u] = ld16(wrow + 4 * min(u, CH / 4 - 1));
+  for (int rr = 0; rr < kRouterMRows / 4; ++rr) {
+    const int r = wave * (kRouterMRows / 4) + rr;
     const u32x4* xr = (const u32x4*)(x + (size_t)min(r0 + r, N - 1) * H);
     float rp = 1.0f;
     if (pre_w != nullptr) {  // pre_feedforward_layernorm_2 (model.py:315)
@@ -330,26 +345,33 @@ __global__ __launch_bounds__(256) void router_scores_tile_kernel(const uint16_t*
     }
   }
   __syncthreads();
-  const int rg = tid >> 7;
-  for (int e0 = 0; e0 < E; e0 += 128) {
-    const int e = e0 + (tid & 127);
-    if (e >= E) continue;
-    const u32x4* wrow = (const u32x4*)(proj + (size_t)e * H);
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int c0 = 0; c0 < CH; c0 += 8) {  // CH % 8 == 0 on this path
-      u32x4 w[8];
+  if (e0 >= E) return;  // no barrier below
+  const u32x4* xrow = xs_rows + (lane & 15) * CH + (lane >> 4);
+  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+  const int nch = CH / 4;  // 32-wide k chunks
+  for (int c0 = 0; c0 < nch; c0 += PF) {
 #pragma unroll
-      for (int u = 0; u < 8; ++u) w[u] = ld16(wrow + c0 + u);
+    for (int u = 0; u < PF; ++u) {
+      const int c = c0 + u;
+      if (c < nch) {
+        const u32x4 wv = wq[u];
+        wq[u] = ld16(wrow + 4 * min(c + PF, nch - 1));  // chunk c + PF (clamped: a cache hit at the end)
+        const u32x4 xv = xrow[4 * c];
+        const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[q] = dot8_f64(w[u], xs_rows[(4 * rg + q) * CH + c0 + u], acc[q]);
+        for (int s = 0; s < 8; ++s) {
+          const double a = (double)((s & 1) ? bf_hi(xw[s >> 1]) : bf_lo(xw[s >> 1]));
+          const double b = (double)((s & 1) ? bf_hi(ww[s >> 1]) : bf_lo(ww[s >> 1]));
+          acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+        }
+      }
     }
+  }
+  const int e = e0 + (lane & 15);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int n = r0 + 4 * rg + q;
-      if (n < N) scores[(size_t)n * E + e] = rbf(f32_of(acc[q]));
-    }
+  for (int r = 0; r < 4; ++r) {
+    const int n = r0 + 4 * r + (lane >> 4);
+    if (n < N && e < E) scores[(size_t)n * E + e] = rbf(f32_of(acc[r]));
   }
 }
 
@@ -357,13 +379,14 @@ static void launch_scores(const uint16_t* x, const uint16_t* pre_w, const uint16
                           int N, int H, int E, float eps, float* scores, hipStream_t st) {
   dim3 grid((unsigned)((E + 7) / 8), (unsigned)N);
   const float c = bf16_inv_sqrt(H);
-  // the tiled kernel (8 rows per block, every expert) takes ~110 us per call
-  // whatever N up to 2,048 rows at H = 2816, E = 128; the per-row kernel
-  // grows with N (~5 us at 54 rows, ~200 us at 2,048): tiles from 1,024 rows
-  if (N >= 1024 && H % 64 == 0 && H <= 4096 && ((uintptr_t)scale & 15u) == 0 && ((uintptr_t)pre_w & 15u) == 0) {
-    const size_t lds = (size_t)kRouterRows * (H / 8) * 16;
-    hipLaunchKernelGGL(router_scores_tile_kernel, dim3((unsigned)((N + kRouterRows - 1) / kRouterRows)), dim3(256),
-                       lds, st, x, pre_w, scale, proj, N, H, E, eps, c, scores);
+  // many rows: 16-row tiles on f64 MFMA; the per-row kernel grows with N
+  // (~5 us at 54 rows, ~200 us at 2,048)
+  if (N >= 128 && H % 32 == 0 && H <= kRouterMaxH && ((uintptr_t)scale & 15u) == 0 &&
+      ((uintptr_t)pre_w & 15u) == 0) {
+    const dim3 tgrid((unsigned)((N + kRouterMRows - 1) / kRouterMRows),
+                     (unsigned)((E + kRouterMExperts - 1) / kRouterMExperts));
+    hipLaunchKernelGGL(router_scores_mfma_kernel, tgrid, dim3(256), 0, st, x, pre_w, scale, proj, N, H, E, eps, c,
+                       scores);
     return;
   }
   const bool aligned = ((uintptr_t)scale & 15u) == 0 && ((uintptr_t)pre_w & 15u) == 0;

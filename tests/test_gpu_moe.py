@@ -277,8 +277,8 @@ def test_moe_block_tiny_and_f32_combine():
 
 
 def test_router_scores_many_rows_match_row_path(c2):
-    """N >= 1024 rows take the tiled router kernel (8 rows per block, every
-    expert); its scores equal the per-row kernel's (fewer rows) bit for bit
+    """N >= 128 rows take the f64-MFMA router kernel (16 rows x 64 experts per
+    block); its scores equal the per-row kernel's (64-row calls) bit for bit
     (both sum exact bf16 products in f64 and round once), with and without
     the pre_feedforward_layernorm_2 pre-norm; 1,031 rows leave a ragged last
     tile."""
@@ -289,10 +289,25 @@ def test_router_scores_many_rows_match_row_path(c2):
     pre = _gen((h,), 9, "router.pre", 0.5)
     for pw in (None, pre):
         many = ops.moe_router_scores(x, g["router.scale"], g["router.proj"], cfg.rms_norm_eps, pre_norm_w=pw)
-        rows = torch.cat([ops.moe_router_scores(x[i:i + 256].contiguous(), g["router.scale"], g["router.proj"],
-                                                cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, n, 256)])
+        rows = torch.cat([ops.moe_router_scores(x[i:i + 64].contiguous(), g["router.scale"], g["router.proj"],
+                                                cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, n, 64)])
         torch.cuda.synchronize()
         assert torch.equal(many, rows), (pw is None, (many != rows).sum().item())
+
+
+def test_router_scores_mfma_path_bit_exact(c2):
+    """300 rows (the f64-MFMA kernel, a ragged last tile) against the oracle's
+    f64 product of the same normalised rows, rounded once."""
+    cfg, g, cpu = c2
+    n = 300
+    x = _gen((n, cfg.hidden_size), 1, "x.mfma300", 1.0)
+    s = ops.moe_router_scores(x, g["router.scale"], g["router.proj"], cfg.rms_norm_eps)
+    torch.cuda.synchronize()
+    xc = twin.rms_norm(x.cpu(), None, cfg.rms_norm_eps)
+    c = float(twin.rb(torch.tensor(cfg.hidden_size ** -0.5, dtype=torch.float32)))
+    x2 = twin.rb(twin.f32(twin.rb(twin.f32(xc) * twin.f32(cpu["router.scale"]))) * np.float32(c))
+    exp = twin.f32(twin.rb(torch.einsum("nh,eh->ne", x2.double(), cpu["router.proj"].double())))
+    assert np.array_equal(s.cpu().numpy(), exp.numpy())
 
 
 @pytest.mark.parametrize("e,k,n", [(128, 8, 64), (16, 4, 64), (256, 32, 16), (200, 8, 16)])
