@@ -7,6 +7,9 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
+#include <utility>
 #include <stdint.h>
 
 namespace g4mi {
@@ -95,6 +98,16 @@ __device__ __forceinline__ u32x4 ld_stream(const u32x4* p) { return __builtin_no
 // same threadIdx.x >> 6, and saying so keeps loops and branches on it
 // uniform (scalar branches; no exec-masked loops whose loads the compiler
 // sinks into divergent blocks behind a full vmcnt(0) wait).
+// f(integral_constant<int, i>) for i = 0 .. N-1
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 

@@ -94,16 +94,6 @@ constexpr int kBK = 64;  // K per pipeline stage
 // MFMAs; ST = 3 (one block per CU) covers more latency when there are fewer
 // tiles than CUs.
 
-// f(integral_constant<int, i>) for i = 0 .. N-1
-template <typename F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
 // Waits until at most N of this wave's vector memory operations (the DMA of
 // later steps) are outstanding and its LDS reads are done, then the barrier.
 template <int N>
