@@ -228,15 +228,18 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
   }
   u32x4 bt[TPW][KS];
   long long ot[TPW];
-#pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
+  auto load_first = [&](int tt) {
     const bool valid = pe0[tt] >= 0 && pe0[tt] < a.num_pages;
     ot[tt] = valid ? ((((long long)pe0[tt] * a.KV + kv) * a.page) + ((start + jc0[tt]) % a.page)) * (long long)D
                    : -1ll;
     const uint16_t* kp = k_pages + max(ot[tt], 0ll) + 8 * kg;
 #pragma unroll
     for (int s = 0; s < KS; ++s) bt[tt][s] = ld16((const u32x4*)(kp + 32 * s));
-  }
+  };
+  // the first tile of each wave before the prologue, the others after it (a
+  // wave that requested every tile up front would stall at issue, with the
+  // prologue behind the stalled requests)
+  load_first(0);
   // padding rows G..15 of the A operand are zero
   for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -258,7 +261,9 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
     }
   }
   stage_store<NT>(pts, ptl);
-  __syncthreads();
+  lds_barrier();
+#pragma unroll
+  for (int tt = 1; tt < TPW; ++tt) load_first(tt);
   if (mine) {
     const long long off = page_off_lds(a, ptl, first, pos, kv);
     if (off >= 0)
@@ -318,7 +323,7 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
       ocur = onext;
     }
   }
-  __syncthreads();
+  lds_barrier();
   // the split's max and sum of exp per head: wave w owns heads w, w+NW, so
   // the heads reduce in parallel and no further barrier is needed
 #pragma unroll
@@ -522,7 +527,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
     ok[st] = (st < nst) && (j < len) && valid;
   }
   reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
-  __syncthreads();
+  lds_barrier();
   // normalised probabilities, rounded to bf16 (model.py:212), zero past len
 #pragma unroll
   for (int r = 0; r < SPT; ++r) {
@@ -530,7 +535,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
     const float sv = sreg[r];
     if (j < len) pr[g * kShortLen + j] = (sv == -INFINITY) ? 0.0f : rbf(expf(sv - mg[g]) / sg[g]);
   }
-  __syncthreads();
+  lds_barrier();
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
@@ -561,7 +566,7 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
 #pragma unroll
       for (int i = 0; i < 8; ++i) red[(wave * G + g) * kSliceD + sub * 8 + i] = acc[g][i];
   }
-  __syncthreads();
+  lds_barrier();
   for (int e = tid; e < G * kSliceD; e += NT) {
     const int g = e / kSliceD, dd = e % kSliceD;
     float v = red[g * kSliceD + dd];
@@ -573,11 +578,19 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
 
 // pv_long8: the long-range body for 8 waves (NW = 8).  Wave w owns the
 // head dims [w*D/8, (w+1)*D/8): DW/8 lanes per position, PPV positions per
-// wave step, and every step's V row slice of the split is requested at once
-// (at most kChunkMax / PPV steps), so a whole split's V rows are in flight
-// together; then the pairs of steps are dotted with the bf16 probabilities
-// as in the 4-wave body.  Writes the wave's partial sums to v_out (per head,
-// 8 dims per lane, summed over the PPV positions of a step).
+// wave step, at most kChunkMax / PPV steps per split.  The V row slices of
+// the first 4 steps are requested before the split statistics are merged,
+// those of the next kPvRing - 4 once the probabilities are in LDS; then the
+// pairs of steps are dotted with the bf16 probabilities as in the 4-wave
+// body, each consumed pair's registers refilled with the pair kPvRing steps
+// ahead.  (A CU queues only so many vector memory instructions: a wave that
+// requests more rows than that ahead of other work stalls at issue until
+// the earlier requests drain, so the merge and the products would start
+// only once most of the split had arrived.)
+// Writes the wave's partial sums to v_out (per head, 8 dims per lane, summed
+// over the PPV positions of a step).
+constexpr int kPvRing = 12;
+
 template <int D, int G>
 __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int split, int kv, int b,
                                          const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
@@ -589,15 +602,18 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   constexpr int LPV = DW / 8;                   // lanes per position
   constexpr int PPV = 64 / LPV;                 // positions per wave step
   constexpr int MAXST = kChunkMax / PPV;        // steps per split at most
+  constexpr int RB = kPvRing < MAXST ? kPvRing : MAXST;  // steps in flight
+  constexpr int RB0 = RB < 4 ? RB : 4;                   // of which requested before the merge
   constexpr int RS = (G * kChunkMax + NT - 1) / NT;  // scores per thread
-  static_assert(D % (NW * 8) == 0 && MAXST % 2 == 0, "pv_long8 layout");
+  static_assert(D % (NW * 8) == 0 && MAXST % 2 == 0 && RB % 2 == 0, "pv_long8 layout");
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
   const int slot = lane % PPV, sub = lane / PPV;
   const int dofs = wave * DW + sub * 8;
-  // the split's scores, the split statistics, then every V row of the split
+  // the split's scores, the split statistics, every step's page-table entry,
+  // then the first RB steps' V rows
   float sreg[RS];
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
@@ -611,21 +627,21 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   for (int st = 0; st < MAXST; ++st) pg[st] = pt_row[(start + min(st * PPV + slot, npos - 1)) / a.page];
   // keep the small loads above ahead of the V rows in issue order: vmcnt
   // waits are in order, and a statistics load moved after the rows would
-  // wait for the whole split's V
+  // wait for the rows
   asm volatile("" ::: "memory");
-  u32x4 vv[MAXST];
   bool ok[MAXST];
-#pragma unroll
-  for (int st = 0; st < MAXST; ++st) {
+  auto vrow = [&](int st) {  // V slice of step st (clamped position, page 0 when the entry is invalid)
     const int j = st * PPV + slot;
     const int p = start + min(j, npos - 1);
     const bool valid = pg[st] >= 0 && pg[st] < a.num_pages;
-    const long long off = ((((long long)(valid ? pg[st] : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
-    vv[st] = ld16((const u32x4*)(v_pages + off + dofs));
     ok[st] = (st < nsteps) && (j < npos) && valid;
-  }
+    const long long off = ((((long long)(valid ? pg[st] : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+    return ld16((const u32x4*)(v_pages + off + dofs));
+  };
+  u32x4 vv[RB];
+  static_for<RB0>([&](auto S) __attribute__((always_inline)) { vv[S] = vrow(S); });
   reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
-  __syncthreads();
+  lds_barrier();
   // normalised probabilities, rounded to bf16 (model.py:212), as bf16 pairs:
   // the positions of wave steps 2q and 2q + 1 at lane slot `sl` share word
   // q * PPV + sl (zero past npos)
@@ -640,18 +656,19 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
       pr16[g * kChunkMax + ((step >> 1) * PPV + sl) * 2 + (step & 1)] = f2bf(pv);
     }
   }
-  __syncthreads();
+  lds_barrier();
+  static_for<RB - RB0>([&](auto S) __attribute__((always_inline)) { vv[RB0 + S] = vrow(RB0 + S); });
   const uint32_t* pr32 = reinterpret_cast<const uint32_t*>(lds_f);
   float acc[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
-#pragma unroll
-  for (int u = 0; u < MAXST; u += 2) {
+  static_for<MAXST / 2>([&](auto U) __attribute__((always_inline)) {
+    constexpr int u = 2 * U;
     if (u < nsteps) {
       const u32x4 z = {0u, 0u, 0u, 0u};
-      const u32x4 va = ok[u] ? vv[u] : z, vb = ok[u + 1] ? vv[u + 1] : z;
+      const u32x4 va = ok[u] ? vv[u % RB] : z, vb = ok[u + 1] ? vv[(u + 1) % RB] : z;
       uint32_t vp[8];
       vp[0] = __builtin_amdgcn_perm(vb.x, va.x, 0x05040100u);
       vp[1] = __builtin_amdgcn_perm(vb.x, va.x, 0x07060302u);
@@ -669,7 +686,11 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
         for (int i = 0; i < 8; ++i) acc[g][i] = dot2bf(vp[i], pp, acc[g][i]);
       }
     }
-  }
+    if constexpr (u + RB < MAXST) {
+      vv[u % RB] = vrow(u + RB);
+      vv[(u + 1) % RB] = vrow(u + RB + 1);
+    }
+  });
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -775,7 +796,7 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
   vload(0, vcur, okcur, false);
   stage_store(pts, ptl);
   reduce_split_stats<G>(sst, R, wave, lane, mg, sg);
-  __syncthreads();
+  lds_barrier();
   // normalised probabilities, rounded to bf16 as the reference does
   // (model.py:212), stored as bf16 pairs: the positions of wave steps 2q and
   // 2q + 1 at lane slot `sl` share word q * PPV + sl (zero past npos)
@@ -788,7 +809,7 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
     const int step = j / PPV, sl = j % PPV;
     pr16[g * kChunkMax + ((step >> 1) * PPV + sl) * 2 + (step & 1)] = f2bf(pv);
   }
-  __syncthreads();
+  lds_barrier();
   const uint32_t* pr32 = reinterpret_cast<const uint32_t*>(lds_f);
   float acc[G][8];
 #pragma unroll

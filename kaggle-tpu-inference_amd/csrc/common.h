@@ -108,6 +108,14 @@ __device__ __forceinline__ void static_for(F&& f) {
   static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
+// A block barrier for data exchanged through LDS alone.  __syncthreads()
+// also waits for every global load the wave has in flight (its workgroup
+// fence drains vmcnt), so rows requested ahead of it would all have to
+// arrive before any wave passes; this waits only for the wave's LDS
+// operations, and each load in flight is waited for where its registers are
+// first used.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 
