@@ -228,18 +228,23 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
   }
   u32x4 bt[TPW][KS];
   long long ot[TPW];
-  auto load_first = [&](int tt) {
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
     const bool valid = pe0[tt] >= 0 && pe0[tt] < a.num_pages;
     ot[tt] = valid ? ((((long long)pe0[tt] * a.KV + kv) * a.page) + ((start + jc0[tt]) % a.page)) * (long long)D
                    : -1ll;
+  }
+  auto load_chunks = [&](int tt, int s0, int s1) {
     const uint16_t* kp = k_pages + max(ot[tt], 0ll) + 8 * kg;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) bt[tt][s] = ld16((const u32x4*)(kp + 32 * s));
+    for (int s = s0; s < s1; ++s) bt[tt][s] = ld16((const u32x4*)(kp + 32 * s));
   };
-  // the first tile of each wave before the prologue, the others after it (a
-  // wave that requested every tile up front would stall at issue, with the
-  // prologue behind the stalled requests)
-  load_first(0);
+  // On the 8-wave path only the first KS0 chunks of each wave's first tile
+  // are requested before the prologue, the rest after it: a CU queues only so
+  // many vector memory instructions, and a wave that requested its whole
+  // tiles up front would stall at issue with the prologue behind them.
+  constexpr int KS0 = (NW == 8 && KS > 4) ? 4 : KS;
+  load_chunks(0, 0, KS0);
   // padding rows G..15 of the A operand are zero
   for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
@@ -262,8 +267,9 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
   }
   stage_store<NT>(pts, ptl);
   lds_barrier();
+  load_chunks(0, KS0, KS);
 #pragma unroll
-  for (int tt = 1; tt < TPW; ++tt) load_first(tt);
+  for (int tt = 1; tt < TPW; ++tt) load_chunks(tt, 0, KS);
   if (mine) {
     const long long off = page_off_lds(a, ptl, first, pos, kv);
     if (off >= 0)
@@ -595,8 +601,8 @@ template <int D, int G>
 __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int split, int kv, int b,
                                          const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
                                          const float* ws_scores, const float* ws_stats,
-                                         float* lds_f, float* mg, float* sg, float (*v_out)[8], int& dofs_out,
-                                         int& slot_out) {
+                                         float* lds_f, float* mg, float* sg, int* ptl, float (*v_out)[8],
+                                         int& dofs_out, int& slot_out) {
   constexpr int NW = 8, NT = 512;
   constexpr int DW = D / NW;                    // dims per wave
   constexpr int LPV = DW / 8;                   // lanes per position
@@ -612,8 +618,9 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   const int npos = end - start;
   const int slot = lane % PPV, sub = lane / PPV;
   const int dofs = wave * DW + sub * 8;
-  // the split's scores, the split statistics, every step's page-table entry,
-  // then the first RB steps' V rows
+  // the split's scores, the split statistics, the page-table entries of the
+  // first RB0 steps and of the whole split (staged in LDS for the later
+  // steps), then the first RB0 steps' V rows
   float sreg[RS];
 #pragma unroll
   for (int r = 0; r < RS; ++r) {
@@ -622,24 +629,32 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   }
   SplitStats<G, NW> sst = load_split_stats<G, NW>(a, R, kv, b, wave, lane, ws_stats);
   const int nsteps = (npos + PPV - 1) / PPV;
-  int pg[MAXST];
+  const int first = start / a.page;
+  int pg0[RB0];
 #pragma unroll
-  for (int st = 0; st < MAXST; ++st) pg[st] = pt_row[(start + min(st * PPV + slot, npos - 1)) / a.page];
+  for (int st = 0; st < RB0; ++st) pg0[st] = pt_row[(start + min(st * PPV + slot, npos - 1)) / a.page];
+  const PtStage<NT> pts = stage_load<NT>(a, pt_row, first);
   // keep the small loads above ahead of the V rows in issue order: vmcnt
   // waits are in order, and a statistics load moved after the rows would
   // wait for the rows
   asm volatile("" ::: "memory");
   bool ok[MAXST];
-  auto vrow = [&](int st) {  // V slice of step st (clamped position, page 0 when the entry is invalid)
+  // V slice of step st (clamped position; page 0 when the entry is invalid)
+  auto vrow = [&](auto S) __attribute__((always_inline)) {
+    constexpr int st = S;
     const int j = st * PPV + slot;
     const int p = start + min(j, npos - 1);
-    const bool valid = pg[st] >= 0 && pg[st] < a.num_pages;
+    int e;
+    if constexpr (st < RB0) e = pg0[st];
+    else e = ptl[p / a.page - first];
+    const bool valid = e >= 0 && e < a.num_pages;
     ok[st] = (st < nsteps) && (j < npos) && valid;
-    const long long off = ((((long long)(valid ? pg[st] : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
+    const long long off = ((((long long)(valid ? e : 0) * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
     return ld16((const u32x4*)(v_pages + off + dofs));
   };
   u32x4 vv[RB];
   static_for<RB0>([&](auto S) __attribute__((always_inline)) { vv[S] = vrow(S); });
+  stage_store<NT>(pts, ptl);
   reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
   lds_barrier();
   // normalised probabilities, rounded to bf16 (model.py:212), as bf16 pairs:
@@ -657,7 +672,9 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
     }
   }
   lds_barrier();
-  static_for<RB - RB0>([&](auto S) __attribute__((always_inline)) { vv[RB0 + S] = vrow(RB0 + S); });
+  static_for<RB - RB0>([&](auto S) __attribute__((always_inline)) {
+    vv[RB0 + S] = vrow(std::integral_constant<int, RB0 + S>{});
+  });
   const uint32_t* pr32 = reinterpret_cast<const uint32_t*>(lds_f);
   float acc[G][8];
 #pragma unroll
@@ -687,8 +704,8 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
       }
     }
     if constexpr (u + RB < MAXST) {
-      vv[u % RB] = vrow(u + RB);
-      vv[(u + 1) % RB] = vrow(u + RB + 1);
+      vv[u % RB] = vrow(std::integral_constant<int, u + RB>{});
+      vv[(u + 1) % RB] = vrow(std::integral_constant<int, u + RB + 1>{});
     }
   });
 #pragma unroll
@@ -742,15 +759,17 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
     float v[G][8];
     int dofs, slot;
     pv_long8<D, G>(a, R, split, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, lds_f, mg,
-                   sg, v, dofs, slot);
+                   sg, ptl, v, dofs, slot);
+    // the partials are reduced by attn_reduce_kernel, the next launch
     if (slot == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         const uint32_t o = pbase + (uint32_t)(g * D + dofs) * 4;
-        coherent_store4(rpart, o, make_float4(v[g][0], v[g][1], v[g][2], v[g][3]));
-        coherent_store4(rpart, o + 16, make_float4(v[g][4], v[g][5], v[g][6], v[g][7]));
+        store4(rpart, o, make_float4(v[g][0], v[g][1], v[g][2], v[g][3]));
+        store4(rpart, o + 16, make_float4(v[g][4], v[g][5], v[g][6], v[g][7]));
       }
     }
+    return;
   } else {
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
@@ -891,6 +910,65 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
   store_bf16x4<E4, G * D / 4, NT>(out, sum);
 }
 
+// ------------------------------------------------------------------ split reduction (8-wave path)
+// ctx[b, kv*G + g, :] = bf16(sum of the split partials of the 8-wave P.V
+// launch), summed in the order of the in-kernel reduction of the 4-wave path
+// (groups of kGroup consecutive splits, each in split order from +0, then
+// the group sums in group order from +0).  Run as its own launch, every
+// partial in flight at once: a chain of in-kernel arrivals costs a
+// write-through, an atomic round trip and a read per level.  grid
+// (ceil(G*D/4 / kRedCols), KV, B), 256 threads: thread (h, c) sums groups
+// h, h + 8 of float4 column c.  Ranges the P.V launch finished itself
+// (nothing attended, or at most kShortLen positions) are left alone.
+constexpr int kRedCols = 32;   // float4 columns per block
+constexpr int kRedRows = 8;    // groups summed side by side
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int32_t* __restrict__ pos_arr,
+                                                          const float* __restrict__ ws_part,
+                                                          uint16_t* __restrict__ ctx) {
+  constexpr int N4 = G * D / 4;  // float4 columns of one KV head's group of heads
+  __shared__ float4 gs[kMaxGroups][kRedCols];
+  const int kv = blockIdx.y, b = blockIdx.z;
+  const Range R = attn_range(a, pos_arr[b]);
+  if (R.n_eff == 0 || R.len <= kShortLen) return;
+  const int c = threadIdx.x % kRedCols, h = threadIdx.x / kRedCols;
+  const int col = min((int)blockIdx.x * kRedCols + c, N4 - 1);
+  const int ngroups = (R.n_eff + kGroup - 1) / kGroup;
+  const size_t stride4 = (size_t)a.NH * D / 4;  // float4s per split partial
+  const float4* part = reinterpret_cast<const float4*>(ws_part) + (size_t)b * a.n_split_max * stride4 +
+                       (size_t)kv * G * D / 4 + col;
+#pragma unroll
+  for (int m = 0; m < kMaxGroups / kRedRows; ++m) {
+    const int g = h + kRedRows * m;
+    if (g < ngroups) {
+      const int n = min(kGroup, R.n_eff - g * kGroup);
+      float4 v[kGroup];
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i) v[i] = part[(size_t)(g * kGroup + min(i, n - 1)) * stride4];
+      float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+      for (int i = 0; i < kGroup; ++i)
+        if (i < n) {
+          t.x += v[i].x; t.y += v[i].y; t.z += v[i].z; t.w += v[i].w;
+        }
+      gs[g][c] = t;
+    }
+  }
+  __syncthreads();
+  if (h == 0 && (int)blockIdx.x * kRedCols + c < N4) {
+    float4 t = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int g = 0; g < ngroups; ++g) {
+      const float4 u = gs[g][c];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    uint2 w;
+    w.x = pack2(t.x, t.y);
+    w.y = pack2(t.z, t.w);
+    reinterpret_cast<uint2*>(ctx + (size_t)b * a.NH * D + (size_t)kv * G * D)[col] = w;
+  }
+}
+
 // ------------------------------------------------------------------ append
 // k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) of T tokens of one
 // sequence written at positions pos[t] (model.py:202-206).  grid (T, KV).
@@ -956,6 +1034,8 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
                        k_norm, cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
     hipLaunchKernelGGL((attn_pv_kernel<D, G, 8>), pgrid, dim3(512), 0, st, a, vp, pt, pos, w.scores, w.stats,
                        w.part, w.group, w.counters, ctx);
+    const dim3 rgrid((unsigned)((G * D / 4 + kRedCols - 1) / kRedCols), grid.y, grid.z);
+    hipLaunchKernelGGL((attn_reduce_kernel<D, G>), rgrid, dim3(256), 0, st, a, pos, w.part, ctx);
   }
 }
 

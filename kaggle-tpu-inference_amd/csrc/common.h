@@ -240,6 +240,13 @@ __device__ __forceinline__ void coherent_store4(__amdgpu_buffer_rsrc_t r, uint32
   w.x = __float_as_uint(v.x); w.y = __float_as_uint(v.y); w.z = __float_as_uint(v.z); w.w = __float_as_uint(v.w);
   __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, kCPolSC1);
 }
+// An ordinary (L2 write-back) 16-byte buffer store, for data read only by
+// later launches.
+__device__ __forceinline__ void store4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, float4 v) {
+  u32x4 w;
+  w.x = __float_as_uint(v.x); w.y = __float_as_uint(v.y); w.z = __float_as_uint(v.z); w.w = __float_as_uint(v.w);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, byte_off, 0, 0);
+}
 __device__ __forceinline__ u32x4 coherent_load16(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, kCPolSC1);
 }
