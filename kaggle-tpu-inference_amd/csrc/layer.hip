@@ -123,15 +123,17 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
     vload(x, a.x_in, NCH);
   }
   // The compiler may not sink the prologue loads below the row loads (their
-  // results would then wait for the rows).  All NPF row batches of the wave
-  // are requested before the prologue, so the prologue's latency (the layer
-  // tail is three dependent block reductions) hides under the weight stream.
+  // results would then wait for the rows).  One row batch of the wave is
+  // requested before the prologue and the other NPF - 1 after it: a CU
+  // queues only so many vector memory instructions, and a wave that
+  // requested all its batches first would stall at issue, the prologue (the
+  // layer tail is three dependent block reductions) behind the stalled
+  // requests, until most of its rows had arrived.
   asm volatile("" ::: "memory");
   PairWalk<IT> pw(a.pairs_per_block, (total + 1) / 2);
   constexpr int NPF = kInPrefetch;
   u32x4 w[NPF][IT];
-#pragma unroll
-  for (int d = 0; d < NPF; ++d) load_row<32, IT>(rowptr(min(pw.p + 4 * d, pw.plast)), l, w[d]);
+  load_row<32, IT>(rowptr(min(pw.p, pw.plast)), l, w[0]);
   if constexpr (MODE == kInEmbed) vmul(x, a.embed_c);
   if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, H, a.eps, red);
   if constexpr (MODE != kInNormed) {
@@ -142,7 +144,9 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
     vscale_w(x, r, win);
   }
   vstore(x, xs, NCH);
-  __syncthreads();
+  lds_barrier();
+#pragma unroll
+  for (int d = 1; d < NPF; ++d) load_row<32, IT>(rowptr(min(pw.p + 4 * d, pw.plast)), l, w[d]);
   int p = pw.p;
   // full batches: consume pair p+4d, refill it with pair p+4d+4*NPF (clamped)
   for (; p + 4 * NPF < pw.pend; p += 4 * NPF) {
@@ -264,13 +268,11 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   const int tend = min(t0 + a.tasks_per_block, a.I), tlast = max(tend - 1, 0);
   const int e = (int)blockIdx.x * 8 + wave * 2 + half;
   auto dense_row = [&](int f) { return (half ? a.up : a.gate) + (size_t)f * H; };
-  // every task of this wave (t0 + wave + 4j, j < kFfnInTasks) is requested
-  // before the prologue; router blocks request their one row
+  // the wave's first task (router blocks: their one row) is requested
+  // before the prologue, the other tasks (t0 + wave + 4j, j < kFfnInTasks)
+  // after it, so the prologue does not wait behind requests stalled at issue
   u32x4 w[kFfnInTasks][IT];
   load_row<32, IT>(dense ? dense_row(min(t0 + wave, tlast)) : a.r_proj + (size_t)min(e, a.E - 1) * H, l, w[0]);
-#pragma unroll
-  for (int j = 1; j < kFfnInTasks; ++j)
-    if (dense) load_row<32, IT>(dense_row(min(t0 + wave + 4 * j, tlast)), l, w[j]);
   // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
   vscale_w(o, vrms(o, H, a.eps, red), wpa);
   vadd(x, o);
@@ -300,8 +302,10 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
       }
     }
   }
-  __syncthreads();
+  lds_barrier();
   if (dense) {
+#pragma unroll
+    for (int j = 1; j < kFfnInTasks; ++j) load_row<32, IT>(dense_row(min(t0 + wave + 4 * j, tlast)), l, w[j]);
 #pragma unroll
     for (int j = 0; j < kFfnInTasks; ++j) {
       const int t = t0 + wave + 4 * j;
