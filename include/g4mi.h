@@ -122,7 +122,10 @@ int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, cons
  *   q_raw [B,NH,D], k_raw/v_raw [B,KV,D] bf16: the raw projections of the new
  *   token (v_raw NULL on k==v layers: V = rms_norm(k_raw)); q_norm/k_norm [D];
  *   rope_cos/rope_sin [>=lmax, D/2] bf16; k_pages/v_pages [num_pages,KV,PAGE,D];
- *   page_table [B,max_pages] int32; pos [B] int32 (device).
+ *   page_table [B,max_pages] int32, or NULL when sequence b owns pages
+ *   [b*max_pages, (b+1)*max_pages) in order (B*max_pages <= num_pages; the
+ *   kernels then compute page indices instead of loading them); pos [B]
+ *   int32 (device).
  * With append != 0 the new K/V are normalised, roped and written at pos.
  * ctx [B,NH,D] bf16.  D in {64,128,256,512}; NH/KV in {1,2,4,8};
  * g4mi_attention_min_splits(span) <= n_split_max <= 256, span = window (when

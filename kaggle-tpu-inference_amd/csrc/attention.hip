@@ -75,6 +75,27 @@ __device__ __forceinline__ long long page_off_lds(const AttnDims& a, const int* 
   return ((((long long)page * a.KV + kv) * a.page) + (p % a.page)) * (long long)a.D;
 }
 
+// A sequence's page-table row.  With DENSE the caller passed no table: the
+// cache's sequence b owns pages [b * max_pages, (b + 1) * max_pages) in
+// order, and an entry is computed instead of loaded (one dependent memory
+// round trip less between a position and its K/V rows).
+template <bool DENSE>
+struct PtRow {
+  const int32_t* row;  // unused when DENSE
+  int base;            // b * max_pages when DENSE
+  __device__ __forceinline__ int operator[](int i) const {
+    if constexpr (DENSE) return base + i;
+    else return row[i];
+  }
+};
+template <bool DENSE>
+__device__ __forceinline__ PtRow<DENSE> pt_row_of(const AttnDims& a, const int32_t* page_table, int b) {
+  PtRow<DENSE> r;
+  r.row = DENSE ? page_table : page_table + (size_t)b * a.max_pages;
+  r.base = b * a.max_pages;
+  return r;
+}
+
 // Requests the page-table entries of pages [first, first + 512) of one
 // sequence (clamped to the row) into registers of an NT-thread block;
 // stage_store() writes them to LDS before the block's next barrier.  A split
@@ -83,8 +104,8 @@ template <int NT = 256>
 struct PtStage {
   int v[512 / NT];
 };
-template <int NT = 256>
-__device__ __forceinline__ PtStage<NT> stage_load(const AttnDims& a, const int32_t* pt_row, int first) {
+template <int NT = 256, typename PT>
+__device__ __forceinline__ PtStage<NT> stage_load(const AttnDims& a, const PT& pt_row, int first) {
   PtStage<NT> s;
 #pragma unroll
   for (int r = 0; r < 512 / NT; ++r) s.v[r] = pt_row[min(first + (int)threadIdx.x + NT * r, a.max_pages - 1)];
@@ -155,7 +176,7 @@ __device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const 
 // nothing to prefetch.  NW = 8 (long ranges): 8 waves, and every tile a wave
 // owns (tiles w and w + 8 of a split's 16 at most) is requested before the
 // prologue, so a whole split's K rows are in flight at once.
-template <int D, int G, bool ONE, int NW = 4>
+template <int D, int G, bool ONE, int NW, bool DPT>
 __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
     AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
     const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
@@ -182,7 +203,7 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
-  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
+  const PtRow<DPT> pt_row = pt_row_of<DPT>(a, page_table, b);
 
   // Everything that needs only pos is requested first, in this order: the
   // split's page-table entries, this wave's first K tile's entry, and the
@@ -489,9 +510,9 @@ __device__ __forceinline__ void reduce_split_stats(SplitStats<G, NW>& st, const 
 constexpr int kShortLen = 512;
 constexpr int kSliceD = 32;
 
-template <int D, int G, int NW = 4>
+template <int D, int G, int NW, typename PT>
 __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int kv, int b,
-                                         const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
+                                         const uint16_t* __restrict__ v_pages, const PT& pt_row,
                                          const float* ws_scores, const float* ws_stats,
                                          uint16_t* __restrict__ ctx, float* pr, float* red, float* mg, float* sg) {
   constexpr int NT = NW * 64;
@@ -597,9 +618,9 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
 // over the PPV positions of a step).
 constexpr int kPvRing = 12;
 
-template <int D, int G>
+template <int D, int G, typename PT>
 __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int split, int kv, int b,
-                                         const uint16_t* __restrict__ v_pages, const int32_t* __restrict__ pt_row,
+                                         const uint16_t* __restrict__ v_pages, const PT& pt_row,
                                          const float* ws_scores, const float* ws_stats,
                                          float* lds_f, float* mg, float* sg, int* ptl, float (*v_out)[8],
                                          int& dofs_out, int& slot_out) {
@@ -716,7 +737,7 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   slot_out = slot;
 }
 
-template <int D, int G, int NW = 4>
+template <int D, int G, int NW, bool DPT>
 __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint16_t* __restrict__ v_pages,
                                                       const int32_t* __restrict__ page_table,
                                                       const int32_t* __restrict__ pos_arr,
@@ -742,7 +763,7 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
   const Range R = attn_range(a, pos);
   if (R.n_eff > 0 && R.len <= kShortLen) {  // grid.x >= D / kSliceD (see launch_attn)
     if (split < D / kSliceD)
-      pv_short<D, G, NW>(a, R, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, ctx,
+      pv_short<D, G, NW>(a, R, kv, b, v_pages, pt_row_of<DPT>(a, page_table, b), ws_scores, ws_stats, ctx,
                          lds_f, lds_f + G * kShortLen, mg, sg);
     return;
   }
@@ -758,7 +779,7 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
   if constexpr (NW == 8) {
     float v[G][8];
     int dofs, slot;
-    pv_long8<D, G>(a, R, split, kv, b, v_pages, page_table + (size_t)b * a.max_pages, ws_scores, ws_stats, lds_f, mg,
+    pv_long8<D, G>(a, R, split, kv, b, v_pages, pt_row_of<DPT>(a, page_table, b), ws_scores, ws_stats, lds_f, mg,
                    sg, ptl, v, dofs, slot);
     // the partials are reduced by attn_reduce_kernel, the next launch
     if (slot == 0) {
@@ -774,7 +795,7 @@ __global__ __launch_bounds__(NW * 64) void attn_pv_kernel(AttnDims a, const uint
   const int start = R.lo + split * R.chunk;
   const int end = min(R.lo + R.len, start + R.chunk);
   const int npos = end - start;
-  const int32_t* pt_row = page_table + (size_t)b * a.max_pages;
+  const PtRow<DPT> pt_row = pt_row_of<DPT>(a, page_table, b);
   const int slot = lane % PPV, sub = lane / PPV;  // the positions of a step are consecutive lanes
   const int dofs = wave * (D / 4) + sub * 8;
 
@@ -1013,7 +1034,7 @@ struct AttnWs {
   unsigned int* counters;
 };
 
-template <int D, int G>
+template <int D, int G, bool DPT>
 static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint16_t* q_raw, const uint16_t* k_raw,
                         const uint16_t* v_raw, const uint16_t* q_norm, const uint16_t* k_norm, const uint16_t* cs,
                         const uint16_t* sn, uint16_t* kp, uint16_t* vp, const int32_t* pt, const int32_t* pos,
@@ -1025,14 +1046,14 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
   const int span = (a.window > 0 && a.window < a.lmax) ? a.window : a.lmax;
   const dim3 pgrid(max(grid.x, (unsigned)(D / kSliceD)), grid.y, grid.z);  // short ranges use D / kSliceD blocks
   if (span <= kChunkMin * a.n_split_max) {
-    hipLaunchKernelGGL((attn_qk_kernel<D, G, true>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm, k_norm,
-                       cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
-    hipLaunchKernelGGL((attn_pv_kernel<D, G>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats, w.part,
-                       w.group, w.counters, ctx);
-  } else {
-    hipLaunchKernelGGL((attn_qk_kernel<D, G, false, 8>), grid, dim3(512), 0, st, a, q_raw, k_raw, v_raw, q_norm,
+    hipLaunchKernelGGL((attn_qk_kernel<D, G, true, 4, DPT>), grid, dim3(256), 0, st, a, q_raw, k_raw, v_raw, q_norm,
                        k_norm, cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
-    hipLaunchKernelGGL((attn_pv_kernel<D, G, 8>), pgrid, dim3(512), 0, st, a, vp, pt, pos, w.scores, w.stats,
+    hipLaunchKernelGGL((attn_pv_kernel<D, G, 4, DPT>), pgrid, dim3(256), 0, st, a, vp, pt, pos, w.scores, w.stats,
+                       w.part, w.group, w.counters, ctx);
+  } else {
+    hipLaunchKernelGGL((attn_qk_kernel<D, G, false, 8, DPT>), grid, dim3(512), 0, st, a, q_raw, k_raw, v_raw,
+                       q_norm, k_norm, cs, sn, kp, vp, pt, pos, append, w.scores, w.stats);
+    hipLaunchKernelGGL((attn_pv_kernel<D, G, 8, DPT>), pgrid, dim3(512), 0, st, a, vp, pt, pos, w.scores, w.stats,
                        w.part, w.group, w.counters, ctx);
     const dim3 rgrid((unsigned)((G * D / 4 + kRedCols - 1) / kRedCols), grid.y, grid.z);
     hipLaunchKernelGGL((attn_reduce_kernel<D, G>), rgrid, dim3(256), 0, st, a, pos, w.part, ctx);
@@ -1155,8 +1176,8 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
                                  int64_t NH, int64_t KV, int64_t D, int64_t page_size, int64_t window, float softcap,
                                  float eps, int32_t append, int64_t lmax, int64_t n_split_max, uint16_t* ctx,
                                  void* ws, int64_t ws_bytes, bool clear_counters, void* stream) {
-  G4MI_REQUIRE(q_raw && q_norm && rope_cos && rope_sin && k_pages && v_pages && page_table && pos && ctx && ws,
-               G4MI_EINVAL, "decode_attention: null pointer argument");
+  G4MI_REQUIRE(q_raw && q_norm && rope_cos && rope_sin && k_pages && v_pages && pos && ctx && ws, G4MI_EINVAL,
+               "decode_attention: null pointer argument");
   G4MI_REQUIRE(!append || (k_raw && k_norm), G4MI_EINVAL, "decode_attention: append needs k_raw and k_norm");
   G4MI_REQUIRE(B >= 1 && B <= 65535 && KV >= 1 && KV <= 65535 && NH >= KV && NH % KV == 0, G4MI_EINVAL,
                "decode_attention: bad B=%lld NH=%lld KV=%lld", (long long)B, (long long)NH, (long long)KV);
@@ -1167,6 +1188,11 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
                "decode_attention: %lld query heads per KV head not in {1,2,4,8}", (long long)G);
   G4MI_REQUIRE(page_size >= 1 && max_pages >= 1 && num_pages >= 1 && lmax >= 1, G4MI_EINVAL,
                "decode_attention: bad page_size/max_pages/num_pages/lmax");
+  // no page table: sequence b owns pages [b * max_pages, (b + 1) * max_pages)
+  const bool dense = page_table == nullptr;
+  G4MI_REQUIRE(!dense || B * max_pages <= num_pages, G4MI_EINVAL,
+               "decode_attention: without a page table the pool needs B * max_pages = %lld pages, has %lld",
+               (long long)(B * max_pages), (long long)num_pages);
   G4MI_REQUIRE(window >= 0, G4MI_EINVAL, "decode_attention: negative window");
   const int64_t span = (window > 0 && window < lmax) ? window : lmax;  // most positions one query attends
   G4MI_REQUIRE(n_split_max >= g4mi_attention_min_splits(span) && n_split_max <= kMaxSplits, G4MI_EINVAL,
@@ -1194,10 +1220,15 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
     hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, w.counters, words);
   }
   dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
-#define G4MI_ATT(DD, GG)                                                                                         \
-  if (D == DD && G == GG)                                                                                        \
-    launch_attn<DD, GG>(a, grid, st, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, \
-                        page_table, pos, append, w, ctx);
+#define G4MI_ATT(DD, GG)                                                                                      \
+  if (D == DD && G == GG) {                                                                                   \
+    if (dense)                                                                                                \
+      launch_attn<DD, GG, true>(a, grid, st, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_pages, \
+                                v_pages, page_table, pos, append, w, ctx);                                    \
+    else                                                                                                      \
+      launch_attn<DD, GG, false>(a, grid, st, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin,         \
+                                 k_pages, v_pages, page_table, pos, append, w, ctx);                          \
+  }
   G4MI_ATT(64, 1) G4MI_ATT(64, 2) G4MI_ATT(64, 4) G4MI_ATT(64, 8)
   G4MI_ATT(128, 1) G4MI_ATT(128, 2) G4MI_ATT(128, 4) G4MI_ATT(128, 8)
   G4MI_ATT(256, 1) G4MI_ATT(256, 2) G4MI_ATT(256, 4) G4MI_ATT(256, 8)

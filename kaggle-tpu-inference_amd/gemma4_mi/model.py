@@ -295,6 +295,7 @@ class DecodeRunner:
         H = cfg.hidden_size
         self.max_len = cache["max_len"]
         self.page_table = cache["page_table"][0:1].contiguous()
+        self._bind_pages(0)
         self.layers = [{k[len(f"layers.{i}."):]: v for k, v in params.items() if k.startswith(f"layers.{i}.")}
                        for i in range(cfg.num_hidden_layers)]
         bf = torch.bfloat16
@@ -374,8 +375,9 @@ class DecodeRunner:
             v = self.qkv[q_rows + k_rows:q_rows + k_rows + v_rows].view(1, kv, d) if v_rows else None
             cos, sin = self.rope[lt]
             ctx = self.ctx[:NH * d].view(1, NH, d)
-            ops.decode_attention(q, k, v, lp["q_norm"], lp["k_norm"], cos, sin, self.cache["k"][i],
-                                 self.cache["v"][i], self.page_table, self.pos,
+            kp, vp = self.kv_pools[i]
+            ops.decode_attention(q, k, v, lp["q_norm"], lp["k_norm"], cos, sin, kp, vp,
+                                 None if self.dense_pages else self.page_table, self.pos,
                                  cfg.sliding_window if lt == SLIDING else 0, cfg.attn_logit_softcapping, eps,
                                  self.max_len, self.splits[lt], append=True, ctx=ctx, ws=self.attn_ws)
             ops.oproj(self.ctx, lp["o_proj"], H, NH * d, self.o)
@@ -434,6 +436,25 @@ class DecodeRunner:
         if not 0 <= b < self.cache["page_table"].shape[0]:
             raise ValueError(f"sequence {b} outside the cache's {self.cache['page_table'].shape[0]} rows")
         self.page_table = self.cache["page_table"][b:b + 1]
+        self._bind_pages(b)
+
+    def _bind_pages(self, b: int) -> None:
+        """The K/V pools the attention kernels see.  When page-table row b is
+        the identity on pages [b * max_pages, (b + 1) * max_pages) (the
+        default cache: every sequence owns its pages in order), the kernels
+        get that slice of each pool and no table, and compute page indices
+        instead of loading them (one dependent memory round trip less per
+        attention kernel).  The row is taken to stay so while bound."""
+        pt = self.cache["page_table"]
+        mp = pt.shape[1]
+        ident = torch.arange(b * mp, (b + 1) * mp, dtype=pt.dtype, device=pt.device)
+        self.dense_pages = bool(torch.equal(pt[b], ident)) and all(
+            k.shape[0] >= (b + 1) * mp for k in self.cache["k"])
+        if self.dense_pages:
+            self.kv_pools = [(k[b * mp:(b + 1) * mp], v[b * mp:(b + 1) * mp])
+                             for k, v in zip(self.cache["k"], self.cache["v"])]
+        else:
+            self.kv_pools = list(zip(self.cache["k"], self.cache["v"]))
 
 
 class PrefillRunner:

@@ -272,8 +272,11 @@ def decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_
     """Split-K decode attention over the paged cache (model.py:197-213) for B
     sequences: q_raw [B, NH, D], k_raw / v_raw [B, KV, D] (v_raw None on k==v
     layers), pages [num_pages, KV, PAGE, D], page_table [B, max_pages],
-    pos [B] int32 (device).  Appends the new K/V at pos when `append`.
-    Returns ctx [B, NH, D] bf16."""
+    pos [B] int32 (device).  page_table None: sequence b owns pages
+    [b * max_pages, (b + 1) * max_pages) of the pool in order, max_pages =
+    num_pages // B (the kernels compute page indices instead of loading
+    them).  Appends the new K/V at pos when `append`.  Returns ctx [B, NH, D]
+    bf16."""
     b, nh, d = q_raw.shape
     num_pages, kv, page, d2 = k_pages.shape
     if d2 != d:
@@ -289,13 +292,16 @@ def decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin, k_
     _need(rope_sin, BF16, "rope_sin", tuple(rope_cos.shape))
     _need(k_pages, BF16, "k_pages")
     _need(v_pages, BF16, "v_pages", tuple(k_pages.shape))
-    _need(page_table, torch.int32, "page_table")
     _need(pos, torch.int32, "pos", (b,))
     if rope_cos.shape[1] != d // 2 or rope_cos.shape[0] < lmax:
         raise ValueError("rope tables must be [>= lmax, head_dim/2]")
-    max_pages = page_table.shape[1]
-    if page_table.shape[0] != b:
-        raise ValueError("page_table must have one row per sequence")
+    if page_table is None:
+        max_pages = num_pages // b
+    else:
+        _need(page_table, torch.int32, "page_table")
+        max_pages = page_table.shape[1]
+        if page_table.shape[0] != b:
+            raise ValueError("page_table must have one row per sequence")
     if n_split_max is None:
         n_split_max = max(attention_min_splits(lmax), 1)
     if ctx is None:
@@ -719,9 +725,11 @@ def decode_attention_noalloc(q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope
     num_pages, kv, page, _ = k_pages.shape
     _need(ctx, BF16, "ctx", (b, nh, d))
     _need(pos, torch.int32, "pos", (b,))
-    _need(page_table, torch.int32, "page_table")
+    if page_table is not None:
+        _need(page_table, torch.int32, "page_table")
+    max_pages = num_pages // b if page_table is None else page_table.shape[1]
     _lib.call("g4mi_decode_attention_noalloc", _ptr(q_raw), _ptr(k_raw), _ptr(v_raw), _ptr(q_norm), _ptr(k_norm),
               _ptr(rope_cos), _ptr(rope_sin), _ptr(k_pages), _ptr(v_pages), num_pages, _ptr(page_table),
-              page_table.shape[1], _ptr(pos), b, nh, kv, d, page, int(window), float(softcap or 0.0), float(eps),
+              max_pages, _ptr(pos), b, nh, kv, d, page, int(window), float(softcap or 0.0), float(eps),
               1 if append else 0, int(lmax), int(n_split_max), _ptr(ctx), stream_handle(q_raw.device))
     return ctx

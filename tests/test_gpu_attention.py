@@ -220,3 +220,54 @@ def test_sliding_and_full_layers_share_one_workspace():
                                        lmax, n_split_max=ns, ws=fresh)
             torch.cuda.synchronize()
             assert torch.equal(got.view(torch.int16), exp.view(torch.int16)), (p, D)
+
+
+@pytest.mark.parametrize("NH,KV,D,lmax,window,positions", [
+    (16, 8, 256, 2048, 1024, [0, 53, 511, 512, 700, 1500]),     # 4-wave kernels
+    (16, 2, 512, 32768, 0, [53, 700, 5000, 32767]),            # 8-wave kernels + split reduction
+])
+def test_dense_page_table_matches_identity_table(NH, KV, D, lmax, window, positions):
+    """page_table = NULL (sequence b owns pages [b*max_pages, (b+1)*max_pages)
+    in order) computes page indices instead of loading them: ctx and the
+    appended K/V rows must be bit-identical to the same call with the
+    identity table, for two sequences at different positions."""
+    B, page, seed, eps = 2, 16, 51, 1e-6
+    max_pages = lmax // page
+    q_raw = _gen((B, NH, D), seed, "q")
+    k_raw = _gen((B, KV, D), seed, "k")
+    v_raw = None if window == 0 else _gen((B, KV, D), seed, "v")
+    q_norm, k_norm = _gen((D,), seed, "q_norm", 0.5), _gen((D,), seed, "k_norm", 0.5)
+    cos, sin = gm.rope_table(D, 1e4, 1.0, lmax, DEV)
+    kp0 = _gen((B * max_pages, KV, page, D), seed, "kp")
+    vp0 = _gen((B * max_pages, KV, page, D), seed, "vp")
+    ident = torch.arange(B * max_pages, dtype=torch.int32, device=DEV).view(B, max_pages)
+    ns = gm.decode_splits(KV, window if window else lmax)
+    for i, p in enumerate(positions):
+        print(f"case D={D} KV={KV} pos={p}", flush=True)
+        pos = torch.tensor([p, positions[(i + 1) % len(positions)]], dtype=torch.int32, device=DEV)
+        out = []
+        for table in (ident, None):
+            kp, vp = kp0.clone(), vp0.clone()
+            ctx = ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, table, pos, window,
+                                       50.0, eps, lmax, n_split_max=ns)
+            torch.cuda.synchronize()
+            out.append((ctx, kp, vp))
+        assert torch.equal(out[0][0].view(torch.int16), out[1][0].view(torch.int16)), f"ctx differs at {p}"
+        assert torch.equal(out[0][1].view(torch.int16), out[1][1].view(torch.int16)), f"K pages differ at {p}"
+        assert torch.equal(out[0][2].view(torch.int16), out[1][2].view(torch.int16)), f"V pages differ at {p}"
+
+
+def test_dense_page_table_needs_enough_pages():
+    q = torch.zeros((2, 4, 64), dtype=torch.bfloat16, device=DEV)
+    kp = torch.zeros((3, 2, 16, 64), dtype=torch.bfloat16, device=DEV)  # 2 sequences x 4 pages need 8
+    cos = torch.zeros((64, 32), dtype=torch.bfloat16, device=DEV)
+    nrm = torch.zeros(64, dtype=torch.bfloat16, device=DEV)
+    pos = torch.zeros(2, dtype=torch.int32, device=DEV)
+    ops_max_pages = 4
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device=DEV)
+    ctx = torch.zeros_like(q)
+    with pytest.raises(RuntimeError, match="without a page table"):
+        ops._lib.call("g4mi_decode_attention", ops._ptr(q), ops._ptr(q[:, :2]), None, ops._ptr(nrm), ops._ptr(nrm),
+                      ops._ptr(cos), ops._ptr(cos), ops._ptr(kp), ops._ptr(kp), 3, None, ops_max_pages,
+                      ops._ptr(pos), 2, 4, 2, 64, 16, 0, 0.0, 1e-6, 1, 64, 1, ops._ptr(ctx), ops._ptr(ws), ws.numel(),
+                      ops.stream_handle(q.device))
