@@ -14,7 +14,9 @@ replayed:
   * "head":  the same layers, lm_head and the sampler (or argmax), the
              token after a prefill (engine.py:60-67);
   * "decode": the layers with the decode path's bf16 running combine
-             (model.py:262-294), lm_head and the sampler (or argmax).
+             (model.py:262-294), lm_head and the sampler (or argmax);
+             below SHORT_SPAN positions a second capture ("decode_short")
+             whose full-attention layers are sized for SHORT_SPAN positions.
 The token, position and the whole token history stay on the device; the
 host only replays graphs and copies each produced token into pinned memory,
 so `lookahead` steps stay queued while it reads the oldest one.
@@ -44,6 +46,10 @@ from .limits import allowed_output_tokens
 from .weights import active_params_per_token, init_random_params, load_params, param_bytes
 
 PREFILL_BUCKET = 256
+# Decode steps at positions below this replay a graph whose full-attention
+# layers are sized for 8,192 positions (64 per split at 128 splits, one K tile
+# per wave); later steps replay the max_len-sized graph.
+SHORT_SPAN = 8192
 
 
 def _round_up(x: int, m: int) -> int:
@@ -91,6 +97,9 @@ class Engine:
         self._graphs: dict[tuple, torch.cuda.CUDAGraph] = {}
         self._stream = torch.cuda.Stream(self.device)
         self._pos_host = 0
+        # below this position the decode step replays a graph whose full
+        # attention layers are sized for it (DecodeRunner.set_full_span)
+        self._short_span = SHORT_SPAN if self.max_len > SHORT_SPAN else 0
         self._host_tok = torch.zeros(self.max_len + 1, dtype=torch.int32, pin_memory=True)
         self._prefill_runner: M.PrefillRunner | None = None
         # positions written per cache row since the last reset_cache()
@@ -113,12 +122,16 @@ class Engine:
         sampler = None if greedy else (self._sp, self.top_k, 0 if kind == "head" else 1)
 
         def step():
-            if kind == "feed":
-                r.launch("f32", advance=True, feed=self._prompt)
-            elif kind == "head":
-                r.launch("f32", advance=True, sampler=sampler)
-            else:
-                r.launch("bf16_running", advance=True, sampler=sampler)
+            r.set_full_span(self._short_span if kind == "decode_short" else None)
+            try:
+                if kind == "feed":
+                    r.launch("f32", advance=True, feed=self._prompt)
+                elif kind == "head":
+                    r.launch("f32", advance=True, sampler=sampler)
+                else:
+                    r.launch("bf16_running", advance=True, sampler=sampler)
+            finally:
+                r.set_full_span(None)
 
         # warm the launch path once outside capture (library load, workspaces),
         # on a scratch position so no cache content the caller relies on changes
@@ -223,7 +236,7 @@ class Engine:
                 r.tok.copy_(r.hist[p:p + 1])
                 r.pos.fill_(p)
             greedy = self._set_sampling(key, temperature, top_p)
-            self._graph("decode", greedy).replay()
+            self._graph("decode_short" if p < self._short_span else "decode", greedy).replay()
             self._pos_host = p + 1
             self._dirty[0] = max(self._dirty[0], p + 1)
             return r.hist[p + 1:p + 2].view(1, 1), cache, torch.tensor(p + 1, dtype=torch.int32)
@@ -273,9 +286,8 @@ class Engine:
         toks = torch.zeros((self.batch, bucket), dtype=torch.int32)
         t0 = time.perf_counter()
         if self.prefill_mode == "batched":
-            # prompts of more than 16 rows run their dense products through the
-            # ROCm library GEMM, which creates its handle and loads its kernel
-            # code objects on first use: do that here, not in the first request
+            # the prefill paths of a short and a full bucket once, so the first
+            # request finds every kernel loaded
             for n in sorted({min(32, bucket), bucket}):
                 self.prefill_fn(bucket)(self.params, toks, self.cache, n, 0, 0.0, 1.0)
         tok, self.cache, pos = self.prefill_fn(bucket)(self.params, toks, self.cache, 4, 0, 0.0, 1.0)
@@ -286,6 +298,8 @@ class Engine:
         t0 = time.perf_counter()
         tok, self.cache, pos = self.decode_fn()(self.params, tok, self.cache, pos, 0, 0.0, 1.0)
         self._graph("decode", False)
+        if self._short_span:
+            self._graph("decode_short", False)
         torch.cuda.synchronize(self.device)
         out["decode_compile_s"] = time.perf_counter() - t0
         n = 8

@@ -335,6 +335,8 @@ class DecodeRunner:
             self.splits[lt] = ns
             ws = max(ws, ops._lib.lib().g4mi_decode_attention_workspace_bytes(1, cfg.num_attention_heads, d, lmax, ns))
         self.attn_ws = torch.zeros(ws, dtype=torch.uint8, device=dev)
+        # positions the full layers' attention is launched for (see set_full_span)
+        self.full_span = self.max_len
         self.sample_ws = torch.zeros(ops.sample_workspace_bytes(cfg.vocab_size), dtype=torch.uint8, device=dev)
         self.ffn_ws = torch.zeros(int(ops._lib.lib().g4mi_ffn_in_workspace_bytes()), dtype=torch.uint8, device=dev)
 
@@ -342,6 +344,19 @@ class DecodeRunner:
         cfg = self.cfg
         span = min(cfg.sliding_window, self.max_len) if lt == SLIDING else self.max_len
         return decode_splits(cfg.kv_heads_for(lt), span)
+
+    def set_full_span(self, span: int | None = None) -> None:
+        """Steps launched from now on size the full-attention layers for
+        positions below `span` (None: max_len).  A span up to 64 positions
+        per split (8,192 at 128 splits) runs the attention kernels that take
+        one K tile per wave; the full 32K span needs the long-range kernels
+        and their split reduction.  A step at a position >= span attends to
+        nothing on those layers, so a caller that captures a step with a
+        short span replays it only below that position."""
+        span = self.max_len if span is None else int(span)
+        if not 1 <= span <= self.max_len:
+            raise ValueError(f"span {span} outside [1, {self.max_len}]")
+        self.full_span = span
 
     def launch(self, combine: str = "bf16_running", advance: bool = True, sampler=None, feed=None):
         """Enqueues one token step reading tok/pos.
@@ -376,10 +391,14 @@ class DecodeRunner:
             cos, sin = self.rope[lt]
             ctx = self.ctx[:NH * d].view(1, NH, d)
             kp, vp = self.kv_pools[i]
+            if lt == SLIDING or self.full_span == self.max_len:
+                lmax, ns = self.max_len, self.splits[lt]
+            else:
+                lmax, ns = self.full_span, decode_splits(kv, self.full_span)
             ops.decode_attention(q, k, v, lp["q_norm"], lp["k_norm"], cos, sin, kp, vp,
                                  None if self.dense_pages else self.page_table, self.pos,
                                  cfg.sliding_window if lt == SLIDING else 0, cfg.attn_logit_softcapping, eps,
-                                 self.max_len, self.splits[lt], append=True, ctx=ctx, ws=self.attn_ws)
+                                 lmax, ns, append=True, ctx=ctx, ws=self.attn_ws)
             ops.oproj(self.ctx, lp["o_proj"], H, NH * d, self.o)
             ops.ffn_in(self.x, self.o, lp["post_attention_layernorm"], lp["pre_feedforward_layernorm"],
                        lp.get("pre_feedforward_layernorm_2"), self.x1, self.xe, lp["mlp.gate_proj"],

@@ -164,3 +164,57 @@ def test_sampler_greedy_cases_and_ties():
     assert (_draws(logits, 1.0, 1e-9, 64, 3) == am).all()           # nucleus keeps only the first
     two = _draws(logits, 1.0, 1.0, 2, 400)
     assert set(np.unique(two)) == {12345, 54321}                      # the tie pair, nothing else
+
+
+def test_decode_crosses_the_short_span_graph_boundary():
+    """Below SHORT_SPAN the engine replays a decode graph whose full-attention
+    layers are sized for SHORT_SPAN positions (the kernels that take one K
+    tile per wave); from SHORT_SPAN on, the max_len-sized graph.  Decoding
+    8 steps across the boundary from a prefilled 8,187-token context must
+    give, step for step, the greedy tokens and logits of the same steps
+    replayed with the max_len-sized graph only: the two attention
+    configurations differ only in their f32 summation order (logits within
+    2^-8 of their largest magnitude, corr >= 0.99999)."""
+    from gemma4_mi.engine import SHORT_SPAN
+    cfg = tiny_parity_config()
+    max_len, n0, steps = 2 * SHORT_SPAN, SHORT_SPAN - 5, 8
+    eng = Engine.random(cfg, seed=1, max_len=max_len, top_k=64, device=DEV)
+    r = eng._runner
+    prompt = torch.as_tensor(np.random.default_rng(1).integers(0, cfg.vocab_size, size=(1, n0)), dtype=torch.int32)
+    tok, cache, pos = eng.prefill_fn(n0)(eng.params, prompt, eng.cache, n0, 0, 0.0, 1.0)
+    torch.cuda.synchronize()
+    saved = ([t.clone() for t in cache["k"] + cache["v"]], r.tok.clone(), r.pos.clone(), r.hist.clone())
+
+    def run(force_full):
+        for t, s in zip(cache["k"] + cache["v"], saved[0]):
+            t.copy_(s)
+        r.tok.copy_(saved[1]); r.pos.copy_(saved[2]); r.hist.copy_(saved[3])
+        eng._pos_host = n0
+        dec = eng.decode_fn()
+        t, p = r.hist[n0:n0 + 1].view(1, 1), torch.tensor(n0, dtype=torch.int32)
+        toks, logits = [], []
+        for i in range(steps):
+            if force_full:
+                eng._graph("decode", True).replay()
+                p = torch.tensor(n0 + i + 1, dtype=torch.int32)
+                eng._pos_host = n0 + i + 1
+            else:
+                t, cache_, p = dec(eng.params, t, cache, p, 0, 0.0, 1.0)
+            torch.cuda.synchronize()
+            toks.append(int(r.hist[n0 + i + 1].item()))
+            logits.append(r.logits.clone())
+        return toks, logits
+
+    toks_a, log_a = run(False)
+    assert ("decode_short", True) in eng._graphs and ("decode", True) in eng._graphs
+    toks_b, log_b = run(True)
+    for i in range(steps):
+        a, b = log_a[i].double(), log_b[i].double()
+        scale = b.abs().max().item()
+        err = (a - b).abs().max().item()
+        corr = float(np.corrcoef(a.cpu().numpy(), b.cpu().numpy())[0, 1])
+        print(f"step at position {n0 + i}: max|d|={err:.3e} scale={scale:.3e} corr={corr:.7f}")
+        assert err <= scale * 2.0 ** -8 and corr >= 0.99999, f"logits differ at position {n0 + i}"
+        if toks_a[i] != toks_b[i]:  # only a near-tie may flip the greedy token
+            top2 = torch.topk(b, 2).values
+            assert (top2[0] - top2[1]).item() <= 2 * err, f"greedy token differs at position {n0 + i}"
