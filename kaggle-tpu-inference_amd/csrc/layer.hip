@@ -354,7 +354,10 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
 // One wave per output row h (kOutRows rows per block): the dense down row
 // (I values, 64 lanes) and the k selected experts' down rows (8 lanes per
 // expert slot, FIT = F/64 chunks).
-constexpr int kOutThreads = 256;
+// 11 waves per block: the 26B layer's 2,816 rows are then one block on every
+// one of the 256 CUs (4-row blocks left 192 CUs with 3 blocks and 64 with 2,
+// and the kernel ended with the 3-block CUs).
+constexpr int kOutThreads = 704;
 constexpr int kOutRows = kOutThreads / 64;
 struct FfnOutArgs {
   const uint16_t* act_mlp;  // [I]
@@ -381,36 +384,39 @@ template <int FIT>
 __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
   constexpr int F = FIT * 64;
   constexpr int NT = kOutThreads;
-  extern __shared__ u32x4 act_lds[];  // I/8 chunks
+  extern __shared__ u32x4 act_lds[];  // I/8 chunks of act_mlp, then K * F/8 of act_moe
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int h = blockIdx.x * kOutRows + wave;
   const int ich = a.I / 8;
   constexpr int DIT = 8;  // dense chunks per lane, at most (I <= 4096)
+  const int dit = (ich + 63) / 64;  // of which this I needs
   const bool hv = h < a.H;
   const int hc = min(h, a.H - 1);
   const int g = lane >> 3, l8 = lane & 7;
   // small operands first (issue order = completion order for vmcnt): the
   // routed expert of this lane group and this thread's share of act_mlp
   const int ei = (a.e_down != nullptr) ? a.top_i[min(g, a.K - 1)] : -1;
-  constexpr int ACT_PER = 4096 / 8 / NT;  // act_mlp chunks per thread: I <= 4096
+  constexpr int ACT_PER = (4096 / 8 + NT - 1) / NT;  // act_mlp chunks per thread: I <= 4096
   u32x4 av[ACT_PER];
 #pragma unroll
   for (int j = 0; j < ACT_PER; ++j) av[j] = ld16((const u32x4*)a.act_mlp + min(tid + NT * j, ich - 1));
-  // weight rows, unconditional with clamped addresses
+  // the routed experts' activations (K * F/8 chunks, written by the previous
+  // kernel) are staged in LDS once per block like act_mlp: loaded per wave
+  // they took as many vector memory slots as the expert rows
+  constexpr int MOE_PER = (8 * F / 8 + NT - 1) / NT;  // act_moe chunks per thread: K <= 8
+  const int mch = (a.act_moe != nullptr) ? a.K * (F / 8) : 0;
+  u32x4 avm[MOE_PER];
+#pragma unroll
+  for (int j = 0; j < MOE_PER; ++j)
+    avm[j] = ld16((const u32x4*)(a.act_moe != nullptr ? a.act_moe : a.act_mlp) + min(tid + NT * j, max(mch, 1) - 1));
+  // weight rows, unconditional with clamped addresses (the dense row: only
+  // the chunks this I has)
   u32x4 wd[DIT];
   {
     const u32x4* drow = (const u32x4*)(a.down + (size_t)hc * a.I);
 #pragma unroll
-    for (int i = 0; i < DIT; ++i) wd[i] = ld_stream(drow + min(lane + 64 * i, ich - 1));
-  }
-  // this lane group's slot activations (written by the previous kernel):
-  // requested with the weight rows, not after them
-  u32x4 am[FIT];
-  {
-    const u32x4* avm = (const u32x4*)((a.act_moe != nullptr ? a.act_moe : a.act_mlp) +
-                                      (size_t)(a.act_moe != nullptr ? min(g, max(a.K, 1) - 1) : 0) * F);
-#pragma unroll
-    for (int i = 0; i < FIT; ++i) am[i] = ld16(avm + (a.act_moe != nullptr ? l8 + 8 * i : 0));
+    for (int i = 0; i < DIT; ++i)
+      if (i < dit) wd[i] = ld_stream(drow + min(lane + 64 * i, ich - 1));
   }
   const int e = (g < a.K && ei >= 0 && ei < a.E) ? ei : -1;
   u32x4 we[FIT];
@@ -422,7 +428,10 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
 #pragma unroll
   for (int j = 0; j < ACT_PER; ++j)
     if (tid + NT * j < ich) act_lds[tid + NT * j] = av[j];
-  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < MOE_PER; ++j)
+    if (tid + NT * j < mch) act_lds[ich + tid + NT * j] = avm[j];
+  lds_barrier();
   if (hv) {  // wave-uniform
     float acc = 0.0f;
 #pragma unroll
@@ -435,8 +444,9 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
     if (a.e_down != nullptr) {
       float part = 0.0f;
       if (e >= 0) {
+        const u32x4* am = act_lds + ich + g * (F / 8);  // this lane group's slot (e >= 0: g < K)
 #pragma unroll
-        for (int i = 0; i < FIT; ++i) part = dot8(we[i], am[i], part);
+        for (int i = 0; i < FIT; ++i) part = dot8(we[i], am[l8 + 8 * i], part);
       }
       part = group_sum<8>(part);
       float run = 0.0f;
@@ -753,7 +763,8 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
 }
 
 int64_t g4mi_ffn_out_workspace_bytes(void) {
-  return 4 * kArriveStride * (1 + (1024 + kArriveGroup - 1) / kArriveGroup);  // grid <= 1024 blocks (H <= 4096)
+  // arrival counters of a grid of up to 4096 blocks (H <= 4096 rows, kOutRows per block)
+  return 4 * kArriveStride * (1 + (4096 / kOutRows + kArriveGroup - 1) / kArriveGroup);
 }
 
 int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint16_t* mlp_out,
@@ -785,7 +796,7 @@ int g4mi_ffn_out(const uint16_t* act_mlp, const uint16_t* down, int64_t I, uint1
   a.tail = TailArgs{x1, mlp_out, moe_out, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
   a.w_next = next_ln; a.x_out = x_out; a.xn_out = xn_out; a.counter = (unsigned int*)ws; a.eps = eps;
   dim3 grid((unsigned)((H + kOutRows - 1) / kOutRows));
-  const size_t lds = (size_t)(I / 8) * 16;
+  const size_t lds = (size_t)(I / 8 + (experts_down ? k * (F / 8) : 0)) * 16;
   hipStream_t st = as_stream(stream);
   const int fit = experts_down ? (int)(F / 64) : 1;
   switch (fit) {

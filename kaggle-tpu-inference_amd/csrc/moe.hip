@@ -407,7 +407,9 @@ static void launch_scores(const uint16_t* x, const uint16_t* pre_w, const uint16
 
 static void launch_gateup(int it, const uint16_t* x, const uint16_t* gu, const float* scores, const uint16_t* pes,
                           float* tw, int32_t* ti, int N, int F, int E, int K, uint16_t* act, hipStream_t st) {
-  const int waves = 4;
+  // the in-block selection needs 4 waves; with the routing given, 2-wave
+  // blocks spread the 8 x 704 tasks of a 26B token evenly (11 blocks per CU)
+  const int waves = (scores != nullptr) ? 4 : 2;
   dim3 grid((unsigned)((K * F + waves - 1) / waves), (unsigned)N);
   switch (it) {
 #define G4MI_CASE(I)                                                                                           \

@@ -14,7 +14,7 @@ namespace g4mi {
 // adds nothing to a sum of squares); only stores are masked.
 template <int NT>
 struct VecT {
-  static constexpr int NC = 512 / NT;
+  static constexpr int NC = (512 + NT - 1) / NT;
   u32x4 c[NC];
 };
 using Vec = VecT<256>;
