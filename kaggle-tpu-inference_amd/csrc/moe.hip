@@ -177,14 +177,18 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
     const uint16_t* __restrict__ pes, float* __restrict__ top_w, int32_t* __restrict__ top_i, int F, int E, int K,
     uint16_t* __restrict__ act) {
   constexpr int H = IT * 256;
+  constexpr int XPT = (H / 8 + 127) / 128;  // x chunks per thread (blocks of >= 128 threads)
   __shared__ SelectLds L;
+  __shared__ u32x4 xs[H / 8];
   const int lane = threadIdx.x & 63, half = lane >> 5, l = lane & 31;
   const int task = blockIdx.x * (blockDim.x >> 6) + wave_id();
   const int n = blockIdx.y;
+  // x is staged in LDS once per block: each wave loading it itself took as
+  // many vector memory slots as its expert rows
   const u32x4* xv = (const u32x4*)(x + (size_t)n * H);
-  u32x4 xr[IT];
+  u32x4 xr[XPT];
 #pragma unroll
-  for (int i = 0; i < IT; ++i) xr[i] = ld16(xv + l + 32 * i);
+  for (int j = 0; j < XPT; ++j) xr[j] = ld16(xv + min((int)threadIdx.x + (int)blockDim.x * j, H / 8 - 1));
   if (scores != nullptr) {
     block_select(scores + (size_t)n * E, pes, E, K, L);
     if (blockIdx.x == 0 && threadIdx.x < K) {
@@ -200,9 +204,13 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   u32x4 w[IT];
 #pragma unroll
   for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 32 * i);
+#pragma unroll
+  for (int j = 0; j < XPT; ++j)
+    if ((int)threadIdx.x + (int)blockDim.x * j < H / 8) xs[threadIdx.x + blockDim.x * j] = xr[j];
+  lds_barrier();
   float acc = 0.0f;
 #pragma unroll
-  for (int i = 0; i < IT; ++i) acc = dot8(w[i], xr[i], acc);
+  for (int i = 0; i < IT; ++i) acc = dot8(w[i], xs[l + 32 * i], acc);
   acc = group_sum<32>(acc);
   const float up = __shfl(acc, 32, kWave);
   if (lane == 0 && task < K * F) {
@@ -220,29 +228,49 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
 // beyond 8 take further passes.  Combine:
 //   bf16_running = 1: bf16 running sum of bf16(part) in slot order (model.py:289-293)
 //   bf16_running = 0: bf16 of the f32 sum of parts (the dense contraction, model.py:250)
+// The token's K * F activations are staged in LDS once per block (each wave
+// loading them itself took as many vector memory slots as its expert rows),
+// and a block is kDownWaves rows: the 26B layer's 2,816 rows are then one
+// block per CU.
+constexpr int kDownWaves = 11;
+
 template <int IT>
-__global__ __launch_bounds__(256) void moe_down_kernel(
+__global__ __launch_bounds__(64 * kDownWaves) void moe_down_kernel(
     const uint16_t* __restrict__ act, const uint16_t* __restrict__ down, const int32_t* __restrict__ top_i,
     int H, int E, int K, int bf16_running, uint16_t* __restrict__ out) {
   constexpr int F = IT * 64;
-  const int lane = threadIdx.x & 63, g = lane >> 3, l = lane & 7;
-  const int h = blockIdx.x * (blockDim.x >> 6) + wave_id();
+  constexpr int NT = 64 * kDownWaves;
+  extern __shared__ u32x4 act_lds[];  // K * F/8 chunks of token n
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 3, l = lane & 7;
+  const int h = blockIdx.x * kDownWaves + wave_id();
   const int n = blockIdx.y;
-  if (h >= H) return;
+  const int hc = min(h, H - 1);
+  const int mch = K * (F / 8);
+  const u32x4* actn = (const u32x4*)(act + (size_t)n * K * F);
+  // the first 8 slots' experts and this thread's first activation chunk,
+  // then the rows, then the staging store
+  const int e0 = (g < K) ? top_i[n * K + g] : -1;
+  const u32x4 a0 = ld16(actn + min(tid, mch - 1));
   float run = 0.0f;
   bool first = true;
   for (int s0 = 0; s0 < K; s0 += 8) {
     const int slot = s0 + g;
+    const int e = (s0 == 0) ? e0 : ((slot < K) ? top_i[n * K + slot] : -1);
+    const bool ok = slot < K && e >= 0 && e < E;
+    const u32x4* row = (const u32x4*)(down + ((size_t)(ok ? e : 0) * H + hc) * F);
+    u32x4 w[IT];
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 8 * i);
+    if (s0 == 0) {
+      if (tid < mch) act_lds[tid] = a0;
+      for (int c = tid + NT; c < mch; c += NT) act_lds[c] = ld16(actn + c);
+      lds_barrier();
+    }
     float part = 0.0f;
-    const int e = (slot < K) ? top_i[n * K + slot] : -1;
-    if (e >= 0 && e < E) {
-      const u32x4* row = (const u32x4*)(down + ((size_t)e * H + h) * F);
-      const u32x4* av = (const u32x4*)(act + ((size_t)n * K + slot) * F);
-      u32x4 w[IT];
+    if (ok) {
+      const u32x4* av = act_lds + slot * (F / 8);
 #pragma unroll
-      for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 8 * i);
-#pragma unroll
-      for (int i = 0; i < IT; ++i) part = dot8(w[i], ld16(av + l + 8 * i), part);
+      for (int i = 0; i < IT; ++i) part = dot8(w[i], av[l + 8 * i], part);
     }
     part = group_sum<8>(part);
     const int cnt = min(8, K - s0);
@@ -257,7 +285,7 @@ __global__ __launch_bounds__(256) void moe_down_kernel(
       first = false;
     }
   }
-  if (lane == 0) out[(size_t)n * H + h] = f2bf(run);
+  if (lane == 0 && h < H) out[(size_t)n * H + h] = f2bf(run);
 }
 
 // ------------------------------------------------------------------ launchers
@@ -424,12 +452,13 @@ static void launch_gateup(int it, const uint16_t* x, const uint16_t* gu, const f
 
 static void launch_down(int it, const uint16_t* act, const uint16_t* dn, const int32_t* ti, int N, int H, int E,
                         int K, int running, uint16_t* out, hipStream_t st) {
-  const int waves = 4;
-  dim3 grid((unsigned)((H + waves - 1) / waves), (unsigned)N);
+  dim3 grid((unsigned)((H + kDownWaves - 1) / kDownWaves), (unsigned)N);
+  const size_t lds = (size_t)K * it * 64 * 2;  // K * F bf16 activations
   switch (it) {
-#define G4MI_CASE(I)                                                                                               \
-  case I:                                                                                                          \
-    hipLaunchKernelGGL(moe_down_kernel<I>, grid, dim3(64 * waves), 0, st, act, dn, ti, H, E, K, running, out); \
+#define G4MI_CASE(I)                                                                                         \
+  case I:                                                                                                    \
+    hipLaunchKernelGGL(moe_down_kernel<I>, grid, dim3(64 * kDownWaves), lds, st, act, dn, ti, H, E, K, running, \
+                       out);                                                                                 \
     return;
     G4MI_IT_CASES(G4MI_CASE)
 #undef G4MI_CASE
