@@ -218,7 +218,7 @@ def run_moe_block(args) -> dict:
     gu_us = _time_graph(g_gu, max(1, args.steps // G)) / (max(1, args.steps // G) * G) * 1e3
     achieved = wl.gateup_bytes() / (gu_us * 1e-6) / 1e9
     res = {
-        "metric": METRIC,
+        "metric": f"isolated MoE decode block tok/s (26B-A4B experts, batch {args.batch})",
         "value": args.batch / (ms * 1e-3),
         "unit": "tok/s",
         "ms_per_step": ms,
@@ -324,9 +324,11 @@ def run_attention(args) -> dict:
         "config": {"workload": "isolated decode attention at position 32767, softcap 50, seed 2, "
                                "caches rotated per launch (>= 512 MiB)", **out, "launch": "HIP graph"},
         "roofline": {
-            "kernel": "attn_qk + attn_pv (full layer, 32K positions)", "bound": "hbm", "achieved": full["gbs"],
+            "kernel": "attn_qk + attn_pv + attn_reduce (full layer, 32K positions)", "bound": "hbm",
+            "achieved": full["gbs"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": full["gbs"] / HBM_PEAK_GBS,
-            "traffic": _measured_traffic("attn_qk_kernel+attn_pv_kernel<512>", "attention_32k_traffic.txt"),
+            "traffic": _measured_traffic("attn_qk_kernel+attn_pv_kernel+attn_reduce_kernel<512>",
+                                         "attention_32k_traffic.txt"),
             "bytes_per_launch": full["bytes_per_launch"], "avg_launch_us": full["us_per_launch"],
         },
     }
