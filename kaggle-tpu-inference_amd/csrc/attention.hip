@@ -173,9 +173,10 @@ __device__ __forceinline__ void norm_rope_slice(float* x, const float* w, const 
 // 16-position tiles w, w+4, ... of the split; the next tile's K loads are in
 // flight while the current one is multiplied.  ONE: the launch guarantees
 // at most kChunkMin positions per split (one tile per wave), so there is
-// nothing to prefetch.  NW = 8 (long ranges): 8 waves, and every tile a wave
-// owns (tiles w and w + 8 of a split's 16 at most) is requested before the
-// prologue, so a whole split's K rows are in flight at once.
+// nothing to prefetch.  NW = 8 (long ranges): 8 waves, each owning tiles w
+// and w + 8 of a split's 16 at most, all requested by the end of the q
+// prologue (part of the first before it, see KS0), so a whole split's K rows
+// are in flight at once.
 template <int D, int G, bool ONE, int NW, bool DPT>
 __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
     AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
@@ -263,8 +264,10 @@ __global__ __launch_bounds__(NW * 64) void attn_qk_kernel(
   // On the 8-wave path only the first KS0 chunks of each wave's first tile
   // are requested before the prologue, the rest after it: a CU queues only so
   // many vector memory instructions, and a wave that requested its whole
-  // tiles up front would stall at issue with the prologue behind them.
-  constexpr int KS0 = (NW == 8 && KS > 4) ? 4 : KS;
+  // tiles up front would stall at issue with the prologue behind them (8 of
+  // the 16 chunks at head_dim 512: the full 32K layer 41.1 -> 40.2 us against
+  // 4, no better with 16).
+  constexpr int KS0 = (NW == 8 && KS > 8) ? 8 : KS;
   load_chunks(0, 0, KS0);
   // padding rows G..15 of the A operand are zero
   for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
@@ -606,8 +609,8 @@ __device__ __forceinline__ void pv_short(const AttnDims& a, const Range& R, int 
 // pv_long8: the long-range body for 8 waves (NW = 8).  Wave w owns the
 // head dims [w*D/8, (w+1)*D/8): DW/8 lanes per position, PPV positions per
 // wave step, at most kChunkMax / PPV steps per split.  The V row slices of
-// the first 4 steps are requested before the split statistics are merged,
-// those of the next kPvRing - 4 once the probabilities are in LDS; then the
+// the first 8 steps are requested before the split statistics are merged,
+// those of the next kPvRing - 8 once the probabilities are in LDS; then the
 // pairs of steps are dotted with the bf16 probabilities as in the 4-wave
 // body, each consumed pair's registers refilled with the pair kPvRing steps
 // ahead.  (A CU queues only so many vector memory instructions: a wave that
@@ -630,7 +633,7 @@ __device__ __forceinline__ void pv_long8(const AttnDims& a, const Range& R, int 
   constexpr int PPV = 64 / LPV;                 // positions per wave step
   constexpr int MAXST = kChunkMax / PPV;        // steps per split at most
   constexpr int RB = kPvRing < MAXST ? kPvRing : MAXST;  // steps in flight
-  constexpr int RB0 = RB < 4 ? RB : 4;                   // of which requested before the merge
+  constexpr int RB0 = RB < 8 ? RB : 8;                   // of which requested before the merge
   constexpr int RS = (G * kChunkMax + NT - 1) / NT;  // scores per thread
   static_assert(D % (NW * 8) == 0 && MAXST % 2 == 0 && RB % 2 == 0, "pv_long8 layout");
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
