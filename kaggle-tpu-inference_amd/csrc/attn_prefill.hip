@@ -16,6 +16,10 @@
 // (the K/V tiles are shared by the group), 4 waves of 16 rows.  Key blocks of
 // KB keys (one page slice) are staged in LDS: K as [key][D] (the B operand of
 // Q.K^T reads 16-byte rows), V transposed to [D][key] (the B operand of P.V).
+// The next key block's K/V rows are requested into registers while the
+// current one is multiplied (LDS-only barriers, so they stay in flight), and
+// the block's page-table entries are staged in LDS once, so no step waits on
+// a page-table load.
 // v_mfma_f32_16x16x32_bf16: lane l holds A[l%16][8(l/16)..+7],
 // B[l%16][8(l/16)..+7] and receives C[4(l/16)+i][l%16].
 #include <math.h>
@@ -26,6 +30,7 @@
 namespace g4mi {
 
 constexpr int kPfRows = 64;  // query rows per block
+constexpr int kPfPtl = 256;  // page-table entries of a block staged in LDS (later pages are loaded directly)
 
 struct PfAttnArgs {
   const uint16_t* q;        // [T, NH, D] normalised + rotated
@@ -106,6 +111,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
   __shared__ __align__(16) uint16_t kt[KB * LDK];
   __shared__ __align__(16) uint16_t vt[D * LDV];
   __shared__ __align__(16) uint16_t pt[kPfRows * LDP];
+  __shared__ int ptl[kPfPtl];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int kv = blockIdx.y;
   const int nqb = (a.T + QP - 1) / QP;
@@ -138,27 +144,52 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
   const int kb0 = k_lo / KB, kb1 = pos_last / KB;
   const float cap = a.softcap;
 
-  // K (and V) tile of key block kb into LDS; invalid pages read as zero
-  auto stage = [&](int kb, bool with_v) {
+  // the block's page-table entries, staged once (a barrier follows before use)
+  const int first_pg = (kb0 * KB) / a.page;
+  for (int i = tid; i < kPfPtl; i += 256) ptl[i] = a.pt[min(first_pg + i, a.max_pages - 1)];
+  auto page_of = [&](int kb) {
+    const int idx = (kb * KB) / a.page - first_pg;
+    return (idx < kPfPtl) ? ptl[idx] : a.pt[min(first_pg + idx, a.max_pages - 1)];
+  };
+  // K (and V) rows of key block kb into registers (fetch), then into LDS
+  // (put); invalid pages read as zero.  The loads are unconditional (page 0
+  // stands in for an invalid entry) and the zero is selected afterwards.
+  constexpr int CPT = KB * D / 8 / 256;  // 16-byte chunks per thread and tile
+  static_assert(CPT * 256 * 8 == KB * D, "tile chunks");
+  struct Tile {
+    u32x4 k[CPT], v[CPT];
+    bool ok;
+  };
+  auto fetch = [&](int kb, bool with_v, Tile& T) {
     const int k0 = kb * KB;
-    const int pg = a.pt[min(k0 / a.page, a.max_pages - 1)];
-    const bool ok = pg >= 0 && pg < a.num_pages;
-    const size_t base = (((size_t)max(pg, 0) * a.KV + kv) * a.page + (k0 % a.page)) * D;
-    constexpr int CH = KB * D / 8;  // 16-byte chunks per tile
-    // K: lanes walk a key row (coalesced loads, conflict-free 16-byte stores)
+    const int pg = page_of(kb);
+    T.ok = pg >= 0 && pg < a.num_pages;
+    const size_t base = (((size_t)(T.ok ? pg : 0) * a.KV + kv) * a.page + (k0 % a.page)) * D;
 #pragma unroll
-    for (int c = tid; c < CH; c += 256) {
-      const int j = c / (D / 8), d0 = (c % (D / 8)) * 8;
-      const u32x4 kv4 = ok ? ld16((const u32x4*)(a.k_pages + base) + c) : u32x4{0u, 0u, 0u, 0u};
-      *(u32x4*)(kt + j * LDK + d0) = kv4;
+    for (int i = 0; i < CPT; ++i) T.k[i] = ld16((const u32x4*)(a.k_pages + base) + tid + 256 * i);
+    if (with_v) {
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + 256 * i, j = c % KB, d0 = (c / KB) * 8;
+        T.v[i] = ld16((const u32x4*)(a.v_pages + base + (size_t)j * D + d0));
+      }
+    }
+  };
+  auto put = [&](const Tile& T, bool with_v) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+    // K: lanes walk a key row (conflict-free 16-byte stores)
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + 256 * i, j = c / (D / 8), d0 = (c % (D / 8)) * 8;
+      *(u32x4*)(kt + j * LDK + d0) = T.ok ? T.k[i] : z;
     }
     // V transposed: lanes walk the keys of one 8-value column group, so the
     // 2-byte LDS stores of a wave land in consecutive halfwords
     if (with_v) {
 #pragma unroll
-      for (int c = tid; c < CH; c += 256) {
-        const int j = c % KB, d0 = (c / KB) * 8;
-        const u32x4 v4 = ok ? ld16((const u32x4*)(a.v_pages + base + (size_t)j * D + d0)) : u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < CPT; ++i) {
+        const int c = tid + 256 * i, j = c % KB, d0 = (c / KB) * 8;
+        const u32x4 v4 = T.ok ? T.v[i] : z;
         const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -191,19 +222,29 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
     }
   };
 
-  // ---- pass 1: row max and sum of exp
+  // Pass 1 (row max and sum of exp), then pass 2 (p = bf16(exp(s - m) / l),
+  // O += P . V), each step's K/V rows requested one step ahead (pass 2's
+  // first tile during pass 1's last step).  Step q < n is pass 1 over key
+  // block kb0 + q, step n + q pass 2 over the same block.  (Two tiles in
+  // flight at head_dim 512 spilled registers and ran slower: 459 against
+  // 441 us per full layer of a 2,048-token prompt.)
+  const int n = kb1 - kb0 + 1;
+  auto target = [&](int q, Tile& T) {  // request step q's rows (no-op past the last step)
+    if (q < 2 * n) fetch(kb0 + (q < n ? q : q - n), q >= n, T);
+  };
   float m[4], l[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     m[i] = -INFINITY;
     l[i] = 0.0f;
   }
-  for (int kb = kb0; kb <= kb1; ++kb) {
-    __syncthreads();
-    stage(kb, false);
-    __syncthreads();
+  auto step1 = [&](int q, Tile& T) {
+    lds_barrier();
+    put(T, false);
+    target(q + 1, T);
+    lds_barrier();
     float s[NT][4];
-    scores(kb, s);
+    scores(kb0 + q, s);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float bm = s[0][i];
@@ -220,25 +261,29 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
       l[i] = (m[i] == -INFINITY) ? e : l[i] * expf(m[i] - mn) + e;
       m[i] = mn;
     }
-  }
+  };
+  Tile tile;
+  lds_barrier();  // ptl
+  target(0, tile);
+  for (int q = 0; q < n; ++q) step1(q, tile);
 
-  // ---- pass 2: p = bf16(exp(s - m) / l), O += P . V
   f32x4 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   uint16_t* pw = pt + 16 * wave * LDP;  // this wave's 16 rows of P
-  for (int kb = kb0; kb <= kb1; ++kb) {
-    __syncthreads();
-    stage(kb, true);
-    __syncthreads();
+  auto step2 = [&](int q, Tile& T) {
+    lds_barrier();
+    put(T, true);
+    target(n + q + 1, T);
+    lds_barrier();
     float s[NT][4];
-    scores(kb, s);
+    scores(kb0 + q, s);
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+    for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = (s[n][i] == -INFINITY || !(l[i] > 0.0f)) ? 0.0f : rbf(expf(s[n][i] - m[i]) / l[i]);
-        pw[(4 * (lane >> 4) + i) * LDP + 16 * n + fr] = f2bf(p);
+        const float p = (s[nn][i] == -INFINITY || !(l[i] > 0.0f)) ? 0.0f : rbf(expf(s[nn][i] - m[i]) / l[i]);
+        pw[(4 * (lane >> 4) + i) * LDP + 16 * nn + fr] = f2bf(p);
       }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -253,7 +298,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
                                                         __builtin_bit_cast(bf16x8, vb), o[dt], 0, 0, 0);
       }
     }
-  }
+  };
+  for (int q = 0; q < n; ++q) step2(q, tile);
 
   // ---- ctx = bf16(O): row 4(l/16)+i of the wave, d = 16*dt + l%16
 #pragma unroll
