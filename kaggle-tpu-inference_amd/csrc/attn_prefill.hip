@@ -12,8 +12,12 @@
 // l) -- exactly the bf16 operand the reference's PV product takes -- and
 // accumulates P . V on MFMA.
 //
-// Block: 64 query rows = 64/G positions x the G query heads of one KV head
-// (the K/V tiles are shared by the group), 4 waves of 16 rows.  Key blocks of
+// Block: 16 * NW query rows = 16 * NW / G positions x the G query heads of
+// one KV head (the K/V tiles are shared by the group), NW waves of 16 rows:
+// 8 waves up to head_dim 256 (each staged K/V tile then serves 128 rows: the
+// kernel is bound by the K/V rows each CU loads from the caches), 4 at 512
+// (a wave holds 16 x 512 accumulators and the Q fragments: one wave per SIMD
+// fits).  Key blocks of
 // KB keys (one page slice) are staged in LDS: K as [key][D] (the B operand of
 // Q.K^T reads 16-byte rows), V transposed to [D][key] (the B operand of P.V).
 // The next key block's K/V rows are requested into registers while the
@@ -29,7 +33,11 @@
 
 namespace g4mi {
 
-constexpr int kPfRows = 64;  // query rows per block
+// waves (of 16 query rows) per block
+template <int D>
+constexpr int pf_waves() {
+  return D >= 512 ? 4 : 8;
+}
 constexpr int kPfPtl = 256;  // page-table entries of a block staged in LDS (later pages are loaded directly)
 
 struct PfAttnArgs {
@@ -99,9 +107,12 @@ __device__ __forceinline__ float row16_sum(float v) {
 }
 
 template <int D, int G>
-__global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
+__global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttnArgs a) {
+  constexpr int NW = pf_waves<D>();
+  constexpr int NTH = 64 * NW;              // threads
+  constexpr int ROWS = 16 * NW;             // query rows per block
   constexpr int KB = (D >= 512) ? 32 : 64;  // keys per block step (divides the page)
-  constexpr int QP = kPfRows / G;           // positions per block
+  constexpr int QP = ROWS / G;              // positions per block
   constexpr int KS = D / 32;                // MFMA k-steps over D (scores)
   constexpr int NT = KB / 16;               // key tiles per step
   constexpr int DT = D / 16;                // output d tiles
@@ -110,7 +121,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
   constexpr int LDP = KB + 8;               // P row stride
   __shared__ __align__(16) uint16_t kt[KB * LDK];
   __shared__ __align__(16) uint16_t vt[D * LDV];
-  __shared__ __align__(16) uint16_t pt[kPfRows * LDP];
+  __shared__ __align__(16) uint16_t pt[ROWS * LDP];
   __shared__ int ptl[kPfPtl];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int kv = blockIdx.y;
@@ -146,7 +157,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
 
   // the block's page-table entries, staged once (a barrier follows before use)
   const int first_pg = (kb0 * KB) / a.page;
-  for (int i = tid; i < kPfPtl; i += 256) ptl[i] = a.pt[min(first_pg + i, a.max_pages - 1)];
+  for (int i = tid; i < kPfPtl; i += NTH) ptl[i] = a.pt[min(first_pg + i, a.max_pages - 1)];
   auto page_of = [&](int kb) {
     const int idx = (kb * KB) / a.page - first_pg;
     return (idx < kPfPtl) ? ptl[idx] : a.pt[min(first_pg + idx, a.max_pages - 1)];
@@ -154,8 +165,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
   // K (and V) rows of key block kb into registers (fetch), then into LDS
   // (put); invalid pages read as zero.  The loads are unconditional (page 0
   // stands in for an invalid entry) and the zero is selected afterwards.
-  constexpr int CPT = KB * D / 8 / 256;  // 16-byte chunks per thread and tile
-  static_assert(CPT * 256 * 8 == KB * D, "tile chunks");
+  constexpr int CPT = KB * D / 8 / NTH;  // 16-byte chunks per thread and tile
+  static_assert(CPT >= 1 && CPT * NTH * 8 == KB * D, "tile chunks");
   struct Tile {
     u32x4 k[CPT], v[CPT];
     bool ok;
@@ -166,11 +177,11 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
     T.ok = pg >= 0 && pg < a.num_pages;
     const size_t base = (((size_t)(T.ok ? pg : 0) * a.KV + kv) * a.page + (k0 % a.page)) * D;
 #pragma unroll
-    for (int i = 0; i < CPT; ++i) T.k[i] = ld16((const u32x4*)(a.k_pages + base) + tid + 256 * i);
+    for (int i = 0; i < CPT; ++i) T.k[i] = ld16((const u32x4*)(a.k_pages + base) + tid + NTH * i);
     if (with_v) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int c = tid + 256 * i, j = c % KB, d0 = (c / KB) * 8;
+        const int c = tid + NTH * i, j = c % KB, d0 = (c / KB) * 8;
         T.v[i] = ld16((const u32x4*)(a.v_pages + base + (size_t)j * D + d0));
       }
     }
@@ -180,7 +191,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
     // K: lanes walk a key row (conflict-free 16-byte stores)
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
-      const int c = tid + 256 * i, j = c / (D / 8), d0 = (c % (D / 8)) * 8;
+      const int c = tid + NTH * i, j = c / (D / 8), d0 = (c % (D / 8)) * 8;
       *(u32x4*)(kt + j * LDK + d0) = T.ok ? T.k[i] : z;
     }
     // V transposed: lanes walk the keys of one 8-value column group, so the
@@ -188,7 +199,7 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(PfAttnArgs a) {
     if (with_v) {
 #pragma unroll
       for (int i = 0; i < CPT; ++i) {
-        const int c = tid + 256 * i, j = c % KB, d0 = (c / KB) * 8;
+        const int c = tid + NTH * i, j = c % KB, d0 = (c / KB) * 8;
         const u32x4 v4 = T.ok ? T.v[i] : z;
         const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
@@ -358,11 +369,13 @@ int g4mi_prefill_attention(const uint16_t* q, const uint16_t* k_pages, const uin
   a.q = q; a.k_pages = k_pages; a.v_pages = v_pages; a.pt = page_table; a.ctx = ctx;
   a.T = (int)T; a.NH = (int)NH; a.KV = (int)KV; a.page = (int)page_size; a.num_pages = (int)num_pages;
   a.max_pages = (int)max_pages; a.p0 = (int)p0; a.window = (int)window; a.softcap = softcap;
-  const int QP = kPfRows / (int)G;
-  dim3 grid((unsigned)((T + QP - 1) / QP), (unsigned)KV);
   hipStream_t st = as_stream(stream);
-#define G4MI_PF(DD, GG) \
-  if (D == DD && G == GG) hipLaunchKernelGGL((attn_prefill_kernel<DD, GG>), grid, dim3(256), 0, st, a);
+#define G4MI_PF(DD, GG)                                                                                   \
+  if (D == DD && G == GG) {                                                                               \
+    constexpr int QP = 16 * pf_waves<DD>() / GG;                                                          \
+    hipLaunchKernelGGL((attn_prefill_kernel<DD, GG>), dim3((unsigned)((T + QP - 1) / QP), (unsigned)KV),  \
+                       dim3(64 * pf_waves<DD>()), 0, st, a);                                              \
+  }
   G4MI_PF(64, 1) G4MI_PF(64, 2) G4MI_PF(64, 4) G4MI_PF(64, 8)
   G4MI_PF(128, 1) G4MI_PF(128, 2) G4MI_PF(128, 4) G4MI_PF(128, 8)
   G4MI_PF(256, 1) G4MI_PF(256, 2) G4MI_PF(256, 4) G4MI_PF(256, 8)
