@@ -170,7 +170,11 @@ __global__ __launch_bounds__(256) void router_select_kernel(const float* __restr
 //     act = bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(top_w))   (model.py:270-271)
 // Routing comes either from top_w/top_i (global) or, when `scores` is given,
 // from a per-block selection; block x == 0 of each token then also stores
-// top_w/top_i for later kernels.
+// top_w/top_i for later kernels.  With the routing given and several tokens
+// (N * K <= 64 pairs), an expert chosen by more than one (token, slot) pair
+// has its rows read once: the first such pair's wave computes row f for
+// every pair that chose the expert (the other tokens' x from global memory,
+// the same dot products), and the later pairs' waves return.
 template <int IT>
 __global__ __launch_bounds__(256) void moe_gateup_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gate_up, const float* __restrict__ scores,
@@ -200,6 +204,10 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   const int slot = tc / F, f = tc - slot * F;
   const int ei = (scores != nullptr) ? L.topi[slot] : top_i[n * K + slot];
   const bool ok = task < K * F && ei >= 0 && ei < E;  // else: contribute nothing
+  const int NK = (int)gridDim.y * K;
+  const bool dedup = scores == nullptr && gridDim.y > 1 && NK <= 64;  // block-uniform
+  const int pe_raw = top_i[min(lane, NK - 1)];  // every pair's expert, one per lane (unconditional load)
+  const int pe = (dedup && lane < NK) ? pe_raw : -1;
   const u32x4* row = (const u32x4*)(gate_up + ((size_t)(max(min(ei, E - 1), 0) * 2 + half) * F + f) * H);
   u32x4 w[IT];
 #pragma unroll
@@ -208,16 +216,41 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   for (int j = 0; j < XPT; ++j)
     if ((int)threadIdx.x + (int)blockDim.x * j < H / 8) xs[threadIdx.x + blockDim.x * j] = xr[j];
   lds_barrier();
-  float acc = 0.0f;
+  // act of pair q = (token nq, slot q % K) from row f of its expert (in w)
+  auto emit = [&](int q, int nq) __attribute__((always_inline)) {
+    float acc = 0.0f;
+    if (nq == n) {
 #pragma unroll
-  for (int i = 0; i < IT; ++i) acc = dot8(w[i], xs[l + 32 * i], acc);
-  acc = group_sum<32>(acc);
-  const float up = __shfl(acc, 32, kWave);
-  if (lane == 0 && task < K * F) {
-    const float tw = (scores != nullptr) ? L.topw[slot] : top_w[n * K + slot];
-    const float g = rbf(acc), u = rbf(up);
-    const float a = rbf(rbf(rbf(gelu_tanh(g)) * u) * rbf(tw));
-    act[((size_t)n * K + slot) * F + f] = ok ? f2bf(a) : (uint16_t)0;
+      for (int i = 0; i < IT; ++i) acc = dot8(w[i], xs[l + 32 * i], acc);
+    } else {
+      const u32x4* xq = (const u32x4*)(x + (size_t)nq * H);
+      u32x4 xv[IT];
+#pragma unroll
+      for (int i = 0; i < IT; ++i) xv[i] = ld16(xq + l + 32 * i);
+#pragma unroll
+      for (int i = 0; i < IT; ++i) acc = dot8(w[i], xv[i], acc);
+    }
+    acc = group_sum<32>(acc);
+    const float up = __shfl(acc, 32, kWave);
+    if (lane == 0) {
+      const float tw = (scores != nullptr) ? L.topw[q % K] : top_w[q];
+      const float g = rbf(acc), u = rbf(up);
+      const float a = rbf(rbf(rbf(gelu_tanh(g)) * u) * rbf(tw));
+      act[(size_t)q * F + f] = ok ? f2bf(a) : (uint16_t)0;
+    }
+  };
+  if (task >= K * F) return;
+  const int p = n * K + slot;
+  if (!dedup || !ok) {
+    emit(p, n);
+    return;
+  }
+  unsigned long long same = __ballot(pe == ei);  // the pairs that chose this expert (includes p)
+  if ((same & ((1ull << p) - 1ull)) != 0ull) return;  // an earlier pair's wave computes row f for them all
+  while (same != 0ull) {
+    const int q = (int)__builtin_ctzll(same);
+    same &= same - 1ull;
+    emit(q, q / K);
   }
 }
 

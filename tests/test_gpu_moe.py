@@ -142,6 +142,26 @@ def test_grouped_decode_experts_equal_pair_path_c2(c2, n):
     _check_out(got, _dense_selected(cfg, cpu, x.cpu()), f"grouped experts f32 combine n={n}")
 
 
+@pytest.mark.parametrize("n,pool", [(2, 8), (4, 12), (8, 8), (8, 20), (8, 128)])
+def test_gateup_shared_experts_read_once_bit_identical(c2, n, pool):
+    """With the routing given and several tokens, an expert chosen by more than
+    one (token, slot) pair has its gate/up rows read once (the first pair's
+    waves compute every pair's act); act must equal the token-at-a-time calls
+    (one token: no sharing) bit for bit.  The experts are drawn from `pool` of
+    them (pool 8: every token chose the same 8 experts, in different slots)."""
+    cfg, g, _ = c2
+    k = cfg.top_k_experts
+    x = _gen((n, cfg.hidden_size), 3, f"xs.n{n}.{pool}", 1.0)
+    rng = np.random.default_rng(1000 + 10 * n + pool)
+    ti = torch.tensor(np.stack([rng.permutation(pool)[:k] for _ in range(n)]), dtype=torch.int32, device=DEV)
+    tw = torch.tensor(rng.uniform(0.01, 0.3, size=(n, k)), dtype=torch.float32, device=DEV)
+    gu = g["experts.gate_up_proj"]
+    got = ops.moe_gateup(x, gu, tw, ti)
+    ref = torch.cat([ops.moe_gateup(x[i:i + 1], gu, tw[i:i + 1], ti[i:i + 1]) for i in range(n)])
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (n, pool)
+
+
 def test_grouped_decode_experts_tiny_shapes():
     """Tiny-model expert shapes (hidden 256, 16 experts top-4, width 128) at
     16 tokens: 64 pairs over at most 16 experts."""
