@@ -72,8 +72,7 @@ struct InArgs {
 };
 
 // Row walk shared by the GEMV kernels: a block owns `ppb` consecutive row
-// pairs (ppb a multiple of 4); wave w handles pairs w, w+4, ... and half-wave
-// h row 2*pair+h.  Each wave keeps the next pair's loads in flight while it
+// pairs; wave w handles pairs w, w+4, ... and half-wave h row 2*pair+h.  Each wave keeps the next pair's loads in flight while it
 // reduces the current one, so a block per CU streams at full rate and the
 // block's prologue is computed once per CU instead of once per 8 rows.
 template <int IT>
@@ -680,7 +679,11 @@ int g4mi_layer_in(int32_t mode, const int32_t* tok, const uint16_t* embed, int64
   a.out = qkv_out; a.H = (int)H; a.eps = eps;
   const int total = (int)(q_rows + k_rows + v_rows);
   const int npairs = (total + 1) / 2;
-  a.pairs_per_block = row_groups_per_block(npairs);
+  // one block per CU: the pairs are not rounded up to a multiple of the 4
+  // waves (the full 26B layer's 4,608 pairs are 18 per block on 256 CUs, not
+  // 20 on 231; a CU streams its block's rows at its own rate, so the waves'
+  // 5 or 4 pairs do not matter)
+  a.pairs_per_block = max(1, (npairs + gemv_blocks() - 1) / gemv_blocks());
   dim3 grid((unsigned)((npairs + a.pairs_per_block - 1) / a.pairs_per_block));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {
