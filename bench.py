@@ -576,7 +576,8 @@ def run_decode(args) -> dict:
             "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
             "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS,
             "kernels_per_token": 7 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token (Engine.decode_fn)",
-            "prefill": "Engine.prefill_fn: batched (library dense GEMMs, dense-MoE prefill, MFMA prefill attention)",
+            "prefill": "Engine.prefill_fn: batched (hand-written MFMA GEMMs, dense-MoE prefill on the selected "
+                       "experts, MFMA prefill attention)",
             "first_tokens": res["tokens"][:8],
         },
         "roofline": {
@@ -636,8 +637,8 @@ def _prefill_flops(cfg, n: int) -> dict:
 
 def run_prefill(args) -> dict:
     """Prefill of the 26B-A4B-shaped model: --prompt-len uniform-random tokens
-    (seed 4) through Engine.prefill_fn (batched: library dense GEMMs, the dense-MoE
-    prefill on the selected experts, MFMA prefill attention), first token sampled
+    (seed 4) through Engine.prefill_fn (batched: hand-written MFMA GEMMs, the
+    dense-MoE prefill on the selected experts, MFMA prefill attention), first token sampled
     greedily.  value = prompt tok/s."""
     import numpy as np
     import torch
