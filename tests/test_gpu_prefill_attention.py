@@ -7,7 +7,9 @@ Cases: a small full layer with separate V; a small sliding layer with k==v
 and softcap 50 continuing a 70-position cached prefix (p0 = 70) over a
 shuffled page table; the 26B sliding shape (16 q / 8 KV heads, head_dim 256)
 with a 100-position window; the 26B full shape (16 q / 2 KV heads,
-head_dim 512, k==v, partial RoPE 0.25) over 300 rows.
+head_dim 512, k==v, partial RoPE 0.25) over 300 rows; 70 rows after a
+16,448-position cached prefix (key pages past the 256 whose table entries a
+block stages in LDS).
 
 Tolerances: ctx (bf16) corr >= 0.9999, >= 95% of elements bit-identical,
 every element within 2^-6 of the output's max magnitude.  The GPU accumulates
@@ -108,3 +110,11 @@ def test_26b_sliding_shape():
 
 def test_26b_full_shape():
     _prefill_case(300, 16, 2, 512, 0, 0.0, True, 1e6, 0.25, 44)
+
+
+def test_long_cached_prefix_beyond_the_staged_page_entries():
+    """A block stages the page-table entries of its first 256 key pages in LDS
+    and reads later entries directly: 70 query rows after a 16,448-position
+    cached prefix (258 pages of 64 over a shuffled table) attend keys on both
+    sides of that limit."""
+    _prefill_case(70, 4, 2, 64, 0, 0.0, False, 1e4, 1.0, 45, p0=16448)
