@@ -627,9 +627,20 @@ int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, cons
   G4MI_REQUIRE(al16(ws), G4MI_EALIGN, "moe_block_decode: workspace must be 16-byte aligned");
   float* scores = (float*)ws;
   uint16_t* act = (uint16_t*)((char*)ws + g4mi_moe_router_workspace_bytes(N, E));
-  int rc = g4mi_moe_router_scores(xn, nullptr, router_scale, router_proj, N, H, E, eps, scores, stream);
-  if (rc) return rc;
-  rc = g4mi_moe_gateup_routed(xn, scores, per_expert_scale, gate_up, N, H, F, E, k, act, top_w, top_i, stream);
+  int rc;
+  if (N > 1 && N * k <= 64) {
+    // several tokens: one selection launch, then the gate/up with the routing
+    // given, which reads an expert chosen by several tokens once
+    rc = g4mi_moe_router_topk(xn, nullptr, router_scale, router_proj, per_expert_scale, N, H, E, k, eps, top_w,
+                              top_i, ws, g4mi_moe_router_workspace_bytes(N, E), stream);
+    if (rc) return rc;
+    rc = g4mi_moe_gateup(xn, gate_up, top_w, top_i, N, H, F, E, k, act, stream);
+  } else {
+    // one token: the selection runs in every gate/up block (no launch between)
+    rc = g4mi_moe_router_scores(xn, nullptr, router_scale, router_proj, N, H, E, eps, scores, stream);
+    if (rc) return rc;
+    rc = g4mi_moe_gateup_routed(xn, scores, per_expert_scale, gate_up, N, H, F, E, k, act, top_w, top_i, stream);
+  }
   if (rc) return rc;
   return g4mi_moe_down(act, down, top_i, N, H, F, E, k, combine, out, stream);
 }
