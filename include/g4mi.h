@@ -82,7 +82,9 @@ int g4mi_moe_router_topk(const uint16_t* x, const uint16_t* pre_norm_w, const ui
  *   act[N,k,F] bf16 = bf16(bf16(bf16(gelu(g)) * u) * bf16(top_w)) where (g, u)
  *   are the gate/up rows of expert top_i[n,slot] applied to xn [N,H].
  * gate_up [E,2,F,H] bf16 (gate rows then up rows).  Reads only the selected
- * experts' rows.  H = 256*i, F = 64*i (1 <= i <= 16), k <= 32. */
+ * experts' rows; with N > 1 and N*k <= 64 an expert chosen by several
+ * (token, slot) pairs has its rows read once for all of them (same results).
+ * H = 256*i, F = 64*i (1 <= i <= 16), k <= 32. */
 int g4mi_moe_gateup(const uint16_t* xn, const uint16_t* gate_up, const float* top_w, const int32_t* top_i,
                     int64_t N, int64_t H, int64_t F, int64_t E, int64_t k, uint16_t* act, void* stream);
 
@@ -108,7 +110,9 @@ int g4mi_moe_experts_decode(const uint16_t* xn, const uint16_t* gate_up, const u
 
 /* The whole MoE decode block of model.py:235-294 on xn [N,H] (the
  * pre_feedforward_layernorm_2 output): router scores, then gate/up with the
- * selection fused in, then down + combine.  Three kernels, no host sync. */
+ * selection fused in, then down + combine (three kernels); with N > 1 and
+ * N*k <= 64 the selection is its own kernel and the gate/up reads a shared
+ * expert once (four kernels).  No host sync. */
 int64_t g4mi_moe_block_workspace_bytes(int64_t N, int64_t E, int64_t F, int64_t k);
 int g4mi_moe_block_decode(const uint16_t* xn, const uint16_t* router_scale, const uint16_t* router_proj,
                           const uint16_t* per_expert_scale, const uint16_t* gate_up, const uint16_t* down,
