@@ -401,9 +401,20 @@ def _e2e_decode(args) -> dict:
     ms = e0.elapsed_time(e1) / args.steps
     p1 = int(pos)
     toks = eng._runner.hist[prompt_len: p1 + 1].cpu().tolist()
+    # the median inter-token latency: up to 64 more steps with an event between
+    # the graph replays (after the tokens above were read)
+    n_itl = max(0, min(64, args.max_len - 1 - p1))
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_itl + 1)]
+    evs[0].record()
+    for i in range(n_itl):
+        tok, cache, pos = dec(eng.params, tok, cache, pos, seed, 0.0, 1.0)
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    itl_median = float(np.median([evs[i].elapsed_time(evs[i + 1]) for i in range(n_itl)])) if n_itl else ms
     bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
     return {"cfg": cfg, "params": eng.params, "cache": eng.cache, "engine": eng, "ms": ms, "ttft": ttft,
-            "first": first, "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt}
+            "first": first, "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt,
+            "itl_median_ms": itl_median, "itl_median_positions": [p1, p1 + n_itl]}
 
 
 def _filled_decode(res, steps: int = 64, warm: int = 4) -> dict:
@@ -572,7 +583,8 @@ def run_decode(args) -> dict:
             "layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size, "experts": cfg.num_experts,
             "top_k": cfg.top_k_experts, "vocab": cfg.vocab_size, "max_len": args.max_len, "seed": 3,
             "prompt_len": args.prompt_len, "positions_timed": [res["p0"], res["p1"]],
-            "ttft_s": res["ttft"], "itl_ms": ms,
+            "ttft_s": res["ttft"], "itl_ms": ms, "itl_median_ms": res["itl_median_ms"],
+            "itl_median_positions": res["itl_median_positions"],
             "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
             "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS,
             "kernels_per_token": 7 * cfg.num_hidden_layers + 2, "launch": "HIP graph per token (Engine.decode_fn)",
