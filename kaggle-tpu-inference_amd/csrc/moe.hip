@@ -32,7 +32,8 @@ constexpr int kMaxH = 16384;
 // The dot is exact (f64, bf16*bf16 products are exact) and rounded once, so
 // the scores -- and the top-k they induce -- do not depend on reduction order.
 //
-// Fast path H = 256*IT: grid (ceil(E/8), N), 4 waves x 2 rows.  Each half-wave
+// More tokens, H = 256*IT: grid (ceil(E/8), N), 4 waves x 2 rows (the rows
+// then come from the caches, and the prologue is shared by 8 rows).  Each half-wave
 // issues its row's IT 16-byte loads first; meanwhile the block builds x2 once
 // in LDS (each thread owns at most two 8-value chunks), then every half-wave
 // dots its row against it.
@@ -110,6 +111,82 @@ __global__ __launch_bounds__(256) void router_scores_kernel(
     if (l == 0) scores[(size_t)n * E + e] = rbf(f32_of(acc));
   }
 }
+
+// Few tokens (N <= 16), H = 256*IT: grid (ceil(E/2), N), one wave per block,
+// a half-wave per expert row.  Every operand (the row's IT 16-byte chunks per lane, the
+// token's activations and both norm weights) is requested before the first
+// reduction, so a block waits on one memory round trip; the two norms are
+// wave reductions, and x2 passes through LDS to the dots.  (With 8 rows per
+// 4-wave block the weights were loaded after each block reduction: three
+// dependent round trips, 16 blocks for the 26B router's 0.72 MB.)
+template <int IT>
+__global__ __launch_bounds__(64) void router_scores_wave_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ pre_w, const uint16_t* __restrict__ scale,
+    const uint16_t* __restrict__ proj, int E, float eps, float inv_sqrt_h_bf, float* __restrict__ scores) {
+  constexpr int H = IT * 256;
+  constexpr int CH = H / 8;                // 16-byte chunks per row
+  constexpr int PER = (CH + 63) / 64;      // chunks per lane
+  __shared__ u32x4 xs[CH];
+  const int lane = threadIdx.x, half = lane >> 5, l = lane & 31;
+  const int n = blockIdx.y;
+  const int e = blockIdx.x * 2 + half;
+  u32x4 w[IT];
+  const u32x4* row = (const u32x4*)(proj + (size_t)min(e, E - 1) * H);
+#pragma unroll
+  for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 32 * i);
+  const u32x4* xr = (const u32x4*)(x + (size_t)n * H);
+  const u32x4* pwr = (const u32x4*)(pre_w != nullptr ? pre_w : scale);
+  u32x4 v[PER], pw[PER], sc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const int c = min(lane + 64 * j, CH - 1);
+    v[j] = ld16(xr + c);
+    pw[j] = ld16(pwr + c);
+    sc[j] = ld16((const u32x4*)scale + c);
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j)
+    if (lane + 64 * j >= CH) v[j] = u32x4{0u, 0u, 0u, 0u};
+  if (pre_w != nullptr) {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) ss = sumsq8_f64(v[j], ss);
+    const float r = rms_scale(group_sum_f64<64>(ss), H, eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) v[j] = scale8(v[j], r, &pw[j]);
+  }
+  {
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) ss = sumsq8_f64(v[j], ss);
+    const float r = rms_scale(group_sum_f64<64>(ss), H, eps);
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int c = lane + 64 * j;
+      if (c < CH) {
+        float f[8], g[8];
+        unpack8(v[j], f);
+        unpack8(sc[j], g);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r) * g[q]) * inv_sqrt_h_bf);
+        u32x4 o;
+        o.x = pack2(f[0], f[1]); o.y = pack2(f[2], f[3]); o.z = pack2(f[4], f[5]); o.w = pack2(f[6], f[7]);
+        xs[c] = o;
+      }
+    }
+  }
+  __syncthreads();
+  double a0 = 0.0, a1 = 0.0;
+#pragma unroll
+  for (int i = 0; i < IT; ++i) {
+    if (i & 1) a1 = dot8_f64(w[i], xs[l + 32 * i], a1);
+    else a0 = dot8_f64(w[i], xs[l + 32 * i], a0);
+  }
+  const double acc = group_sum_f64<32>(a0 + a1);
+  if (e < E && l == 0) scores[(size_t)n * E + e] = rbf(f32_of(acc));
+}
+
+constexpr int kRouterWaveRows = 16;  // tokens up to which router_scores_wave_kernel runs
 
 // Generic-H router scores: one block per (8 experts, token); the router input
 // is rebuilt in LDS with block reductions.
@@ -455,8 +532,12 @@ static void launch_scores(const uint16_t* x, const uint16_t* pre_w, const uint16
     switch (H / 256) {
 #define G4MI_CASE(I)                                                                                       \
   case I:                                                                                                  \
-    hipLaunchKernelGGL(router_scores_kernel<I>, grid, dim3(256), 0, st, x, pre_w, scale, proj, E, eps, c, \
-                       scores);                                                                            \
+    if (N <= kRouterWaveRows)                                                                              \
+      hipLaunchKernelGGL(router_scores_wave_kernel<I>, dim3((unsigned)((E + 1) / 2), (unsigned)N), dim3(64), 0, \
+                         st, x, pre_w, scale, proj, E, eps, c, scores);                                    \
+    else                                                                                                   \
+      hipLaunchKernelGGL(router_scores_kernel<I>, grid, dim3(256), 0, st, x, pre_w, scale, proj, E, eps, c, \
+                         scores);                                                                          \
     return;
       G4MI_IT_CASES(G4MI_CASE)
 #undef G4MI_CASE
