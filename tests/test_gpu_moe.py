@@ -249,7 +249,7 @@ def test_router_workspace_reuse_across_batch_sizes(c2):
         assert np.array_equal(ti.cpu().numpy(), ei.numpy().astype(np.int32)), n
 
 
-@pytest.mark.parametrize("n", [1, 4, 8])
+@pytest.mark.parametrize("n", [1, 4, 8, 16, 17])
 def test_router_scores_bit_exact(c2, n):
     cfg, g, cpu = c2
     x = _gen((n, cfg.hidden_size), 1, f"x.n{n}", 1.0)
@@ -313,6 +313,23 @@ def test_router_scores_many_rows_match_row_path(c2):
                                                 cfg.rms_norm_eps, pre_norm_w=pw) for i in range(0, n, 64)])
         torch.cuda.synchronize()
         assert torch.equal(many, rows), (pw is None, (many != rows).sum().item())
+
+
+def test_router_scores_wave_kernel_matches_block_kernel(c2):
+    """Up to 16 rows the router runs one-wave blocks of two experts, from 17
+    rows 4-wave blocks of eight.  Both take exact f64 dots of the same
+    rounded router input, so 17 rows in one call equal the same rows in calls
+    of 16 and 1, bit for bit, with and without the pre_feedforward_layernorm_2
+    pre-norm."""
+    cfg, g, _ = c2
+    x = _gen((17, cfg.hidden_size), 9, "router.wave", 1.0)
+    pre = _gen((cfg.hidden_size,), 9, "router.wave.pre", 0.5)
+    for pw in (None, pre):
+        block = ops.moe_router_scores(x, g["router.scale"], g["router.proj"], cfg.rms_norm_eps, pre_norm_w=pw)
+        wave = torch.cat([ops.moe_router_scores(x[i:j].contiguous(), g["router.scale"], g["router.proj"],
+                                                cfg.rms_norm_eps, pre_norm_w=pw) for i, j in ((0, 16), (16, 17))])
+        torch.cuda.synchronize()
+        assert torch.equal(block, wave), (pw is None, (block != wave).sum().item())
 
 
 def test_router_scores_mfma_path_bit_exact(c2):
