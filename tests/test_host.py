@@ -216,3 +216,30 @@ def test_fold_in_keys():
 
     assert M.fold_in(7, 3) == (7, 3)
     assert M.fold_in((7, 99), 5) == (7, 5)
+
+
+def _run_bench(*argv):
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    return subprocess.run([sys.executable, os.path.join(root, "bench.py"), *argv], capture_output=True, text=True,
+                          timeout=300, cwd=root)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits 2 with a message that
+    says so, before touching torch or a device."""
+    r = _run_bench("--gpus", "2")
+    assert r.returncode == 2
+    assert "one MI355X" in r.stderr and "--gpus 2" in r.stderr
+    assert r.stdout == ""
+
+
+@pytest.mark.skipif(torch.cuda.is_available(), reason="checks the no-GPU exit")
+def test_bench_without_a_gpu_exits_without_a_result_line():
+    r = _run_bench("--workload", "moe_block", "--steps", "1", "--warmup", "0")
+    assert r.returncode == 2
+    assert "needs a GPU" in r.stderr
+    assert r.stdout == ""
