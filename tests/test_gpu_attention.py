@@ -7,7 +7,8 @@ decode positions on both sides of the 512-position limit between the
 per-slice PV path and the split partials; and the two isolated
 attention workloads at 32K positions (sliding window 1024 with 16 q / 8 KV
 heads at head_dim 256; full k==v with 16 q / 2 KV heads at head_dim 512;
-RoPE applied, softcap 50, seed 2).
+RoPE applied, softcap 50, seed 2); positions outside the cache (past it,
+negative) and page-table entries outside the pool on each P.V path.
 
 Tolerances: the appended K/V rows are bit-exact (same deterministic norm and
 RoPE recipe); ctx (bf16) has corr >= 0.9999, every element within 2^-7 of
@@ -188,6 +189,73 @@ def test_out_of_range_position_attends_to_nothing():
     torch.cuda.synchronize()
     assert torch.count_nonzero(ctx).item() == 0
     assert torch.equal(kp, kp0) and torch.equal(vp, vp0)
+
+
+def test_negative_position_attends_to_nothing():
+    """A device position below zero leaves the cache untouched and yields ctx = 0."""
+    B, NH, KV, D, lmax, page = 1, 4, 2, 64, 64, 16
+    q = _gen((B, NH, D), 6, "q")
+    k = _gen((B, KV, D), 6, "k")
+    qn = _gen((D,), 6, "qn")
+    cos, sin = gm.rope_table(D, 1e4, 1.0, lmax, DEV)
+    kp = _gen((4, KV, page, D), 6, "kp")
+    vp = _gen((4, KV, page, D), 6, "vp")
+    kp0, vp0 = kp.clone(), vp.clone()
+    pt = torch.arange(4, dtype=torch.int32, device=DEV)[None]
+    ctx = ops.decode_attention(q, k, k, qn, qn, cos, sin, kp, vp, pt, torch.tensor([-1], dtype=torch.int32,
+                               device=DEV), 0, 0.0, 1e-6, lmax)
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(ctx).item() == 0
+    assert torch.equal(kp, kp0) and torch.equal(vp, vp0)
+
+
+@pytest.mark.parametrize("lmax,pos,ns", [
+    (1024, 300, 16),    # one range of at most 512 positions (per-slice P.V)
+    (2048, 900, 32),    # 4-wave splits with the in-kernel reduction
+    (4096, 3000, 16),   # 8-wave splits and the reduction launch
+])
+def test_page_entries_outside_the_pool_are_skipped(lmax, pos, ns):
+    """Two page-table entries inside the attended range point outside the
+    pool (-1 and num_pages + 5): their positions take no part, as if masked
+    (the oracle with those positions masked out), the appended K/V rows are
+    bit-exact, and no other page of the pool changes."""
+    B, NH, KV, D, page, seed, eps = 1, 8, 2, 64, 16, 61, 1e-6
+    G = NH // KV
+    max_pages = lmax // page
+    q_raw = _gen((B, NH, D), seed, "q")
+    k_raw = _gen((B, KV, D), seed, "k")
+    v_raw = _gen((B, KV, D), seed, "v")
+    q_norm, k_norm = _gen((D,), seed, "q_norm", 0.5), _gen((D,), seed, "k_norm", 0.5)
+    cos, sin = gm.rope_table(D, 1e4, 1.0, lmax, DEV)
+    ck, cv = _gen((lmax, KV, D), seed, "ck"), _gen((lmax, KV, D), seed, "cv")
+    ident = list(range(max_pages))
+    kp = _pages_from_contig(ck, page, ident, max_pages)
+    vp = _pages_from_contig(cv, page, ident, max_pages)
+    bad = [3, (pos // page) // 2]
+    pt = torch.arange(max_pages, dtype=torch.int32)
+    pt[bad[0]] = -1
+    pt[bad[1]] = max_pages + 5
+    kp0, vp0 = kp.clone(), vp.clone()
+    ctx = ops.decode_attention(q_raw, k_raw, v_raw, q_norm, k_norm, cos, sin, kp, vp, pt[None].to(DEV),
+                               torch.tensor([pos], dtype=torch.int32, device=DEV), 0, 0.0, eps, lmax,
+                               n_split_max=ns)
+    torch.cuda.synchronize()
+
+    class C:
+        sliding_window = 0
+    mask = twin.decode_masks(C, lmax, pos)[twin.FULL].clone()
+    for i in bad:
+        mask[..., i * page:(i + 1) * page] = False
+    c, s = twin.rope_tables([pos], twin.rope_inv_freq(D, 1e4, 1.0))
+    ectx, ek, ev = twin.attention_core(q_raw[0].cpu().reshape(1, 1, KV, G, D), k_raw[0].cpu().reshape(1, 1, KV, D),
+                                       v_raw[0].cpu().reshape(1, 1, KV, D), q_norm.cpu(), k_norm.cpu(), c, s,
+                                       ck.cpu()[None], cv.cpu()[None], pos, mask, lmax, eps, 0.0)
+    _check(ctx[0].reshape(-1), ectx.reshape(-1), f"ctx pos {pos} with pages {bad} outside the pool")
+    wp = pos // page
+    assert torch.equal(kp[wp, :, pos % page].cpu().view(torch.int16), ek[0, pos].view(torch.int16))
+    assert torch.equal(vp[wp, :, pos % page].cpu().view(torch.int16), ev[0, pos].view(torch.int16))
+    others = [i for i in range(max_pages) if i != wp]
+    assert torch.equal(kp[others], kp0[others]) and torch.equal(vp[others], vp0[others])
 
 
 def test_sliding_and_full_layers_share_one_workspace():
