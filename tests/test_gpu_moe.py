@@ -162,6 +162,28 @@ def test_gateup_shared_experts_read_once_bit_identical(c2, n, pool):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (n, pool)
 
 
+@pytest.mark.parametrize("n", [1, 4])
+def test_expert_indices_outside_the_table_contribute_nothing(c2, n):
+    """A routed expert index outside [0, E) (-1, E + 7) is skipped: the
+    output is bit-identical to the same routing with that slot pointing at a
+    valid expert with routing weight 0 (whose activation is exactly zero),
+    at one token and at four (the gate/up that reads a shared expert once)."""
+    cfg, g, _ = c2
+    x = _gen((n, cfg.hidden_size), 1, f"x.badexp{n}", 1.0)
+    tw, ti = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                 cfg.top_k_experts, cfg.rms_norm_eps)
+    ti_bad, tw_zero = ti.clone(), tw.clone()
+    ti_bad[0, 3] = -1
+    tw_zero[0, 3] = 0.0
+    if n > 1:
+        ti_bad[n - 1, 5] = cfg.num_experts + 7
+        tw_zero[n - 1, 5] = 0.0
+    out_bad = ops.moe_experts(x, g["experts.gate_up_proj"], g["experts.down_proj"], tw, ti_bad)
+    out_zero = ops.moe_experts(x, g["experts.gate_up_proj"], g["experts.down_proj"], tw_zero, ti)
+    torch.cuda.synchronize()
+    assert torch.equal(out_bad.view(torch.int16), out_zero.view(torch.int16))
+
+
 def test_grouped_decode_experts_tiny_shapes():
     """Tiny-model expert shapes (hidden 256, 16 experts top-4, width 128) at
     16 tokens: 64 pairs over at most 16 experts."""
