@@ -4,6 +4,8 @@
 * generate() at temperature 0 yields the oracle's greedy tokens (prefill
   event first, then decode events with the reference's fields), through the
   captured feed/head/decode graphs with lookahead 3;
+* prompts of 1, 37, 256 and 300 tokens (one and two prefill buckets) give
+  the oracle's greedy tokens, or declared near ties, teacher-forced;
 * prefill_fn / decode_fn keep the reference's calling convention
   ((tok [1,1], cache, pos) returns, cache updated in place);
 * stop ids end the stream; a prompt that fills the context raises ValueError;
@@ -22,6 +24,7 @@ from scipy import stats
 from gemma4_mi import ops
 from gemma4_mi.config import tiny_parity_config
 from gemma4_mi.engine import Engine
+from greedy_check import check_stream
 from oracle import twin
 
 pytestmark = pytest.mark.gpu
@@ -58,6 +61,23 @@ def test_stepwise_prefill_engine_matches_oracle(setup):
     eng2 = Engine(None, MAX_LEN, 1, 64, cfg=cfg, params=eng.params, device=DEV, prefill="stepwise")
     toks = [e["token"] for e in eng2.generate(prompt.tolist(), max_new_tokens=9, temperature=0.0, stop_ids=())]
     assert toks == list(gen_o[:9])
+
+
+@pytest.mark.parametrize("plen", [1, 37, 256, 300])
+def test_prompt_lengths_across_prefill_buckets(setup, plen):
+    """Prompts of 1, 37, 256 (one whole bucket) and 300 tokens (two buckets)
+    through the batched prefill, then 5 greedy decode steps: the bucket is the
+    reference's (multiples of 256), and every token is the oracle's greedy
+    choice given the same history, or a declared near tie."""
+    cfg, eng, _, _ = setup
+    max_len = 640
+    eng2 = Engine(None, max_len, 1, 64, cfg=cfg, params=eng.params, device=DEV)
+    prompt = np.random.default_rng(100 + plen).integers(0, cfg.vocab_size, size=plen).astype(np.int64)
+    events = list(eng2.generate(prompt.tolist(), max_new_tokens=6, temperature=0.0, stop_ids=()))
+    assert events[0]["prompt_tokens"] == plen and events[0]["prefill_bucket"] == max(256, -(-plen // 256) * 256)
+    gen = [e["token"] for e in events]
+    assert len(gen) == 6
+    check_stream(cfg, twin.random_params(cfg, 0), prompt, gen, max_len, what=f"prompt of {plen}")
 
 
 def test_step_functions_calling_convention(setup):
