@@ -46,6 +46,15 @@ const char* g4mi_last_error_string(void);
  * layout of the cross-lane reductions every kernel uses. */
 int g4mi_selftest_lane_reductions(const float* in, float* out, double* out_d, int32_t waves, void* stream);
 
+/* Diagnostics (no counterpart in the reference; runs on the host, no GPU
+ * needed): the MFMA GEMM's block -> tile map.  For a grid sized for max_tiles
+ * row tiles x ncol_tiles column tiles with mtiles row tiles live (grouped
+ * tiles come from a device list whose live count is known only on the GPU),
+ * out[2b], out[2b+1] = the (row tile, column tile) block b computes, or -1, -1
+ * for a block that exits.  out_len >= 2 * 8 * ceil(max_tiles*ncol_tiles/8). */
+int g4mi_selftest_tile_order(int32_t mtiles, int32_t max_tiles, int32_t ncol_tiles, int32_t grouped,
+                             int32_t* out, int64_t out_len);
+
 /* ---------------------------------------------------------------- init
  * Fills out[0:n) with bf16(std * z), z ~ N(0,1) from Philox4x32-10 keyed by
  * `key` (element i uses counter i/2) and a Box-Muller transform in f64.

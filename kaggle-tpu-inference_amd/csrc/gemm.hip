@@ -107,10 +107,15 @@ __device__ __forceinline__ void wait_vm_barrier() {
 // (a group's A and B tiles are shared in the XCD's L2).  Grouped tiles
 // (tile list order, column tiles inner): a run covers whole tiles, so an A
 // tile is read once per XCD and the tiles of one group are neighbours.
-// Returns false for ids past the live tile count.
-__device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles_col, int& tx, int& ty, bool grouped) {
+// The grid holds 8 * ceil(max tiles / 8) blocks; with mtiles the live count
+// (at most the maximum) block bid maps to id = (bid % 8) * per + bid / 8,
+// one-to-one onto [0, nb) over the blocks with bid / 8 < per.  Returns false
+// for every other block.
+__host__ __device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles_col, int& tx, int& ty,
+                                                 bool grouped) {
   const int nb = mtiles * ntiles_col;
   const int per = (nb + 7) / 8;
+  if (bid / 8 >= per) return false;
   const int id = (bid % 8) * per + bid / 8;
   if (id >= nb) return false;
   if (grouped) {
@@ -118,7 +123,7 @@ __device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles_col, int
     ty = id % ntiles_col;
   } else {
     constexpr int G = 8;
-    const int grp = id / (G * ntiles_col), fx = grp * G, gs = min(mtiles - fx, G);
+    const int grp = id / (G * ntiles_col), fx = grp * G, gs = mtiles - fx < G ? mtiles - fx : G;
     tx = fx + (id % (G * ntiles_col)) % gs;
     ty = (id % (G * ntiles_col)) / gs;
   }
@@ -654,6 +659,25 @@ int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K
   if ((K / 32 + 3) / 4 > 24) hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 32>), grid, dim3(256), 0, st, g);
   else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 24>), grid, dim3(256), 0, st, g);
   return check_launch("gemm_bf16_segments");
+}
+
+// Host-only diagnostics: the tile that block bid of a grid sized for
+// max_tiles row tiles runs when mtiles of them are live, as (tx, ty) in
+// out[2 bid], out[2 bid + 1], or (-1, -1) for a block that exits.
+int g4mi_selftest_tile_order(int32_t mtiles, int32_t max_tiles, int32_t ncol_tiles, int32_t grouped,
+                             int32_t* out, int64_t out_len) {
+  G4MI_REQUIRE(out != nullptr, G4MI_EINVAL, "selftest_tile_order: null output");
+  G4MI_REQUIRE(mtiles >= 0 && max_tiles >= 1 && mtiles <= max_tiles && ncol_tiles >= 1, G4MI_EINVAL,
+               "selftest_tile_order: need 0 <= mtiles <= max_tiles and ncol_tiles >= 1");
+  const int64_t nb = (int64_t)max_tiles * ncol_tiles, grid = (nb + 7) / 8 * 8;
+  G4MI_REQUIRE(grid <= 2147483647 && out_len >= 2 * grid, G4MI_EINVAL, "selftest_tile_order: output too small");
+  for (int64_t b = 0; b < grid; ++b) {
+    int tx = -1, ty = -1;
+    if (!tile_of((int)b, mtiles, ncol_tiles, tx, ty, grouped != 0)) tx = ty = -1;
+    out[2 * b] = tx;
+    out[2 * b + 1] = ty;
+  }
+  return 0;
 }
 
 }  // extern "C"

@@ -150,8 +150,10 @@ class Engine:
         r.tok.copy_(saved_tok)
         r.pos.copy_(saved_pos)
         r.hist.copy_(hist_save)
-        # the warm step wrote K/V at the scratch position: clear that page again
-        self._zero_pages(0, self.max_len - 1, self.max_len)
+        # the warm step wrote K/V at the scratch position: clear those rows
+        # again (only them: the rest of their page may hold the request's
+        # positions, which the captured step is about to attend)
+        self._zero_position(0, self.max_len - 1)
         torch.cuda.synchronize(self.device)
         self._graphs[key] = g
         return g
@@ -263,6 +265,12 @@ class Engine:
         p0, p1 = b * mp + lo // page, b * mp + (hi + page - 1) // page
         for t in self.cache["k"] + self.cache["v"]:
             t[p0:p1].zero_()
+
+    def _zero_position(self, b: int, p: int) -> None:
+        """Zeroes the K/V rows of position p of cache row b (pools [pages, KV, page, D])."""
+        page, mp = self.cache["page_size"], self.cache["page_table"].shape[1]
+        for t in self.cache["k"] + self.cache["v"]:
+            t[b * mp + p // page, :, p % page].zero_()
 
     def reset_cache(self):
         """A zero cache again (engine.py:96-97 builds a new one; here the

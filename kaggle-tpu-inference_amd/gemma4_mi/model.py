@@ -642,26 +642,21 @@ class HeadRunner:
             self.ops.argmax_finalize(self.blk_val, self.blk_idx, self.tok, self.pos, self.hist)
 
 
-_RUNNERS: dict = {}
-
-
 def _runners_for(cfg: TextConfig, params: dict, cache: dict) -> dict:
-    """The runners that forward() uses for this (params, cache) pair, built on
-    first use: the decode runner, the head and the batched prefill."""
-    key = (id(params), id(cache["k"][0]))
-    rs = _RUNNERS.get(key)
-    if rs is None or rs["decode"].params is not params or rs["decode"].cache is not cache:
-        _RUNNERS.clear()
-        dev = cache["k"][0].device
-        r = DecodeRunner(cfg, params, cache, device=dev)
-        rs = {"decode": r, "head": HeadRunner(cfg, params, dev), "prefill": None}
-        _RUNNERS[key] = rs
-    return rs
+    """The runners one forward() call uses for this (params, cache) pair: the
+    decode runner and the head (the batched prefill is added when needed).
+    They are built per call and dropped when it returns, so no module state
+    keeps the caller's weights or cache alive after the caller lets go of
+    them (the buffers come back from torch's caching allocator)."""
+    dev = cache["k"][0].device
+    return {"decode": DecodeRunner(cfg, params, cache, device=dev), "head": HeadRunner(cfg, params, dev),
+            "prefill": None}
 
 
 def runner_for(cfg: TextConfig, params: dict, cache: dict) -> DecodeRunner:
-    """The DecodeRunner bound to this (params, cache) pair, built on first use."""
-    return _runners_for(cfg, params, cache)["decode"]
+    """A DecodeRunner bound to this (params, cache) pair (a new one per call;
+    it references both for as long as the caller keeps it)."""
+    return DecodeRunner(cfg, params, cache, device=cache["k"][0].device)
 
 
 def forward(cfg: TextConfig, mesh, params: dict, tokens, positions, cache: dict, write_at, masks: dict, kv_len: int,

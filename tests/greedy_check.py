@@ -9,20 +9,30 @@ import numpy as np
 from oracle import twin
 
 
-def check_stream(cfg, params_cpu, prompt, gen, max_len, tie=2e-3, what="stream"):
+# the tiny model's logits are ~N(0, 0.006): the GPU's measured max |d| against the
+# oracle is 1.2e-4 (one bf16 ulp at 0.02), so a flipped argmax needs an oracle
+# top-two gap within 2 x 1.2e-4
+TINY_TIE = 2.5e-4
+
+
+def check_stream(cfg, params_cpu, prompt, gen, max_len, tie=TINY_TIE, what="stream"):
     """gen = the GPU's first token after the prompt, then its decode tokens.
-    Returns the teacher-forced agreement count; asserts the near-tie rule."""
+    Returns the teacher-forced agreement count; asserts the near-tie rule and
+    that every step the oracle does not call a near tie agrees."""
     logits, _ = twin.prefill_then_decode(cfg, params_cpu, prompt, len(gen) - 1, max_len, all_logits=False,
                                          forced=gen)
     rows = logits.numpy()
-    agree = 0
+    agree, near = 0, 0
     for s, t in enumerate(gen):
         best = int(np.argmax(rows[s]))
+        top2 = np.sort(rows[s])[-2:]
+        near += float(top2[1] - top2[0]) <= tie
         if t == best:
             agree += 1
             continue
         gap = float(rows[s][best] - rows[s][t])
         print(f"{what}: step {s} token {t} vs oracle {best}, oracle gap {gap:.3e}")
         assert gap <= tie, f"{what}: step {s} is not a near tie ({gap:.3e})"
-    print(f"{what}: teacher-forced agreement {agree}/{len(gen)}")
+    print(f"{what}: teacher-forced agreement {agree}/{len(gen)} ({near} oracle near ties)")
+    assert agree >= len(gen) - near
     return agree

@@ -124,3 +124,42 @@ def test_missing_library_fails_loudly(tmp_path, monkeypatch):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises((ImportError, OSError)):
         _lib.lib()
+
+
+@pytest.mark.parametrize("grouped", [0, 1])
+@pytest.mark.parametrize("max_tiles,ncol", [(256, 22), (256, 1), (17, 5), (9, 3), (1, 1), (64, 11)])
+def test_gemm_tile_order_covers_each_live_tile_once(lib, grouped, max_tiles, ncol):
+    """The MFMA GEMM's block -> tile map (the library's own code, run on the
+    host): with any live tile count up to the grid's maximum, every (row tile,
+    column tile) is computed by exactly one block and no block computes a tile
+    past the live count.  Plain tiling always runs at mtiles == max_tiles."""
+    grid = (max_tiles * ncol + 7) // 8 * 8
+    out = (ctypes.c_int32 * (2 * grid))()
+    lives = range(max_tiles + 1) if grouped else [max_tiles]
+    for mt in lives:
+        assert lib.g4mi_selftest_tile_order(mt, max_tiles, ncol, grouped, out, 2 * grid) == 0
+        seen = {}
+        for b in range(grid):
+            tx, ty = out[2 * b], out[2 * b + 1]
+            if tx < 0:
+                assert ty < 0
+                continue
+            assert 0 <= tx < mt and 0 <= ty < ncol, (mt, b, tx, ty)
+            assert (tx, ty) not in seen, f"tile {(tx, ty)} computed by blocks {seen[(tx, ty)]} and {b} (live {mt})"
+            seen[(tx, ty)] = b
+        assert len(seen) == mt * ncol, (mt, len(seen))
+
+
+def test_gemm_tile_order_groups_row_tiles_per_xcd(lib):
+    """Plain tiling: consecutive blocks go to the 8 XCDs in turn, and each XCD's
+    run holds consecutive tile ids (groups of 8 row tiles, column tiles inner)."""
+    mt, ncol = 32, 4
+    grid = mt * ncol
+    out = (ctypes.c_int32 * (2 * grid))()
+    assert lib.g4mi_selftest_tile_order(mt, mt, ncol, 0, out, 2 * grid) == 0
+    per = grid // 8
+    for x in range(8):
+        tiles = [(out[2 * (y * 8 + x)], out[2 * (y * 8 + x) + 1]) for y in range(per)]
+        # XCD x runs ids [x*per, (x+1)*per): one group of 8 row tiles x 2 column tiles
+        assert {t[0] for t in tiles} == set(range((x // 2) * 8, (x // 2) * 8 + 8)), (x, tiles)
+    _expect(lib.g4mi_selftest_tile_order(5, 4, 1, 1, out, 2 * grid), EINVAL, "selftest_tile_order")

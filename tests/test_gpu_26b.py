@@ -50,8 +50,11 @@ from oracle import twin
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-TIE = 2e-3         # declared near tie: the oracle's top two logits within this
-LOGIT_TOL = 2e-3   # logits are ~N(0, 0.02); a bf16 ulp at 0.1 is 4.9e-4
+# logits are ~N(0, 0.021): a bf16 ulp at 0.1 is 4.9e-4, the measured max |d|
+# against the oracle; a flipped argmax needs the oracle's top-two gap within
+# 2 x that
+LOGIT_TOL = 1e-3
+TIE = 1e-3         # declared near tie: the oracle's top two logits within this
 P, N_DEC, MAX_LEN = 54, 8, 1024
 
 
@@ -81,18 +84,22 @@ def _rnd(shape, g, std):
 
 
 def _check_near_ties(got_tok, exp_logits, what):
-    """Each got_tok[s] is the argmax of exp_logits[s] or within TIE of its max."""
-    agree = 0
+    """Each got_tok[s] is the argmax of exp_logits[s] or within TIE of its max,
+    and every step whose oracle top-two gap exceeds TIE agrees."""
+    agree, near = 0, 0
     for s, t in enumerate(got_tok):
         row = exp_logits[s]
         best = int(np.argmax(row))
+        top2 = np.sort(row)[-2:]
+        near += float(top2[1] - top2[0]) <= TIE
         if t == best:
             agree += 1
             continue
         gap = float(row[best] - row[t])
         print(f"{what}: step {s} token {t} vs oracle {best}, oracle logit gap {gap:.3e}")
         assert gap <= TIE, f"{what}: step {s} is not a near tie ({gap:.3e})"
-    print(f"{what}: teacher-forced agreement {agree}/{len(got_tok)}")
+    print(f"{what}: teacher-forced agreement {agree}/{len(got_tok)} ({near} oracle near ties)")
+    assert agree >= len(got_tok) - near
     return agree
 
 
@@ -137,7 +144,7 @@ def test_ffn_in_selects_the_oracle_experts(m26, layer):
         same_act.append((ga == a_ref.double()).double().mean().item())
         assert torch.allclose(ga, a_ref.double(), rtol=2.0 ** -6, atol=1e-4), case
     print(f"layer {layer}: activation bit-identical fraction {np.mean(same_act):.4f}")
-    assert np.mean(same_act) >= 0.98
+    assert np.mean(same_act) >= 0.999  # measured 0.9998
 
 
 @pytest.mark.parametrize("combine", ["bf16_running", "f32"])
@@ -170,7 +177,7 @@ def test_ffn_out_at_26b_shapes(m26, combine):
     same = (got == ref).double().mean().item()
     print(f"{combine}: moe_out bit-identical {same:.4f}, max|d| {(got - ref).abs().max().item():.3e}")
     assert (got - ref).abs().max().item() <= ref.abs().max().item() * 2.0 ** -6
-    assert same >= 0.95
+    assert same >= 0.99  # measured 1.0
 
 
 def test_lm_head_over_262144_rows(m26):
@@ -205,7 +212,7 @@ def test_lm_head_over_262144_rows(m26):
     same = np.mean(np.abs(got - ref) <= 4 * np.spacing(np.abs(ref)))
     err = np.abs(got - ref).max()
     print(f"lm_head: {same:.5f} of 262,144 logits equal, max|d| {err:.3e}, token {int(tok.item())}")
-    assert same >= 0.99 and err <= 2.0 ** -7 * np.abs(ref).max()
+    assert same >= 0.999 and err <= 2.0 ** -7 * np.abs(ref).max()  # measured 0.9999, 1.2e-4
     assert int(tok.item()) == int(np.argmax(got))  # first index of the maximum of the kernel's logits
     best = int(np.argmax(ref))
     assert int(tok.item()) == best or ref[best] - ref[int(tok.item())] <= TIE
@@ -269,7 +276,7 @@ def test_decode_runner_logits_match_oracle(m26, gen26):
             if set(o) != set(gsel):
                 print(f"step {s} layer {layer}: gpu {gsel} oracle {o}")
     print(f"decode expert sets identical: {np.mean(same):.3f}")
-    assert np.mean(same) >= 0.9
+    assert np.mean(same) >= 0.99
 
 
 def test_batched_prefill_256_matches_oracle(m26):
@@ -382,3 +389,88 @@ def test_batch_engine_matches_batch1_runner(m26):
         assert corr >= 0.9999 and err.max() <= LOGIT_TOL
         _check_near_ties(toks[1:], exp, f"batch row {b}")
         del r, pr, cache
+
+
+def test_batch_decode_at_8k_contexts(m26):
+    """Config 5's decode half at its context length: eight sequences
+    prefilled to 8,150-8,190 tokens (staggered, each through the batched
+    prefill into pages handed out by one PagePool), then 4 batched greedy
+    steps (model.py:402-408 masks per position; engine.py:71-83).  At B = 8
+    and these lengths every layer runs the long-range attention path (8-wave
+    scores and P.V kernels and the split reduction launch; asserted from the
+    split counts).  Each row's logits at every step against the batch-1
+    decode runner fed the same tokens, and rows 0 and 7 at the last step
+    against the oracle run on that row's K/V cache rows copied to the host."""
+    cfg, params, cpu, po = m26
+    lens = (8150, 8156, 8161, 8167, 8172, 8178, 8184, 8190)
+    B, n_steps, max_len = 8, 4, 8448
+    prompts = [np.random.default_rng(60 + b).integers(0, cfg.vocab_size, size=n).tolist()
+               for b, n in enumerate(lens)]
+    eng = BatchEngine(cfg, params, batch=B, max_len=max_len, device=DEV)
+    # both layer kinds take the 8-wave path: span > 64 positions per split
+    for lt, span in ((SLIDING, min(cfg.sliding_window, max_len)), (FULL, max_len)):
+        assert span > 64 * eng.runner.splits[lt], (lt, eng.runner.splits[lt])
+    firsts = [eng.add(b, p) for b, p in enumerate(prompts)]
+    # the pool mapped each sequence's pages out of one shared pool, in add order
+    owned = [set(o) for o in eng.pool.owned]
+    assert all(not (owned[a] & owned[b]) for a in range(B) for b in range(a + 1, B))
+    blog = []
+    for _ in range(n_steps):
+        eng.step()
+        blog.append(eng.runner.logits_bf.float().cpu().clone())
+    torch.cuda.synchronize()
+    hist = eng.runner.hist.cpu()
+    cap = np.float32(cfg.final_logit_softcapping)
+    got_all = [np.stack([(torch.tanh(blog[s][b] / cap) * cap).numpy() for s in range(n_steps)]) for b in range(B)]
+
+    # every row against the batch-1 runner (its own dense cache) fed the same tokens
+    cache1 = gm.init_cache(cfg, None, 1, max_len, device=DEV)
+    r = gm.DecodeRunner(cfg, params, cache1, device=DEV)
+    pr = gm.PrefillRunner(cfg, params, cache1, 8192, device=DEV, rope=r.rope)
+    prompt_d = torch.empty(8192, dtype=torch.int32, device=DEV)
+    for b, p in enumerate(prompts):
+        n = len(p)
+        toks = hist[b, n:n + n_steps + 1].tolist()
+        assert toks[0] == firsts[b]
+        prompt_d[:n].copy_(torch.tensor(p, dtype=torch.int32))
+        pr.run(prompt_d, n)
+        r.pos.fill_(n - 1)
+        r.head(*pr.last_row(n))
+        first = int(r.tok.item())
+        exp_rows = []
+        for s in range(n_steps):
+            r.set_state(toks[s], n + s)
+            r.launch("bf16_running", advance=False)
+            exp_rows.append(r.logits.cpu().clone())
+        torch.cuda.synchronize()
+        exp = torch.stack(exp_rows).numpy()
+        got = got_all[b]
+        err = np.abs(got - exp)
+        corr = np.corrcoef(got.ravel(), exp.ravel())[0, 1]
+        print(f"8K row {b} ({n} tokens): max|d| {err.max():.3e} corr {corr:.7f} first {toks[0]} vs {first}")
+        assert toks[0] == first
+        assert corr >= 0.9999 and err.max() <= LOGIT_TOL
+        _check_near_ties(toks[1:], exp, f"8K batch row {b} vs batch-1")
+    del r, pr, cache1
+    torch.cuda.empty_cache()
+
+    # rows 0 and 7, last step: the oracle (model.py:333-386 at one position)
+    # on the row's own cache rows, gathered through its page table
+    for b in (0, B - 1):
+        n = len(prompts[b])
+        pos = n + n_steps - 1
+        tok = int(hist[b, pos])
+        oc = twin.init_cache(cfg, 1, max_len)
+        for i in range(cfg.num_hidden_layers):
+            k, v = gm.cache_positions(eng.cache, i, batch=b, upto=pos)
+            oc["k"][i][0, :pos] = k.cpu()
+            oc["v"][i][0, :pos] = v.cpu()
+        lg, _ = twin.forward(cfg, po, np.array([[tok]]), np.array([pos]), oc, pos,
+                             twin.decode_masks(cfg, max_len, pos), max_len, False, None)
+        exp = lg[0, 0].numpy()
+        got = got_all[b][n_steps - 1]
+        err = np.abs(got - exp)
+        corr = np.corrcoef(got, exp)[0, 1]
+        print(f"8K row {b} at position {pos} vs oracle: max|d| {err.max():.3e} corr {corr:.7f}")
+        assert corr >= 0.9999 and err.max() <= LOGIT_TOL
+        _check_near_ties([int(hist[b, pos + 1])], exp[None], f"8K batch row {b} vs oracle")

@@ -80,6 +80,27 @@ def test_prompt_lengths_across_prefill_buckets(setup, plen):
     check_stream(cfg, twin.random_params(cfg, 0), prompt, gen, max_len, what=f"prompt of {plen}")
 
 
+@pytest.mark.parametrize("mode", ["batched", "stepwise"])
+def test_prompt_in_the_last_page_on_a_fresh_engine(setup, mode):
+    """A prompt of max_len - 10 tokens on a fresh Engine: its decode (and, when
+    stepwise, head) graphs are first captured while the prompt's K/V rows sit
+    in the cache's last page, and the capture's warm step (run at the scratch
+    position max_len - 1) must leave those rows intact.  The tokens equal
+    those of an engine whose graphs were captured on a short prompt, and
+    every one is the teacher-forced oracle's greedy choice."""
+    cfg, eng, _, _ = setup
+    plen = MAX_LEN - 10
+    prompt = np.random.default_rng(7).integers(0, cfg.vocab_size, size=plen).astype(np.int64)
+    warm = Engine(None, MAX_LEN, 1, 64, cfg=cfg, params=eng.params, device=DEV, prefill=mode)
+    list(warm.generate([1, 2, 3], max_new_tokens=3, temperature=0.0, stop_ids=()))
+    want = [e["token"] for e in warm.generate(prompt.tolist(), max_new_tokens=9, temperature=0.0, stop_ids=())]
+    fresh = Engine(None, MAX_LEN, 1, 64, cfg=cfg, params=eng.params, device=DEV, prefill=mode)
+    got = [e["token"] for e in fresh.generate(prompt.tolist(), max_new_tokens=9, temperature=0.0, stop_ids=())]
+    print(f"{mode}: fresh {got} warmed {want}")
+    assert got == want
+    check_stream(cfg, twin.random_params(cfg, 0), prompt, got, MAX_LEN, what=f"{mode} prompt of {plen}")
+
+
 def test_step_functions_calling_convention(setup):
     cfg, eng, prompt, gen_o = setup
     eng.reset_cache()

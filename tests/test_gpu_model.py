@@ -6,10 +6,10 @@ the prefill path (dense-MoE combine), then 32 greedy decode steps.
 
 Checks, against the CPU oracle on the same weights:
   * the GPU weight generator reproduces the numpy generator bit for bit;
-  * logits at all 160 positions: corr >= 0.9999 and max |d| <= 2e-3 (the
+  * logits at all 160 positions: corr >= 0.9999 and max |d| <= 5e-4 (the
     logits are ~N(0, 0.03); a bf16 ulp at 0.1 is 4.9e-4);
   * teacher-forced greedy tokens: identical, except where the oracle's top
-    two logits are within 2e-3 (a declared near tie);
+    two logits are within 2.5e-4 (a declared near tie);
   * per-layer top-k expert indices at every position: >= 99% identical sets
     (deep layers see hidden states that differ by bf16 roundings; the
     bit-exact check on identical inputs is in test_gpu_moe.py).
@@ -22,13 +22,14 @@ import torch
 from gemma4_mi import model as gm
 from gemma4_mi.config import tiny_parity_config
 from gemma4_mi.weights import init_random_params
-from greedy_check import check_stream
+from greedy_check import TINY_TIE, check_stream
 from oracle import twin
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 P, N_DEC, MAX_LEN = 128, 32, 256
-TIE = 2e-3
+LOGIT_TOL = 5e-4  # measured max |d| 1.2e-4 (one bf16 ulp of logits ~N(0, 0.006))
+TIE = TINY_TIE
 
 
 @pytest.fixture(scope="module")
@@ -73,13 +74,15 @@ def test_prefill_and_teacher_forced_decode(c1):
     corr = np.corrcoef(got.ravel(), exp.ravel())[0, 1]
     print(f"logits: max|d|={err.max():.3e} corr={corr:.7f}")
     assert corr >= 0.9999
-    assert err.max() <= 2e-3
+    assert err.max() <= LOGIT_TOL
 
     am_g, am_o = got.argmax(-1), exp.argmax(-1)
     srt = np.sort(exp, -1)
     gap = srt[:, -1] - srt[:, -2]
     mism = np.nonzero(am_g != am_o)[0]
-    print(f"greedy argmax: {len(mism)} of {len(am_o)} positions differ; near ties there: {gap[mism]}")
+    print(f"greedy argmax: {len(mism)} of {len(am_o)} positions differ; near ties there: {gap[mism]}; "
+          f"{int(np.sum(gap <= TIE))} oracle near ties in all")
+    assert len(mism) <= int(np.sum(gap <= TIE))
     for i in mism:
         assert exp[i, am_o[i]] - exp[i, am_g[i]] <= TIE, f"position {i}: not a near tie"
 
@@ -128,7 +131,7 @@ def test_batched_prefill_matches_oracle(c1):
     err = np.abs(got - exp)
     corr = np.corrcoef(got, exp)[0, 1]
     print(f"batched prefill, last row logits: max|d|={err.max():.3e} corr={corr:.7f}")
-    assert corr >= 0.9999 and err.max() <= 2e-3
+    assert corr >= 0.9999 and err.max() <= LOGIT_TOL
     assert int(r.tok.item()) == gen_o[0] and int(r.pos.item()) == P and int(r.hist[P].item()) == gen_o[0]
 
     ref_cache = gm.init_cache(cfg, None, 1, MAX_LEN, device=DEV)
@@ -179,7 +182,7 @@ def test_long_context_prefill_then_decode():
     decode steps, against the oracle: the full-attention layer then attends to
     more than 1,024 positions, so the decode step's split-K attention runs its
     two-level partial reduction (17-18 splits of 64 positions).  Same bar as
-    the short prompt: logits corr >= 0.9999, max |d| <= 2e-3, greedy tokens
+    the short prompt: logits corr >= 0.9999, max |d| <= 5e-4, greedy tokens
     equal but for declared near ties."""
     cfg = tiny_parity_config()
     params_cpu = twin.random_params(cfg, 0)
@@ -204,6 +207,6 @@ def test_long_context_prefill_then_decode():
     err = np.abs(got - exp)
     corr = np.corrcoef(got.ravel(), exp.ravel())[0, 1]
     print(f"long context logits: max|d|={err.max():.3e} corr={corr:.7f}")
-    assert corr >= 0.9999 and err.max() <= 2e-3
+    assert corr >= 0.9999 and err.max() <= LOGIT_TOL
     for i in np.nonzero(got.argmax(-1) != exp.argmax(-1))[0]:
         assert exp[i].max() - exp[i, got[i].argmax()] <= TIE, f"step {i}: not a near tie"

@@ -30,7 +30,8 @@ from oracle import twin
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-TIE = 2e-3
+LOGIT_TOL = 5e-4  # measured max |d| 1.2e-4 against the HF fixture and the oracle
+TIE = 2.5e-4
 
 
 def _bits(t):
@@ -158,7 +159,7 @@ def test_parity_procedure_prefill(parity):
     err = np.abs(got[rows] - exp)
     corr = np.corrcoef(got[rows].ravel(), exp.ravel())[0, 1]
     print(f"prefill vs HF fixture: max|d|={err.max():.3e} corr={corr:.7f}")
-    assert corr >= 0.9999 and err.max() <= 2e-3
+    assert corr >= 0.9999 and err.max() <= LOGIT_TOL
     mism = np.nonzero(got.argmax(-1) != fx["argmax"][:seq])[0]
     assert all(fx["top2_gap"][i] <= TIE for i in mism), mism
     assert bool((logits[0, seq:] == 0).all())  # padded rows are not computed
@@ -191,7 +192,7 @@ def test_parity_procedure_decode_step(parity):
     olg, _ = twin.forward(cfg, params_cpu, ids[:, pref_len:pref_len + 1], np.array([pref_len]), oc, pref_len,
                           twin.decode_masks(cfg, bucket, pref_len), bucket, False)
     oexp = olg[0, 0].numpy()
-    assert np.abs(dgot - oexp).max() <= 2e-3 and np.corrcoef(dgot, oexp)[0, 1] >= 0.9999
+    assert np.abs(dgot - oexp).max() <= LOGIT_TOL and np.corrcoef(dgot, oexp)[0, 1] >= 0.9999
 
 
 def test_forward_rows_are_sequences(parity):
@@ -259,3 +260,25 @@ def test_engine_batch_rows_and_reset_cache():
     torch.cuda.synchronize()
     for pool in eng.cache["k"] + eng.cache["v"]:
         assert int(torch.count_nonzero(pool).item()) == 0
+
+
+def test_forward_keeps_no_reference_to_params_or_cache():
+    """forward() builds its runners per call: once the caller drops its params
+    and cache, nothing in the library keeps them (or their HBM) alive."""
+    import gc
+    import weakref
+
+    cfg = tiny_parity_config()
+    params = init_random_params(cfg, 0, device=DEV)
+    cache = M.init_cache(cfg, None, 1, 256, device=DEV)
+    ids = np.arange(8, dtype=np.int32)[None]
+    logits, cache = M.forward(cfg, None, params, ids, np.arange(8), cache, 0, M.prefill_masks(cfg, 8, 8), kv_len=8,
+                              dense_moe=True)
+    logits2, cache = M.forward(cfg, None, params, ids[:, :1], np.array([8]), cache, 8, M.decode_masks(cfg, 256, 8),
+                               kv_len=256, dense_moe=False)
+    torch.cuda.synchronize()
+    refs = [weakref.ref(params["embed"]), weakref.ref(params["layers.0.q_proj"]), weakref.ref(cache["k"][0]),
+            weakref.ref(cache["page_table"])]
+    del params, cache, logits, logits2
+    gc.collect()
+    assert all(r() is None for r in refs), [r() is None for r in refs]

@@ -6,9 +6,9 @@ This follows the reference's own parity procedure (tests/test_parity.py:
 29-159: a tiny HF Gemma-4 with eager attention/experts as the oracle of the
 model), on the same seeded weights the GPU path uses.  Tolerances are the
 reference's bar tightened to this build's: corr >= 0.9999 and max |d| <=
-2e-3 on the logit rows the fixture keeps (the logits are ~N(0, 0.03)),
+5e-4 on the logit rows the fixture keeps (the logits are ~N(0, 0.03)),
 greedy argmax identical at all 160 positions except declared near ties
-(HF's top-two gap <= 2e-3), the generated ids identical, and >= 99% of the
+(HF's top-two gap <= 5e-4), the generated ids identical, and >= 99% of the
 per-layer top-k expert sets identical (HF sums experts in another order, so
 rare near-tie routes may differ).
 """
@@ -43,7 +43,8 @@ def test_logit_rows(run):
     err = np.abs(got - exp).max()
     corr = np.corrcoef(got.ravel(), exp.ravel())[0, 1]
     assert corr >= 0.9999, corr
-    assert err <= 2e-3, err
+    print(f"oracle vs HF fixture: max|d| {err:.3e} corr {corr:.7f}")
+    assert err <= 5e-4, err
 
 
 def test_greedy_argmax_and_generated_ids(run):
@@ -51,7 +52,7 @@ def test_greedy_argmax_and_generated_ids(run):
     p = int(fx["prompt_len"])
     am = logits.argmax(-1)
     diff = np.nonzero(am != fx["argmax"])[0]
-    assert all(fx["top2_gap"][i] <= 2e-3 for i in diff), diff
+    assert all(fx["top2_gap"][i] <= 5e-4 for i in diff), diff
     assert len(diff) <= 2
     assert gen[: len(fx["ids"]) - p] == fx["ids"][p:].tolist()
 
