@@ -796,7 +796,51 @@ def run_batch_decode(args) -> dict:
     }
 
 
-WORKLOADS = {"decode": run_decode, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup,
+def run_decode_eager(args) -> dict:
+    """The batch-1 decode step of the 26B-A4B-shaped model launched kernel by
+    kernel on the stream (no HIP graph), at the positions the decode workload
+    times (a 54-token prompt, then --steps greedy steps, the full layers sized
+    for 8,192 positions as in the engine's short-span graph).  For per-kernel
+    hardware counters: the launches are the decode graph's, in its order.
+    value = tok/s of the eager launches (host launch cost included)."""
+    import numpy as np
+    import torch
+
+    from gemma4_mi import model as gm
+    from gemma4_mi.config import gemma4_26b_a4b_config
+    from gemma4_mi.weights import init_random_params
+
+    cfg = gemma4_26b_a4b_config()
+    seed, p_len, steps = 3, args.prompt_len, args.steps
+    params = init_random_params(cfg, seed, device="cuda:0")
+    cache = gm.init_cache(cfg, None, 1, args.max_len, device="cuda:0")
+    r = gm.DecodeRunner(cfg, params, cache, device="cuda:0")
+    pr = gm.PrefillRunner(cfg, params, cache, 256, device="cuda:0", rope=r.rope)
+    prompt = np.random.default_rng(seed).integers(0, cfg.vocab_size, size=p_len)
+    pr.run(torch.tensor(prompt, dtype=torch.int32, device="cuda:0"), p_len)
+    r.pos.fill_(p_len - 1)
+    r.head(*pr.last_row(p_len))
+    r.set_full_span(min(8192, args.max_len))
+    _log(f"prefill of {p_len} tokens done; {args.warmup} + {steps} eager steps")
+    for _ in range(args.warmup):
+        r.launch("bf16_running", advance=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        r.launch("bf16_running", advance=True)
+        if steps <= 16:  # a counter-collecting profiler makes each step slow: show progress
+            torch.cuda.synchronize()
+            _log(f"eager step {i + 1}/{steps}")
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / max(steps, 1)
+    return {"metric": "batch-1 decode tok/s, eager launches (profiling)", "value": 1000.0 / ms, "unit": "tok/s",
+            "ms_per_step": ms, "dtype": "bf16",
+            "config": {"workload": "gemma4-26B-A4B-shaped random-init decode, batch 1, eager launches",
+                       "prompt_len": p_len, "positions": [p_len + args.warmup, p_len + args.warmup + steps]},
+            "roofline": None}
+
+
+WORKLOADS = {"decode": run_decode, "decode_eager": run_decode_eager, "moe_block": run_moe_block, "copy": run_copy, "gateup": run_gateup,
              "prefill": run_prefill, "batch_decode": run_batch_decode, "attention": run_attention}
 
 
