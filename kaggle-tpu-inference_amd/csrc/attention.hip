@@ -25,6 +25,7 @@
 // Device-side positions and page indices are range-checked: an out-of-range
 // position attends to nothing (ctx = 0, no cache write) and an out-of-range
 // page entry is skipped, so bad inputs cannot address outside the buffers.
+#include <cstdlib>
 #include <mutex>
 
 #include "capi_util.h"
@@ -117,9 +118,16 @@ __device__ __forceinline__ void stage_store(const PtStage<NT>& s, int* ptl) {
   for (int r = 0; r < 512 / NT; ++r) ptl[threadIdx.x + NT * r] = s.v[r];
 }
 
+// The maximum over the 64 lanes, in every lane: the DPP steps of group_sum
+// inside each row of 16 lanes, then two ds_bpermute steps (max is exact, so
+// any order gives the same bits).
 __device__ __forceinline__ float wave_max_bfly(float m) {
-#pragma unroll
-  for (int s = 1; s < 64; s <<= 1) m = fmaxf(m, __shfl_xor(m, s, kWave));
+  m = fmaxf(m, dpp_f<kDppXor1>(m));
+  m = fmaxf(m, dpp_f<kDppXor2>(m));
+  m = fmaxf(m, dpp_f<kDppHalfMirror>(m));
+  m = fmaxf(m, dpp_f<kDppMirror>(m));
+  m = fmaxf(m, __shfl_xor(m, 16, kWave));
+  m = fmaxf(m, __shfl_xor(m, 32, kWave));
   return m;
 }
 
@@ -993,6 +1001,352 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int3
   }
 }
 
+// ------------------------------------------------------------------ one launch per layer, one XCD per KV head
+// Batch 1, 8 KV heads (the sliding layers: model.py:207-213 with the window
+// mask of model.py:402-408), every split at most kChunkMin positions and at
+// most kLocalLen positions attended.  The 8 XCDs take a launch's blocks in
+// turn (block b runs on XCD b % 8, checked on the host before the path is
+// used), so the blocks b, b + 8, b + 16, ... share one XCD and its L2.  A
+// block serves KV head kv = its XCD, and role r = b / 8:
+//   r < n_split_max (scores): split r's scores, as attn_qk_kernel computes
+//     them (q norm + RoPE, the append, MFMA scores, softcap, the split's max
+//     and sum of exp), stored with plain stores (they stay in the XCD's L2);
+//     then the block counts in on its head's counter;
+//   r - n_split_max = x < D / kSliceD (P.V): requests the V rows of head
+//     dims [x * kSliceD, +kSliceD) at every attended position at its start,
+//     rebuilds the new V row of position pos from v_raw (the rows were
+//     requested before the append), waits until all n_eff splits have
+//     counted in (device-scope polls, a bounded wait), reads the head's
+//     scores and statistics from the L2 and sums P.V in the order of
+//     pv_short (each lane its positions in step order, a DPP sum over the
+//     lanes of a step, then the waves in order), extended to kLocalLen
+//     positions.
+// The last P.V block of a head resets the head's counters for the next
+// launch.
+constexpr int kLocalLen = 1024;
+constexpr int kLocalPage = 64;       // cache page size of this path (positions per page)
+constexpr int kLocalSpin = 1 << 22;  // polls before a waiting block gives up (~0.1 s)
+
+__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15; }
+
+template <int D, int G, bool DPT>
+__device__ __forceinline__ void attn_local_scores(
+    const AttnDims& a, const Range& R, int kv, int split, int pos, const uint16_t* __restrict__ q_raw,
+    const uint16_t* __restrict__ k_raw, const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm,
+    const uint16_t* __restrict__ k_norm, const uint16_t* __restrict__ rope_cos, const uint16_t* __restrict__ rope_sin,
+    uint16_t* __restrict__ k_pages, uint16_t* __restrict__ v_pages, const int32_t* __restrict__ page_table,
+    int append, float* ws_scores, float* ws_stats, unsigned int* cnt) {
+  constexpr int PL = D / 64;
+  constexpr int NT = 256;
+  constexpr int KS = D / 32;
+  static_assert(G <= 2, "waves 0..G-1 take the q heads, waves 2 and 3 the new K and V");
+  if (threadIdx.x >= NT) return;  // the fifth wave polls in the P.V role only
+  __shared__ __align__(16) uint16_t qa[16 * D];
+  __shared__ __align__(16) uint16_t kn16[D];
+  __shared__ float knew[D];
+  __shared__ float vnew[D];
+  __shared__ float sc[G][kChunkMin];
+  __shared__ int ptl[512];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int start = R.lo + split * R.chunk;
+  const int end = min(R.lo + R.len, start + R.chunk);
+  const int npos = end - start;
+  const PtRow<DPT> pt_row = pt_row_of<DPT>(a, page_table, 0);
+  const int kg = lane >> 4, col = lane & 15;
+  constexpr int PG = kLocalPage;
+  const int first = start / PG;
+  const PtStage<NT> pts = stage_load<NT>(a, pt_row, first);
+  const int jc0 = min(wave * 16 + col, npos - 1);
+  const int pe0 = pt_row[(start + jc0) / PG];
+  // prologue rows: wave w < G takes q head w; the split that ends at pos
+  // appends the new K (wave 2) and V (wave 3)
+  const int so = lane * PL, jo = so % (D / 2);
+  const bool mine = append && (end == pos + 1);
+  float qx[PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
+  load_slice<PL>(q_raw + ((size_t)kv * G + min(wave, G - 1)) * D + so, qx);
+  load_slice<PL>(q_norm + so, qw);
+  load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
+  load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
+  {
+    const uint16_t* kr = mine ? k_raw + (size_t)kv * D : q_norm;
+    const uint16_t* vr = (mine && v_raw != nullptr) ? v_raw + (size_t)kv * D : kr;
+    load_slice<PL>((wave == 2 ? kr : vr) + so, kvx);
+    load_slice<PL>((mine ? k_norm : q_norm) + so, kw);
+  }
+  // this wave's K tile (positions 16 w .. 16 w + 15 of the split)
+  u32x4 bt[KS];
+  const bool valid0 = pe0 >= 0 && pe0 < a.num_pages;
+  const long long ot = valid0 ? ((((long long)pe0 * a.KV + kv) * PG) + ((start + jc0) % PG)) * (long long)D : -1ll;
+  {
+    const uint16_t* kp = k_pages + max(ot, 0ll) + 8 * kg;
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) bt[s2] = ld16((const u32x4*)(kp + 32 * s2));
+  }
+  for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
+  if (wave < G) {
+    norm_rope_slice<D>(qx, qw, cs, sn, a.eps, true);
+#pragma unroll
+    for (int i = 0; i < PL; ++i) qa[wave * D + so + i] = f2bf(qx[i]);
+  }
+  if (mine && wave >= 2) {
+    norm_rope_slice<D>(kvx, wave == 2 ? kw : nullptr, cs, sn, a.eps, wave == 2);
+    float* dst = (wave == 2) ? knew : vnew;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      dst[so + i] = kvx[i];
+      if (wave == 2) kn16[so + i] = f2bf(kvx[i]);
+    }
+  }
+  stage_store<NT>(pts, ptl);
+  lds_barrier();
+  if (mine) {
+    const int pe = ptl[pos / PG - first];
+    if (pe >= 0 && pe < a.num_pages) {
+      const long long off = ((((long long)pe * a.KV + kv) * PG) + (pos % PG)) * (long long)D;
+      for (int d = tid; d < D; d += NT) {
+        k_pages[off + d] = f2bf(knew[d]);
+        v_pages[off + d] = f2bf(vnew[d]);
+      }
+    }
+  }
+  u32x4 af[KS];
+#pragma unroll
+  for (int s2 = 0; s2 < KS; ++s2) af[s2] = *(const u32x4*)(qa + col * D + 32 * s2 + 8 * kg);
+  const int ntiles = (npos + 15) >> 4;
+  if (wave < ntiles) {
+    const int j = wave * 16 + col;
+    const bool isnew = mine && (start + j == pos);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s2 = 0; s2 < KS; ++s2) {
+      u32x4 kb = bt[s2];
+      if (mine) kb = isnew ? *(const u32x4*)(kn16 + 32 * s2 + 8 * kg) : kb;
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[s2]),
+                                                    __builtin_bit_cast(bf16x8, kb), acc, 0, 0, 0);
+    }
+    const bool ok = (ot >= 0) || isnew;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G && j < npos) {
+        float sv = rbf(acc[i]);
+        if (a.softcap > 0.0f) sv = tanhf(sv / a.softcap) * a.softcap;
+        sc[h][j] = ok ? sv : -INFINITY;
+      }
+    }
+  }
+  lds_barrier();
+  if (wave < G) {
+    const int g = wave;
+    float m = -INFINITY;
+    for (int j = lane; j < npos; j += 64) m = fmaxf(m, sc[g][j]);
+    m = wave_max_bfly(m);
+    float* srow = ws_scores + ((size_t)kv * G + g) * a.lmax + (start - R.lo);
+    float l = 0.0f;
+    for (int j = lane; j < npos; j += 64) {
+      const float s2 = sc[g][j];
+      l += (s2 == -INFINITY) ? 0.0f : expf(s2 - m);
+      srow[j] = s2;
+    }
+    l = group_sum<64>(l);
+    if (lane == 0) {
+      const int h = kv * G + g;
+      ws_stats[(size_t)h * a.n_split_max + split] = m;
+      ws_stats[((size_t)a.NH + h) * a.n_split_max + split] = l;
+    }
+  }
+  // the block's scores and statistics (and its cache append) have reached
+  // the L2; then count in
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int D, int G, bool DPT>
+__device__ __forceinline__ void attn_local_pv(const AttnDims& a, const Range& R, int kv, int slice, int pos,
+                                              const uint16_t* __restrict__ k_raw, const uint16_t* __restrict__ v_raw,
+                                              const uint16_t* v_pages, const int32_t* __restrict__ page_table,
+                                              int append, const float* ws_scores, const float* ws_stats,
+                                              unsigned int* cnt, uint16_t* __restrict__ ctx) {
+  constexpr int PL = D / 64;
+  constexpr int NT = 256, NW = 4;
+  constexpr int LPS = kSliceD / 8, PPW = 64 / LPS, PPB = NW * PPW;
+  constexpr int NST = kLocalLen / PPB;     // V steps per lane at most
+  constexpr int SPT = G * kLocalLen / NT;  // scores per thread at most
+  __shared__ __align__(16) uint16_t vn16[D];
+  __shared__ float pr[G * kLocalLen];
+  __shared__ float red[NW * G * kSliceD];
+  __shared__ float mg[G], sg[G];
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int slot = lane % PPW, sub = lane / PPW;
+  const int d0 = slice * kSliceD + sub * 8;
+  const int len = R.len;
+  const int nst = (len + PPB - 1) / PPB;
+  constexpr int PG = kLocalPage;
+  const PtRow<DPT> pt_row = pt_row_of<DPT>(a, page_table, 0);
+  // the new V row's raw values, then the V slice at every attended position
+  float vx[PL], dummy[PL];
+  if (append && wave < NW) load_slice<PL>((v_raw != nullptr ? v_raw : k_raw) + (size_t)kv * D + lane * PL, vx);
+  // V steps in chunks of CH (a block-uniform branch per chunk, none inside:
+  // a chunk's LDS reads are then issued together); the rows of steps past
+  // the range are not requested and read as zero
+  constexpr int CH = 4;
+  static_assert(NST % CH == 0, "whole chunks");
+  u32x4 vv[NST];
+  bool okv[NST];
+  if (wave < NW) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int j = st * PPB + wave * PPW + slot;
+      okv[st] = false;
+      vv[st] = u32x4{0u, 0u, 0u, 0u};
+      if (st < nst) {  // block-uniform: no loads for the steps past the range
+        const int p = R.lo + min(j, len - 1);
+        const int pg = pt_row[p / PG];
+        const bool valid = pg >= 0 && pg < a.num_pages;
+        const long long off = ((((long long)(valid ? pg : 0) * a.KV + kv) * PG) + (p % PG)) * (long long)D;
+        vv[st] = ld16((const u32x4*)(v_pages + off + d0));
+        okv[st] = (j < len) && valid;
+      }
+    }
+    // wave 1 rebuilds the new V row (it waits for the loads above)
+    if (append && wave == 1) {
+      norm_rope_slice<D>(vx, nullptr, dummy, dummy, a.eps, false);
+#pragma unroll
+      for (int i = 0; i < PL; ++i) vn16[lane * PL + i] = f2bf(vx[i]);
+    }
+  } else if (lane == 0) {
+    // the fifth wave, with no loads of its own in flight (a wave's loads
+    // return in order, so a poll behind the V rows would see the count
+    // only after them), waits until every split of this head has counted in
+    int it = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < (unsigned)R.n_eff &&
+           ++it < kLocalSpin)
+      __builtin_amdgcn_s_sleep(1);
+  }
+  __syncthreads();
+  if (wave >= NW) return;
+  float sreg[SPT];
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const int idx = tid + NT * r, g = idx / kLocalLen, j = idx % kLocalLen;
+    sreg[r] = ws_scores[((size_t)kv * G + g) * a.lmax + min(j, len - 1)];
+  }
+  SplitStats<G, NW> sst = load_split_stats<G, NW>(a, R, kv, 0, wave, lane, ws_stats);
+  // this block has passed the wait: count out (the last P.V block of the
+  // head resets its counters at the end).  Issued after the score loads, so
+  // waiting for them does not wait for the atomic's return; the returned
+  // count is looked at only at the end of the block.
+  unsigned prev = 0;
+  if (tid == 3 * 64) prev = __hip_atomic_fetch_add(cnt + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  reduce_split_stats<G, NW>(sst, R, wave, lane, mg, sg);
+  lds_barrier();
+  float mr[G], sr[G];  // in registers: the probability loop's LDS stores would otherwise reload them
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mr[g] = mg[g];
+    sr[g] = sg[g];
+  }
+#pragma unroll
+  for (int r = 0; r < SPT; ++r) {
+    const int idx = tid + NT * r, g = idx / kLocalLen, j = idx % kLocalLen;
+    const float sv = sreg[r];
+    if (j < len) pr[g * kLocalLen + j] = (sv == -INFINITY) ? 0.0f : rbf(expf(sv - mr[g]) / sr[g]);
+  }
+  lds_barrier();
+  float acc[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = 0.0f;
+  const u32x4 vnew_slice = append ? *(const u32x4*)(vn16 + d0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int c0 = 0; c0 < NST; c0 += CH) {
+    if (c0 < nst) {
+      float pc[CH][G];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int j = min((c0 + u) * PPB + wave * PPW + slot, kLocalLen - 1);
+#pragma unroll
+        for (int g = 0; g < G; ++g) pc[u][g] = okv[c0 + u] ? pr[g * kLocalLen + j] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int j = (c0 + u) * PPB + wave * PPW + slot;
+        const u32x4 v = (append && R.lo + j == pos) ? vnew_slice : vv[c0 + u];
+        float vf[8];
+        unpack8(v, vf);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[g][i] = fmaf(pc[u][g], vf[i], acc[g][i]);
+      }
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[g][i] = group_sum<PPW>(acc[g][i]);
+  if (slot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) red[(wave * G + g) * kSliceD + sub * 8 + i] = acc[g][i];
+  }
+  lds_barrier();
+  for (int e = tid; e < G * kSliceD; e += NT) {
+    const int g = e / kSliceD, dd = e % kSliceD;
+    float v = red[g * kSliceD + dd];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v += red[(w * G + g) * kSliceD + dd];  // in wave order
+    ctx[((size_t)kv * G + g) * D + slice * kSliceD + dd] = f2bf(v);
+  }
+  if (tid == 3 * 64 && prev == (unsigned)(D / kSliceD) - 1) {  // every P.V block of the head is past the wait
+    __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(cnt + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// grid 8 * (n_split_max + D / kSliceD) blocks of 320 threads (the P.V
+// role's fifth wave polls; the scores role uses four)
+constexpr int kLocalThreads = 320;
+template <int D, int G, bool DPT>
+__global__ __launch_bounds__(kLocalThreads) void attn_local_kernel(
+    AttnDims a, const uint16_t* __restrict__ q_raw, const uint16_t* __restrict__ k_raw,
+    const uint16_t* __restrict__ v_raw, const uint16_t* __restrict__ q_norm, const uint16_t* __restrict__ k_norm,
+    const uint16_t* __restrict__ rope_cos, const uint16_t* __restrict__ rope_sin, uint16_t* __restrict__ k_pages,
+    uint16_t* v_pages, const int32_t* __restrict__ page_table, const int32_t* __restrict__ pos_arr, int append,
+    float* ws_scores, float* ws_stats, unsigned int* counters, uint16_t* __restrict__ ctx) {
+  const int kv = xcc_id();
+  const int role = (int)blockIdx.x >> 3;
+  if (kv >= a.KV) return;
+  const int pos = pos_arr[0];
+  const Range R = attn_range(a, pos);
+  if (R.n_eff == 0) {  // nothing attended: ctx = 0
+    if (role == 0)
+      for (int e = threadIdx.x; e < G * D; e += kLocalThreads) ctx[(size_t)kv * G * D + e] = 0;
+    return;
+  }
+  unsigned int* cnt = counters + (size_t)kv * (kMaxGroups + 1);
+  if (role < a.n_split_max) {
+    if (role < R.n_eff)
+      attn_local_scores<D, G, DPT>(a, R, kv, role, pos, q_raw, k_raw, v_raw, q_norm, k_norm, rope_cos, rope_sin,
+                                   k_pages, v_pages, page_table, append, ws_scores, ws_stats, cnt);
+  } else if (role - a.n_split_max < D / kSliceD) {
+    attn_local_pv<D, G, DPT>(a, R, kv, role - a.n_split_max, pos, k_raw, v_raw, v_pages, page_table, append,
+                             ws_scores, ws_stats, cnt, ctx);
+  }
+}
+
+// Block -> XCD map of this device, checked once (outside graph capture): the
+// one-launch attention needs block b on XCD b % 8 for every b.  The blocks
+// record their XCD in a file-scope array (no allocation).
+constexpr int kXccProbeBlocks = 1024;
+static __device__ int xcc_probe[kXccProbeBlocks];
+__global__ void xcc_map_kernel(int* out) {
+  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
+}
+
 // ------------------------------------------------------------------ append
 // k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) of T tokens of one
 // sequence written at positions pos[t] (model.py:202-206).  grid (T, KV).
@@ -1064,6 +1418,56 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
 }
 
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
+
+// Whether this device runs block b of every launch on the XCD of block b % 8,
+// with 8 consecutive blocks on 8 different XCDs (the dispatcher's round
+// robin), checked once per device by recording each block's XCD for two
+// launches (the first of 13 blocks, so a dispatcher that continued its
+// round robin across launches would show).  Not checked while `st` is being
+// captured into a graph (the check copies to the host): such a call uses the
+// two-launch path and the check runs at the next call outside a capture.
+static std::mutex g_xcc_mu;
+static int g_xcc_state[64];  // 0 unknown, 1 round robin, -1 not
+static bool xcc_round_robin(hipStream_t st) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  std::lock_guard<std::mutex> lock(g_xcc_mu);
+  if (g_xcc_state[dev] != 0) return g_xcc_state[dev] > 0;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
+  constexpr int n = kXccProbeBlocks;
+  int* d = nullptr;
+  if (hipGetSymbolAddress((void**)&d, HIP_SYMBOL(xcc_probe)) != hipSuccess || d == nullptr) {
+    (void)hipGetLastError();
+    return false;
+  }
+  int h[n];
+  bool ok = true;
+  for (int rep = 0; rep < 2 && ok; ++rep) {
+    const int nb = rep == 0 ? 13 : n;
+    hipLaunchKernelGGL(xcc_map_kernel, dim3((unsigned)nb), dim3(64), 0, st, d);
+    ok = hipMemcpyAsync(h, d, nb * sizeof(int), hipMemcpyDeviceToHost, st) == hipSuccess &&
+         hipStreamSynchronize(st) == hipSuccess;
+    bool seen[16] = {};
+    for (int b = 0; ok && b < nb; ++b) {
+      ok = h[b] >= 0 && h[b] < 8 && h[b] == h[b % 8];
+      if (ok && b < 8) {
+        ok = !seen[h[b]];
+        seen[h[b]] = true;
+      }
+    }
+    ok = ok && nb >= 8;
+    if (rep == 0) ok = true;  // the 13-block launch only shifts a round robin that carries over
+  }
+  (void)hipGetLastError();
+  g_xcc_state[dev] = ok ? 1 : -1;
+  return ok;
+}
+
+static bool attn_local_enabled() {
+  const char* e = getenv("G4MI_ATTN_LOCAL");
+  return e == nullptr || atoi(e) != 0;
+}
 
 // Zeroes n words (the arrival counters of a call that brings no workspace of
 // its own, see g4mi_decode_attention_noalloc).
@@ -1221,6 +1625,27 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
   if (clear_counters) {
     const int64_t words = B * NH * (kMaxGroups + 1);
     hipLaunchKernelGGL(zero_words_kernel, dim3((unsigned)((words + 255) / 256)), dim3(256), 0, st, w.counters, words);
+  }
+  // batch 1 with one KV head per XCD and every split within one K tile per
+  // wave: the one-launch attention (attn_local_kernel)
+  if (B == 1 && KV == 8 && page_size == kLocalPage && span <= kLocalLen && span <= (int64_t)kChunkMin * n_split_max &&
+      G <= 2 && D <= 256 &&
+      attn_local_enabled() && xcc_round_robin(st)) {
+    const dim3 lgrid((unsigned)(8 * (n_split_max + D / kSliceD)));
+#define G4MI_LOC(DD, GG)                                                                                       \
+    if (D == DD && G == GG) {                                                                                  \
+      if (dense)                                                                                               \
+        hipLaunchKernelGGL((attn_local_kernel<DD, GG, true>), lgrid, dim3(kLocalThreads), 0, st, a, q_raw, k_raw, v_raw,  \
+                           q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table, pos, append,       \
+                           w.scores, w.stats, w.counters, ctx);                                                 \
+      else                                                                                                     \
+        hipLaunchKernelGGL((attn_local_kernel<DD, GG, false>), lgrid, dim3(kLocalThreads), 0, st, a, q_raw, k_raw, v_raw, \
+                           q_norm, k_norm, rope_cos, rope_sin, k_pages, v_pages, page_table, pos, append,       \
+                           w.scores, w.stats, w.counters, ctx);                                                 \
+    }
+    G4MI_LOC(64, 1) G4MI_LOC(64, 2) G4MI_LOC(128, 1) G4MI_LOC(128, 2) G4MI_LOC(256, 1) G4MI_LOC(256, 2)
+#undef G4MI_LOC
+    return check_launch("decode_attention");
   }
   dim3 grid((unsigned)n_split_max, (unsigned)KV, (unsigned)B);
 #define G4MI_ATT(DD, GG)                                                                                      \
