@@ -1027,8 +1027,6 @@ constexpr int kLocalLen = 1024;
 constexpr int kLocalPage = 64;       // cache page size of this path (positions per page)
 constexpr int kLocalSpin = 1 << 22;  // polls before a waiting block gives up (~0.1 s)
 
-__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15; }
-
 template <int D, int G, bool DPT>
 __device__ __forceinline__ void attn_local_scores(
     const AttnDims& a, const Range& R, int kv, int split, int pos, const uint16_t* __restrict__ q_raw,
@@ -1338,14 +1336,6 @@ __global__ __launch_bounds__(kLocalThreads) void attn_local_kernel(
   }
 }
 
-// Block -> XCD map of this device, checked once (outside graph capture): the
-// one-launch attention needs block b on XCD b % 8 for every b.  The blocks
-// record their XCD in a file-scope array (no allocation).
-constexpr int kXccProbeBlocks = 1024;
-static __device__ int xcc_probe[kXccProbeBlocks];
-__global__ void xcc_map_kernel(int* out) {
-  if (threadIdx.x == 0) out[blockIdx.x] = xcc_id();
-}
 
 // ------------------------------------------------------------------ append
 // k = rope(rms_norm(k_raw, k_norm)), v = rms_norm(v_raw) of T tokens of one
@@ -1418,51 +1408,6 @@ static void launch_attn(const AttnDims& a, dim3 grid, hipStream_t st, const uint
 }
 
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
-
-// Whether this device runs block b of every launch on the XCD of block b % 8,
-// with 8 consecutive blocks on 8 different XCDs (the dispatcher's round
-// robin), checked once per device by recording each block's XCD for two
-// launches (the first of 13 blocks, so a dispatcher that continued its
-// round robin across launches would show).  Not checked while `st` is being
-// captured into a graph (the check copies to the host): such a call uses the
-// two-launch path and the check runs at the next call outside a capture.
-static std::mutex g_xcc_mu;
-static int g_xcc_state[64];  // 0 unknown, 1 round robin, -1 not
-static bool xcc_round_robin(hipStream_t st) {
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
-  std::lock_guard<std::mutex> lock(g_xcc_mu);
-  if (g_xcc_state[dev] != 0) return g_xcc_state[dev] > 0;
-  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-  if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return false;
-  constexpr int n = kXccProbeBlocks;
-  int* d = nullptr;
-  if (hipGetSymbolAddress((void**)&d, HIP_SYMBOL(xcc_probe)) != hipSuccess || d == nullptr) {
-    (void)hipGetLastError();
-    return false;
-  }
-  int h[n];
-  bool ok = true;
-  for (int rep = 0; rep < 2 && ok; ++rep) {
-    const int nb = rep == 0 ? 13 : n;
-    hipLaunchKernelGGL(xcc_map_kernel, dim3((unsigned)nb), dim3(64), 0, st, d);
-    ok = hipMemcpyAsync(h, d, nb * sizeof(int), hipMemcpyDeviceToHost, st) == hipSuccess &&
-         hipStreamSynchronize(st) == hipSuccess;
-    bool seen[16] = {};
-    for (int b = 0; ok && b < nb; ++b) {
-      ok = h[b] >= 0 && h[b] < 8 && h[b] == h[b % 8];
-      if (ok && b < 8) {
-        ok = !seen[h[b]];
-        seen[h[b]] = true;
-      }
-    }
-    ok = ok && nb >= 8;
-    if (rep == 0) ok = true;  // the 13-block launch only shifts a round robin that carries over
-  }
-  (void)hipGetLastError();
-  g_xcc_state[dev] = ok ? 1 : -1;
-  return ok;
-}
 
 static bool attn_local_enabled() {
   const char* e = getenv("G4MI_ATTN_LOCAL");

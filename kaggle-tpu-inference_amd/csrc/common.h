@@ -117,6 +117,16 @@ __device__ __forceinline__ void static_for(F&& f) {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6)); }
+
+// The XCD (0..7) running the calling wave (hardware register XCC_ID).
+__device__ __forceinline__ int xcc_id() { return __builtin_amdgcn_s_getreg((15 << 11) | (0 << 6) | 20) & 15; }
+
+// Whether every launch on this device runs block b on the XCD of block
+// b % 8, 8 consecutive blocks on 8 different XCDs (checked once per device,
+// outside graph capture; xcd.hip).  Blocks b, b + 8, b + 16, ... of such a
+// launch share one L2 and may pass data through it with plain stores and
+// loads.
+bool xcc_round_robin(hipStream_t st);
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *(const u32x4*)p; }
 
 // ------------------------------------------------------------------ reductions

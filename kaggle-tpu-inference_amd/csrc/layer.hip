@@ -232,6 +232,7 @@ struct FfnInArgs {
   float* top_w;                // [K]
   int32_t* top_i;              // [K]
   unsigned int* counter;       // router-block arrivals (zero between launches)
+  int xcd_local;               // router blocks on one XCD (see ffn_in_kernel)
   int H;
   float eps;
 };
@@ -245,10 +246,24 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   __shared__ u32x4 xs[NCH];
   __shared__ double red[16];
   const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5, l = lane & 31, wave = wave_id();
-  // router blocks come first in dispatch order: the router and the expert
-  // selection are this kernel's longest chain
+  // The router and the expert selection are this kernel's longest chain, so
+  // the router blocks come first in dispatch order.  With xcd_local they are
+  // blocks 0, 8, 16, ... (one XCD: block b runs on the XCD of block b % 8),
+  // so their scores reach the selecting block through that XCD's L2 (plain
+  // stores and loads); otherwise blocks 0 .. rblocks-1, with device-scope
+  // stores and loads.
   const int rblocks = (int)gridDim.x - a.dense_blocks;
-  const bool dense = (int)blockIdx.x >= rblocks;
+  const int bid = (int)blockIdx.x;
+  int rb, db;  // router block index (or -1), dense block index
+  if (a.xcd_local) {
+    const bool r = (bid & 7) == 0 && (bid >> 3) < rblocks;
+    rb = r ? (bid >> 3) : -1;
+    db = (bid < 8 * rblocks) ? bid - (bid >> 3) - 1 : bid - rblocks;
+  } else {
+    rb = bid < rblocks ? bid : -1;
+    db = bid - rblocks;
+  }
+  const bool dense = rb < 0;
   // prologue operands first (see layer_in), then the weight rows.  Every
   // load is unconditional (a valid stand-in pointer where an operand is
   // absent): under a branch the compiler waits for the load inside it,
@@ -263,9 +278,9 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   vload(rsc, (!dense && a.r_scale != nullptr) ? a.r_scale : a.w_pa, NCH);
   // dense: this block owns tasks (one (gate, up) row pair each) [t0, tend),
   // wave w takes t0+w, t0+w+4, ...; router blocks own 8 expert rows each.
-  const int t0 = ((int)blockIdx.x - rblocks) * a.tasks_per_block;
+  const int t0 = db * a.tasks_per_block;
   const int tend = min(t0 + a.tasks_per_block, a.I), tlast = max(tend - 1, 0);
-  const int e = (int)blockIdx.x * 8 + wave * 2 + half;
+  const int e = rb * 8 + wave * 2 + half;
   auto dense_row = [&](int f) { return (half ? a.up : a.gate) + (size_t)f * H; };
   // the wave's first task (router blocks: their one row) is requested
   // before the prologue, the other tasks (t0 + wave + 4j, j < kFfnInTasks)
@@ -275,7 +290,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
   vscale_w(o, vrms(o, H, a.eps, red), wpa);
   vadd(x, o);
-  if (blockIdx.x == 0) vstore(x, (u32x4*)a.x1_out, NCH);
+  if (bid == 0) vstore(x, (u32x4*)a.x1_out, NCH);
   const float r1 = vrms(x, H, a.eps, red);
   if (dense) {
     vscale_w(x, r1, wf);
@@ -283,7 +298,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   } else {
     Vec xe = x;
     vscale_w(xe, r1, wf);
-    if (blockIdx.x == 0) vstore(xe, (u32x4*)a.xe_out, NCH);
+    if (rb == 0) vstore(xe, (u32x4*)a.xe_out, NCH);
     // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
     const float r2 = vrms(xe, H, a.eps, red);
 #pragma unroll
@@ -329,8 +344,10 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
       else d0 = dot8_f64(w0[i], xs[l + 32 * i], d0);
     }
     const double acc = group_sum_f64<32>(d0 + d1);
-    if (e < a.E && l == 0)
-      __hip_atomic_store(a.scores + e, rbf(f32_of(acc)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (e >= 0 && e < a.E && l == 0) {
+      if (a.xcd_local) a.scores[e] = rbf(f32_of(acc));
+      else __hip_atomic_store(a.scores + e, rbf(f32_of(acc)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (a.pes == nullptr) return;
     // the last router block to finish selects the experts (model.py:228-231)
     // once, so the expert kernel starts from the routing instead of the scores
@@ -338,9 +355,10 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     __shared__ int flag;
     if (!arrive_last(a.counter, (unsigned)rblocks, &flag)) return;
     const int t = threadIdx.x;
-    const float sv = (t < a.E) ? __hip_atomic_load(a.scores + min(t, a.E - 1), __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)
-                               : -INFINITY;
+    float sv = -INFINITY;
+    if (t < a.E)
+      sv = a.xcd_local ? __hip_atomic_load(a.scores + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP)
+                       : __hip_atomic_load(a.scores + t, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     block_select_values_pes(sv, pes_t, a.E, a.K, L);
     if (t < a.K) {
       a.top_w[t] = L.topw[t];
@@ -616,6 +634,12 @@ __global__ void advance_feed_kernel(const int32_t* __restrict__ feed, int feed_c
 // Work units (row pairs, row groups or tasks) per block for the row walks:
 // about gemv_blocks() blocks (one per CU by default; G4MI_GEMV_BLOCKS
 // overrides it for tuning), 4 waves each, at least one unit per wave.
+// The XCD-local router of ffn_in_kernel (on unless G4MI_FFN_IN_XCD=0).
+static bool ffn_in_xcd_enabled() {
+  const char* e = getenv("G4MI_FFN_IN_XCD");
+  return e == nullptr || atoi(e) != 0;
+}
+
 static int gemv_blocks() {
   static const int n = [] {
     const char* e = getenv("G4MI_GEMV_BLOCKS");
@@ -756,6 +780,8 @@ int g4mi_ffn_in(const uint16_t* x, const uint16_t* o, const uint16_t* post_attn_
   a.pes = per_expert_scale; a.K = (int)k; a.top_w = top_w; a.top_i = top_i; a.counter = (unsigned int*)ws;
   const int rblocks = router_proj ? (int)((E + 7) / 8) : 0;
   dim3 grid((unsigned)(a.dense_blocks + rblocks));
+  a.xcd_local = rblocks > 0 && per_expert_scale != nullptr && a.dense_blocks >= 7 * rblocks && ffn_in_xcd_enabled() &&
+                xcc_round_robin(as_stream(stream));
   hipStream_t st = as_stream(stream);
   switch (H / 256) {
 #define G4MI_C(I) case I: hipLaunchKernelGGL(ffn_in_kernel<I>, grid, dim3(256), 0, st, a); break;
