@@ -1002,9 +1002,12 @@ __global__ __launch_bounds__(256) void attn_reduce_kernel(AttnDims a, const int3
 }
 
 // ------------------------------------------------------------------ one launch per layer, one XCD per KV head
-// Batch 1, 8 KV heads (the sliding layers: model.py:207-213 with the window
-// mask of model.py:402-408), every split at most kChunkMin positions and at
-// most kLocalLen positions attended.  The 8 XCDs take a launch's blocks in
+// Batch 1, at most 8 KV heads (the sliding layers, 8 heads of 256 with 2
+// query heads each: model.py:207-213 with the window mask of
+// model.py:402-408; and the full k==v layers, 2 heads of 512 with 8 query
+// heads each, while they span at most kLocalLen positions), every split at
+// most kChunkMin positions and at most kLocalLen positions attended.  XCDs
+// past the last KV head have nothing to do.  The 8 XCDs take a launch's blocks in
 // turn (block b runs on XCD b % 8, checked on the host before the path is
 // used), so the blocks b, b + 8, b + 16, ... share one XCD and its L2.  A
 // block serves KV head kv = its XCD, and role r = b / 8:
@@ -1037,7 +1040,8 @@ __device__ __forceinline__ void attn_local_scores(
   constexpr int PL = D / 64;
   constexpr int NT = 256;
   constexpr int KS = D / 32;
-  static_assert(G <= 2, "waves 0..G-1 take the q heads, waves 2 and 3 the new K and V");
+  constexpr int GW = (G + 3) / 4;  // query heads per wave: wave w takes heads w, w + 4
+  static_assert(G <= 8, "at most 8 query heads per KV head");
   if (threadIdx.x >= NT) return;  // the fifth wave polls in the P.V role only
   __shared__ __align__(16) uint16_t qa[16 * D];
   __shared__ __align__(16) uint16_t kn16[D];
@@ -1056,12 +1060,13 @@ __device__ __forceinline__ void attn_local_scores(
   const PtStage<NT> pts = stage_load<NT>(a, pt_row, first);
   const int jc0 = min(wave * 16 + col, npos - 1);
   const int pe0 = pt_row[(start + jc0) / PG];
-  // prologue rows: wave w < G takes q head w; the split that ends at pos
-  // appends the new K (wave 2) and V (wave 3)
+  // prologue rows: wave w takes q heads w, w + 4; the split that ends at
+  // pos appends the new K (wave 2) and V (wave 3)
   const int so = lane * PL, jo = so % (D / 2);
   const bool mine = append && (end == pos + 1);
-  float qx[PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
-  load_slice<PL>(q_raw + ((size_t)kv * G + min(wave, G - 1)) * D + so, qx);
+  float qx[GW][PL], qw[PL], cs[PL], sn[PL], kvx[PL], kw[PL];
+#pragma unroll
+  for (int u = 0; u < GW; ++u) load_slice<PL>(q_raw + ((size_t)kv * G + min(wave + 4 * u, G - 1)) * D + so, qx[u]);
   load_slice<PL>(q_norm + so, qw);
   load_slice<PL>(rope_cos + (size_t)pos * (D / 2) + jo, cs);
   load_slice<PL>(rope_sin + (size_t)pos * (D / 2) + jo, sn);
@@ -1081,10 +1086,14 @@ __device__ __forceinline__ void attn_local_scores(
     for (int s2 = 0; s2 < KS; ++s2) bt[s2] = ld16((const u32x4*)(kp + 32 * s2));
   }
   for (int c = tid; c < (16 - G) * D / 8; c += NT) ((u32x4*)(qa + G * D))[c] = u32x4{0u, 0u, 0u, 0u};
-  if (wave < G) {
-    norm_rope_slice<D>(qx, qw, cs, sn, a.eps, true);
 #pragma unroll
-    for (int i = 0; i < PL; ++i) qa[wave * D + so + i] = f2bf(qx[i]);
+  for (int u = 0; u < GW; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      norm_rope_slice<D>(qx[u], qw, cs, sn, a.eps, true);
+#pragma unroll
+      for (int i = 0; i < PL; ++i) qa[g * D + so + i] = f2bf(qx[u][i]);
+    }
   }
   if (mine && wave >= 2) {
     norm_rope_slice<D>(kvx, wave == 2 ? kw : nullptr, cs, sn, a.eps, wave == 2);
@@ -1134,23 +1143,26 @@ __device__ __forceinline__ void attn_local_scores(
     }
   }
   lds_barrier();
-  if (wave < G) {
-    const int g = wave;
-    float m = -INFINITY;
-    for (int j = lane; j < npos; j += 64) m = fmaxf(m, sc[g][j]);
-    m = wave_max_bfly(m);
-    float* srow = ws_scores + ((size_t)kv * G + g) * a.lmax + (start - R.lo);
-    float l = 0.0f;
-    for (int j = lane; j < npos; j += 64) {
-      const float s2 = sc[g][j];
-      l += (s2 == -INFINITY) ? 0.0f : expf(s2 - m);
-      srow[j] = s2;
-    }
-    l = group_sum<64>(l);
-    if (lane == 0) {
-      const int h = kv * G + g;
-      ws_stats[(size_t)h * a.n_split_max + split] = m;
-      ws_stats[((size_t)a.NH + h) * a.n_split_max + split] = l;
+#pragma unroll
+  for (int u = 0; u < GW; ++u) {
+    const int g = wave + 4 * u;
+    if (g < G) {
+      float m = -INFINITY;
+      for (int j = lane; j < npos; j += 64) m = fmaxf(m, sc[g][j]);
+      m = wave_max_bfly(m);
+      float* srow = ws_scores + ((size_t)kv * G + g) * a.lmax + (start - R.lo);
+      float l = 0.0f;
+      for (int j = lane; j < npos; j += 64) {
+        const float s2 = sc[g][j];
+        l += (s2 == -INFINITY) ? 0.0f : expf(s2 - m);
+        srow[j] = s2;
+      }
+      l = group_sum<64>(l);
+      if (lane == 0) {
+        const int h = kv * G + g;
+        ws_stats[(size_t)h * a.n_split_max + split] = m;
+        ws_stats[((size_t)a.NH + h) * a.n_split_max + split] = l;
+      }
     }
   }
   // the block's scores and statistics (and its cache append) have reached
@@ -1573,8 +1585,8 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
   }
   // batch 1 with one KV head per XCD and every split within one K tile per
   // wave: the one-launch attention (attn_local_kernel)
-  if (B == 1 && KV == 8 && page_size == kLocalPage && span <= kLocalLen && span <= (int64_t)kChunkMin * n_split_max &&
-      G <= 2 && D <= 256 &&
+  if (B == 1 && KV <= 8 && page_size == kLocalPage && span <= kLocalLen && span <= (int64_t)kChunkMin * n_split_max &&
+      ((KV == 8 && G <= 2 && D <= 256) || (KV <= 2 && G == 8 && D == 512)) &&
       attn_local_enabled() && xcc_round_robin(st)) {
     const dim3 lgrid((unsigned)(8 * (n_split_max + D / kSliceD)));
 #define G4MI_LOC(DD, GG)                                                                                       \
@@ -1589,6 +1601,7 @@ static int decode_attention_impl(const uint16_t* q_raw, const uint16_t* k_raw, c
                            w.scores, w.stats, w.counters, ctx);                                                 \
     }
     G4MI_LOC(64, 1) G4MI_LOC(64, 2) G4MI_LOC(128, 1) G4MI_LOC(128, 2) G4MI_LOC(256, 1) G4MI_LOC(256, 2)
+    G4MI_LOC(512, 8)
 #undef G4MI_LOC
     return check_launch("decode_attention");
   }

@@ -16,7 +16,10 @@ replayed:
   * "decode": the layers with the decode path's bf16 running combine
              (model.py:262-294), lm_head and the sampler (or argmax);
              below SHORT_SPAN positions a second capture ("decode_short")
-             whose full-attention layers are sized for SHORT_SPAN positions.
+             whose full-attention layers are sized for SHORT_SPAN positions,
+             and below TINY_SPAN a third ("decode_tiny") sized for TINY_SPAN
+             (there the full layers' attention runs in one launch per layer,
+             like the sliding layers').
 The token, position and the whole token history stay on the device; the
 host only replays graphs and copies each produced token into pinned memory,
 so `lookahead` steps stay queued while it reads the oldest one.
@@ -50,6 +53,9 @@ PREFILL_BUCKET = 256
 # layers are sized for 8,192 positions (64 per split at 128 splits, one K tile
 # per wave); later steps replay the max_len-sized graph.
 SHORT_SPAN = 8192
+# Below this position a third graph sizes the full-attention layers for 1,024
+# positions, within reach of the one-launch attention (one XCD per KV head).
+TINY_SPAN = 1024
 
 
 def _round_up(x: int, m: int) -> int:
@@ -100,6 +106,7 @@ class Engine:
         # below this position the decode step replays a graph whose full
         # attention layers are sized for it (DecodeRunner.set_full_span)
         self._short_span = SHORT_SPAN if self.max_len > SHORT_SPAN else 0
+        self._tiny_span = TINY_SPAN if self.max_len > TINY_SPAN else 0
         self._host_tok = torch.zeros(self.max_len + 1, dtype=torch.int32, pin_memory=True)
         self._prefill_runner: M.PrefillRunner | None = None
         # positions written per cache row since the last reset_cache()
@@ -122,7 +129,7 @@ class Engine:
         sampler = None if greedy else (self._sp, self.top_k, 0 if kind == "head" else 1)
 
         def step():
-            r.set_full_span(self._short_span if kind == "decode_short" else None)
+            r.set_full_span({"decode_short": self._short_span, "decode_tiny": self._tiny_span}.get(kind) or None)
             try:
                 if kind == "feed":
                     r.launch("f32", advance=True, feed=self._prompt)
@@ -238,7 +245,8 @@ class Engine:
                 r.tok.copy_(r.hist[p:p + 1])
                 r.pos.fill_(p)
             greedy = self._set_sampling(key, temperature, top_p)
-            self._graph("decode_short" if p < self._short_span else "decode", greedy).replay()
+            kind = "decode_tiny" if p < self._tiny_span else ("decode_short" if p < self._short_span else "decode")
+            self._graph(kind, greedy).replay()
             self._pos_host = p + 1
             self._dirty[0] = max(self._dirty[0], p + 1)
             return r.hist[p + 1:p + 2].view(1, 1), cache, torch.tensor(p + 1, dtype=torch.int32)
@@ -308,6 +316,8 @@ class Engine:
         self._graph("decode", False)
         if self._short_span:
             self._graph("decode_short", False)
+        if self._tiny_span:
+            self._graph("decode_tiny", False)
         torch.cuda.synchronize(self.device)
         out["decode_compile_s"] = time.perf_counter() - t0
         n = 8

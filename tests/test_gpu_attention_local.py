@@ -149,3 +149,41 @@ def test_graph_replays_at_changing_positions():
         assert torch.equal(got[0], _bits(exp[0])), f"ctx at {p}"
         assert torch.equal(got[1], _bits(exp[1])) and torch.equal(got[2], _bits(exp[2])), f"cache at {p}"
         _ = torch.randn(1024, device=DEV).sum().item()  # eager work between replays
+
+
+@pytest.mark.parametrize("pos", [0, 1, 63, 64, 300, 511, 512, 700, 1023])
+def test_one_launch_full_kv_shared_layer(monkeypatch, pos):
+    """The full k==v layer shape (16 q / 2 KV heads of 512, partial RoPE, two
+    XCDs busy) while its span is at most 1,024 positions: bit-identical to
+    the two launches up to 512 attended positions, the oracle beyond."""
+    lmax, nh, kv, d, seed, eps = 1024, 16, 2, 512, 76, 1e-6
+    q_raw, k_raw = _gen((1, nh, d), seed, "q"), _gen((1, kv, d), seed, "k")
+    qn, kn = _gen((d,), seed, "qn", 0.5), _gen((d,), seed, "kn", 0.5)
+    cos, sin = gm.rope_table(d, 1e6, 0.25, lmax, DEV)
+    kp0 = _gen((lmax // PAGE, kv, PAGE, d), seed, "kp")
+    vp0 = _gen((lmax // PAGE, kv, PAGE, d), seed, "vp")
+    ns = gm.decode_splits(kv, lmax)
+    posd = torch.tensor([pos], dtype=torch.int32, device=DEV)
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("G4MI_ATTN_LOCAL", flag)
+        kp, vp = kp0.clone(), vp0.clone()
+        ctx = ops.decode_attention(q_raw, k_raw, None, qn, kn, cos, sin, kp, vp, None, posd, 0, 0.0, eps, lmax,
+                                   n_split_max=ns)
+        torch.cuda.synchronize()
+        out[flag] = (ctx, kp, vp)
+    same = float((_bits(out["1"][0]) == _bits(out["0"][0])).float().mean())
+    print(f"full layer pos {pos}: ctx bit-identical to the two launches {same:.4f}", flush=True)
+    assert torch.equal(_bits(out["1"][1]), _bits(out["0"][1])) and torch.equal(_bits(out["1"][2]), _bits(out["0"][2]))
+    if pos + 1 <= 512:
+        assert same == 1.0
+    else:
+        ck = kp0.permute(0, 2, 1, 3).reshape(lmax, kv, d).cpu()
+        cv = vp0.permute(0, 2, 1, 3).reshape(lmax, kv, d).cpu()
+        n = pos + 1
+        c, s = twin.rope_tables([pos], twin.rope_inv_freq(d, 1e6, 0.25))
+        ectx, _, _ = twin.attention_core(q_raw[0].cpu().reshape(1, 1, kv, nh // kv, d),
+                                         k_raw[0].cpu().reshape(1, 1, kv, d), k_raw[0].cpu().reshape(1, 1, kv, d),
+                                         qn.cpu(), kn.cpu(), c, s, ck[:n][None], cv[:n][None], n - 1,
+                                         torch.ones((1, 1, 1, 1, n), dtype=torch.bool), n, eps, None)
+        _check(out["1"][0].reshape(-1), ectx.reshape(-1), f"one launch, full layer, pos {pos} vs oracle")

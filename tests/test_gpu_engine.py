@@ -207,18 +207,20 @@ def test_sampler_greedy_cases_and_ties():
     assert set(np.unique(two)) == {12345, 54321}                      # the tie pair, nothing else
 
 
-def test_decode_crosses_the_short_span_graph_boundary():
-    """Below SHORT_SPAN the engine replays a decode graph whose full-attention
-    layers are sized for SHORT_SPAN positions (the kernels that take one K
-    tile per wave); from SHORT_SPAN on, the max_len-sized graph.  Decoding
-    8 steps across the boundary from a prefilled 8,187-token context must
-    give, step for step, the greedy tokens and logits of the same steps
-    replayed with the max_len-sized graph only: the two attention
-    configurations differ only in their f32 summation order (logits within
-    2^-8 of their largest magnitude, corr >= 0.99999)."""
-    from gemma4_mi.engine import SHORT_SPAN
+@pytest.mark.parametrize("kind", ["decode_short", "decode_tiny"])
+def test_decode_crosses_the_short_span_graph_boundary(kind):
+    """Below SHORT_SPAN (TINY_SPAN) the engine replays a decode graph whose
+    full-attention layers are sized for SHORT_SPAN (TINY_SPAN) positions;
+    from there on, the max_len-sized graph.  Decoding 8 steps across the
+    boundary from a context prefilled to 5 positions before it must give,
+    step for step, the greedy tokens and logits of the same steps replayed
+    with the max_len-sized graph only: the attention configurations differ
+    only in their f32 summation order (logits within 2^-8 of their largest
+    magnitude, corr >= 0.99999)."""
+    from gemma4_mi.engine import SHORT_SPAN, TINY_SPAN
     cfg = tiny_parity_config()
-    max_len, n0, steps = 2 * SHORT_SPAN, SHORT_SPAN - 5, 8
+    span = SHORT_SPAN if kind == "decode_short" else TINY_SPAN
+    max_len, n0, steps = 2 * span, span - 5, 8
     eng = Engine.random(cfg, seed=1, max_len=max_len, top_k=64, device=DEV)
     r = eng._runner
     prompt = torch.as_tensor(np.random.default_rng(1).integers(0, cfg.vocab_size, size=(1, n0)), dtype=torch.int32)
@@ -247,7 +249,7 @@ def test_decode_crosses_the_short_span_graph_boundary():
         return toks, logits
 
     toks_a, log_a = run(False)
-    assert ("decode_short", True) in eng._graphs and ("decode", True) in eng._graphs
+    assert (kind, True) in eng._graphs and ("decode", True) in eng._graphs
     toks_b, log_b = run(True)
     for i in range(steps):
         a, b = log_a[i].double(), log_b[i].double()
