@@ -16,9 +16,13 @@ Workloads (--workload):
              N(0, 0.02), seed 3, 47 GiB in HBM; a 32,768-position cache; a
              54-token uniform-random prompt, then greedy batch-1 decode:
              warm-up steps + timed steps = 768 tokens.  value = decode tok/s.
+             config.decode_118_822: the same stream timed over positions
+             118-822 (704 steps) whatever --steps is.
              config.filled_cache_decode: the same engine after every cache
              page is filled with N(0,1), 64 timed steps at positions
              32,703-32,766 (full layers attending ~32.7K positions).
+             roofline.moe_block: the isolated MoE block (below) at batches
+             1, 4 and 8, 1,000 steps each.
   moe_block  the isolated MoE decode block: hidden 2816, router 2816x128,
              128 experts top-8 of width 704, bf16, seed 1, batch --batch
              (1, 4 or 8).  One HIP graph holds up to 64 consecutive steps, each
@@ -58,6 +62,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "batch-1 decode tok/s @32K ctx + MoE-decode HBM GB/s as % of MI355X peak"
 HBM_PEAK_GBS = 8000.0
+WINDOW = (118, 822)  # decode positions timed as a fixed window in every decode run
 
 
 def _log(msg: str) -> None:
@@ -199,6 +204,52 @@ class MoeBlock:
             "sample": f"{done} MoE-block steps of batch {self.n} (torch-CPU oracle, bf16 GEMMs) "
                       f"in {el:.1f}s on {_cpu_name()}",
         }
+
+
+def _moe_block_traffic() -> dict:
+    """HBM bytes per step of the isolated MoE block by batch, from the
+    committed rocprofv3 counter summary (lines `batch B: fetch F write W`,
+    copy-calibrated bytes per step summed over the block's kernels)."""
+    out = {}
+    try:
+        for line in open(os.path.join(ROOT, "profiles", "moe_block_26b_a4b_traffic.txt")):
+            if line.startswith("batch ") and "fetch" in line:
+                b = int(line.split(":", 1)[0].split()[1])
+                f = line.split(":", 1)[1].split()
+                out[b] = {"fetch": float(f[f.index("fetch") + 1]), "write": float(f[f.index("write") + 1])}
+    except (OSError, ValueError, IndexError):
+        return {}
+    return out
+
+
+def _moe_block_roofline(steps: int = 1000, batches=(1, 4, 8)) -> dict:
+    """The isolated MoE decode block (router, experts, combine) at each batch:
+    `steps` steps on rotating inputs in HIP graphs of 50, bytes per step (the
+    router table, the distinct selected experts' rows, inputs and outputs),
+    the fraction of the 8 TB/s peak, and the counter-measured HBM bytes."""
+    import torch
+
+    traffic = _moe_block_traffic()
+    out = {"peak": HBM_PEAK_GBS, "unit": "GB/s", "steps": steps}
+    for b in batches:
+        G = _chunk(steps, 50)
+        wl = MoeBlock(b, G)
+        g = _capture(lambda: [wl.block(i) for i in range(G)])
+        _time_graph(g, 2)
+        us = _time_graph(g, steps // G) / steps * 1e3
+        bps, uniq = wl.bytes_per_step(G)
+        gbs = bps / (us * 1e-6) / 1e9
+        t = traffic.get(b)
+        out[f"batch_{b}"] = {"us_per_step": us, "bytes_per_step": bps, "mean_unique_experts": uniq,
+                             "achieved": gbs, "frac": gbs / HBM_PEAK_GBS,
+                             "traffic": (t["fetch"] + t["write"]) if t else None,
+                             "traffic_fetch": t["fetch"] if t else None}
+        _log(f"moe block batch {b}: {us:.2f} us/step, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+        del g, wl
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
+    out["traffic_source"] = "profiles/moe_block_26b_a4b_traffic.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE per step)"
+    return out
 
 
 def run_moe_block(args) -> dict:
@@ -401,9 +452,29 @@ def _e2e_decode(args) -> dict:
     ms = e0.elapsed_time(e1) / args.steps
     p1 = int(pos)
     toks = eng._runner.hist[prompt_len: p1 + 1].cpu().tolist()
+    # a fixed window of the same stream: positions 118-822 (704 steps), the
+    # stretch the 704-step default run times after its 64 warm-up steps
+    window = None
+    w0, w1 = WINDOW
+    if p1 <= w0 and w1 < args.max_len:
+        while int(pos) < w0:
+            tok, cache, pos = dec(eng.params, tok, cache, pos, seed, 0.0, 1.0)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(w1 - w0):
+            tok, cache, pos = dec(eng.params, tok, cache, pos, seed, 0.0, 1.0)
+        e1.record()
+        torch.cuda.synchronize()
+        wms = e0.elapsed_time(e1) / (w1 - w0)
+        wbytes = float(np.mean([decode_bytes(cfg, p) for p in range(w0, w1)]))
+        wgbs = wbytes / (wms * 1e-3) / 1e9
+        window = {"positions_timed": [w0, w1], "steps": w1 - w0, "ms_per_token": wms, "tok_s": 1000.0 / wms,
+                  "bytes_per_token": wbytes, "e2e_hbm_gbs": wgbs, "e2e_frac_of_roofline": wgbs / HBM_PEAK_GBS}
+        _log(f"decode at positions {w0}-{w1 - 1}: {wms:.4f} ms/token ({1000.0 / wms:.1f} tok/s)")
+    p2 = int(pos)
     # the median inter-token latency: up to 64 more steps with an event between
     # the graph replays (after the tokens above were read)
-    n_itl = max(0, min(64, args.max_len - 1 - p1))
+    n_itl = max(0, min(64, args.max_len - 1 - p2))
     evs = [torch.cuda.Event(enable_timing=True) for _ in range(n_itl + 1)]
     evs[0].record()
     for i in range(n_itl):
@@ -414,7 +485,7 @@ def _e2e_decode(args) -> dict:
     bytes_tok = float(np.mean([decode_bytes(cfg, p) for p in range(p0, p1)]))
     return {"cfg": cfg, "params": eng.params, "cache": eng.cache, "engine": eng, "ms": ms, "ttft": ttft,
             "first": first, "p0": p0, "p1": p1, "bytes_tok": bytes_tok, "tokens": toks, "prompt": prompt,
-            "itl_median_ms": itl_median, "itl_median_positions": [p1, p1 + n_itl]}
+            "itl_median_ms": itl_median, "itl_median_positions": [p2, p2 + n_itl], "window": window}
 
 
 def _filled_decode(res, steps: int = 64, warm: int = 4) -> dict:
@@ -599,6 +670,13 @@ def run_decode(args) -> dict:
             "traffic_source": "profiles/moe_gateup_26b_a4b_traffic.txt (rocprofv3 FETCH_SIZE/WRITE_SIZE)",
         },
     }
+    if res["window"] is not None:
+        out["config"]["decode_118_822"] = res["window"]
+    elif [res["p0"], res["p1"]] == list(WINDOW):  # the main timing is that window
+        out["config"]["decode_118_822"] = {"positions_timed": list(WINDOW), "steps": args.steps, "ms_per_token": ms,
+                                           "tok_s": tps, "bytes_per_token": res["bytes_tok"], "e2e_hbm_gbs": e2e_gbs,
+                                           "e2e_frac_of_roofline": e2e_gbs / HBM_PEAK_GBS}
+    out["roofline"]["moe_block"] = _moe_block_roofline()
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = _cpu_decode_baseline(res, args.cpu_seconds, 8)
     # after the CPU baseline, which reads the prompt's cache rows
