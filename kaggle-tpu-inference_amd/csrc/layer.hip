@@ -31,25 +31,11 @@
 #include <cstdlib>
 
 #include "common.h"
+#include "gemv.h"
 #include "rowvec.h"
 #include "select.h"
 
 namespace g4mi {
-
-// ------------------------------------------------------------------ GEMV core
-// S lanes per row, IT 16-byte chunks per lane (K = 8*S*IT).
-template <int S, int IT>
-__device__ __forceinline__ void load_row(const uint16_t* __restrict__ row, int sub, u32x4* w) {
-#pragma unroll
-  for (int i = 0; i < IT; ++i) w[i] = ld_stream((const u32x4*)row + sub + S * i);
-}
-template <int S, int IT>
-__device__ __forceinline__ float dot_row(const u32x4* w, const u32x4* __restrict__ xs, int sub) {
-  float acc = 0.0f;
-#pragma unroll
-  for (int i = 0; i < IT; ++i) acc = dot8(w[i], xs[sub + S * i], acc);
-  return group_sum<S>(acc);
-}
 
 // ------------------------------------------------------------------ layer_in
 enum { kInEmbed = 0, kInTail = 1, kInPlain = 2, kInNormed = 3 };
