@@ -261,6 +261,11 @@ def run_moe_block(args) -> dict:
     total_ms = _time_graph(g_block, args.steps // G)
     ms = total_ms / args.steps
     bps, uniq = wl.bytes_per_step(G)
+    if args.block_only:  # counter runs: the block's own launches only
+        return {"metric": f"isolated MoE decode block tok/s (26B-A4B experts, batch {args.batch})",
+                "value": args.batch / (ms * 1e-3), "unit": "tok/s", "ms_per_step": ms, "dtype": "bf16",
+                "config": {"workload": "moe_decode_block", "batch": args.batch, "bytes_per_step": bps,
+                           "mean_unique_experts": uniq}}
     # dominant kernel: the routed gate/up, G launches per graph on the same inputs
     for i in range(G):
         wl.ops.moe_router_scores(wl.bank[i], wl.scale, wl.proj, 1e-6, out=wl.scores[i])
@@ -934,6 +939,8 @@ def main() -> int:
     ap.add_argument("--batch", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--block-only", action="store_true",
+                    help="moe_block: time the block only (no gate/up roofline leg, no CPU leg), for counter runs")
     args = ap.parse_args()
     if args.steps is None:
         args.steps = {"decode": 704, "prefill": 5, "batch_decode": 256}.get(args.workload, 1000)

@@ -285,10 +285,18 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
   const bool dedup = scores == nullptr && gridDim.y > 1 && NK <= 64;  // block-uniform
   const int pe_raw = top_i[min(lane, NK - 1)];  // every pair's expert, one per lane (unconditional load)
   const int pe = (dedup && lane < NK) ? pe_raw : -1;
+  const int p = n * K + slot;
+  // the pairs that chose this expert (includes p); a wave whose expert an
+  // earlier pair also chose requests no rows: that pair's wave computes
+  // row f for them all (the row address waits for the routing anyway)
+  const unsigned long long same = __ballot(pe == ei);
+  const bool dup = dedup && ok && task < K * F && (same & ((1ull << p) - 1ull)) != 0ull;
   const u32x4* row = (const u32x4*)(gate_up + ((size_t)(max(min(ei, E - 1), 0) * 2 + half) * F + f) * H);
   u32x4 w[IT];
+  if (!dup) {
 #pragma unroll
-  for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 32 * i);
+    for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l + 32 * i);
+  }
 #pragma unroll
   for (int j = 0; j < XPT; ++j)
     if ((int)threadIdx.x + (int)blockDim.x * j < H / 8) xs[threadIdx.x + blockDim.x * j] = xr[j];
@@ -317,16 +325,15 @@ __global__ __launch_bounds__(256) void moe_gateup_kernel(
     }
   };
   if (task >= K * F) return;
-  const int p = n * K + slot;
   if (!dedup || !ok) {
     emit(p, n);
     return;
   }
-  unsigned long long same = __ballot(pe == ei);  // the pairs that chose this expert (includes p)
-  if ((same & ((1ull << p) - 1ull)) != 0ull) return;  // an earlier pair's wave computes row f for them all
-  while (same != 0ull) {
-    const int q = (int)__builtin_ctzll(same);
-    same &= same - 1ull;
+  if (dup) return;
+  unsigned long long rest = same;
+  while (rest != 0ull) {
+    const int q = (int)__builtin_ctzll(rest);
+    rest &= rest - 1ull;
     emit(q, q / K);
   }
 }
