@@ -140,9 +140,11 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
   constexpr int NF = FM + FN, NM = FM * FN;
   static_assert(ST == 2 || ST == 3, "2 or 3 stages");
   static_assert(AI >= 1 && BI >= 1, "tile too small for 256 threads");
-  __shared__ __align__(1024) uint8_t st0[SB];
-  __shared__ __align__(1024) uint8_t st1[SB];
-  __shared__ __align__(1024) uint8_t st2[ST == 3 ? SB : 16];
+  // the ST stages back to back in one array (two blocks of 80 KB, the
+  // 192-row tiles, then fill the CU's 160 KB exactly)
+  __shared__ __align__(1024) uint8_t stages[ST * SB];
+  uint8_t* const st0 = stages;
+  uint8_t* const st1 = stages + SB;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -213,9 +215,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
 
   auto sbase = [&](auto sc) __attribute__((always_inline)) -> uint8_t* {
     constexpr int S = decltype(sc)::value;
-    if constexpr (S == 0) return st0;
-    else if constexpr (S == 1) return st1;
-    else return st2;
+    return stages + S * SB;
   };
   // DMA instruction q (< NL) of step ks into stage sc: 64 lanes x 16 bytes
   // from their global addresses to LDS[l, l + 1024) in lane order (M0 = l).
@@ -544,6 +544,12 @@ static void launch(const GemmArgs& g, int64_t mtiles, hipStream_t st) {
   hipLaunchKernelGGL((gemm_kernel<BM, BN, ST, OCC, EP>), grid, dim3(256), 0, st, g);
 }
 
+int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                    int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                    const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
+                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes, int tile_rows,
+                    void* stream);
+
 }  // namespace g4mi
 
 using namespace g4mi;
@@ -559,6 +565,25 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
                    const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes,
                    void* stream) {
+  return g4mi::gemm_bf16_tiles(a, lda, a_rows, b, ldb, b_group_stride, pair_offset, M, N, K, tiles, ntiles, max_tiles,
+                               epilogue, c, ldc, row_scale, k_slices, ws, ws_bytes, 128, stream);
+}
+
+}  // extern "C"
+
+namespace g4mi {
+
+// g4mi_gemm_bf16 with grouped tiles of up to tile_rows (128 or 192) rows: the
+// MoE prefill's expert tiles are 192 rows once most experts have more than
+// 128 rows (one tile per expert, so its weights stream once, still two
+// blocks per CU).
+int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                    int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                    const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
+                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes, int tile_rows,
+                    void* stream) {
+  G4MI_REQUIRE(tile_rows == 128 || (tile_rows == 192 && tiles != nullptr), G4MI_EINVAL,
+               "gemm: grouped tiles are 128 or 192 rows");
   G4MI_REQUIRE(a && b && c && M >= 1 && N >= 1 && K >= 1, G4MI_EINVAL, "gemm: missing argument");
   G4MI_REQUIRE(K % kBK == 0, G4MI_EUNSUPPORTED, "gemm: K=%lld must be a multiple of %d", (long long)K, kBK);
   G4MI_REQUIRE(lda % 8 == 0 && ldb % 8 == 0 && ((uintptr_t)a & 15u) == 0 && ((uintptr_t)b & 15u) == 0, G4MI_EALIGN,
@@ -598,7 +623,8 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
     }
     return check_launch("gemm_bf16 (skinny)");
   }
-  // grouped tiles are up to 128 rows (128-row kernels); small plain M takes
+  // grouped tiles are up to 128 rows (128-row kernels) or, through
+  // gemm_bf16_tiles, 192; small plain M takes
   // 64-row tiles.  Two blocks per CU (2 stages) for grouped tiles and when
   // there are more tiles than CUs, else one block per CU with 3 stages.
   const bool small = tiles == nullptr && M <= 64;
@@ -614,6 +640,8 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   else launch<BM, BN, S, O, kEpBf16>(g, mtiles, st);
   if (small) {
     G4MI_GEMM(64, 128, 3, 1)
+  } else if (tiles != nullptr && tile_rows == 192) {
+    G4MI_GEMM(192, 128, 2, 2)
   } else if (tiles != nullptr || nblocks > 256) {
     G4MI_GEMM(128, 128, 2, 2)
   } else {
@@ -627,6 +655,10 @@ int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const 
   }
   return check_launch("gemm_bf16");
 }
+
+}  // namespace g4mi
+
+extern "C" {
 
 int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K, int32_t nseg,
                             const uint16_t* const* b, const int64_t* n, uint16_t* const* c, void* stream) {

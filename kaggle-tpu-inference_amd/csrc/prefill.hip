@@ -8,41 +8,44 @@
 // the selected (token, expert) pairs as grouped GEMMs, 16x fewer FLOPs at
 // E = 128, k = 8, with the same rounding points:
 //   1. moe_sort_kernel: tokens grouped by expert (counts, offsets, a gather
-//      list, the per-slot routing weight) and 128-row GEMM tiles per expert
-//      (one tile covers an expert's rows up to 128, so its weights stream once);
+//      list, the per-slot routing weight) and 128- or 192-row GEMM tiles per
+//      expert (one tile covers an expert's rows up to the tile height, so its
+//      weights stream once);
 //   2. gate/up GEMM over the gathered rows with the gated epilogue:
 //      act = bf16(bf16(bf16(gelu(bf16(g))) * bf16(u)) * bf16(w))   (model.py:246-247);
 //   3. down GEMM, f32 output per (token, expert);
 //   4. moe_combine_kernel: out[t] = bf16(sum over the token's slots in order)
 //      -- one f32 sum over (expert, f) as the dense einsum (model.py:250).
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "capi_util.h"
 #include "common.h"
 #include "rowvec.h"
 
-extern "C" int g4mi_gemm_bf16(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
-                              int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
-                              const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue,
-                              void* c, int64_t ldc, const float* row_scale, int64_t k_slices, void* ws,
-                              int64_t ws_bytes, void* stream);
-
 namespace g4mi {
 
-constexpr int kTileRows = 128;  // grouped GEMM tile height (gemm.hip's grouped tiles)
+// gemm.hip: g4mi_gemm_bf16 with grouped tiles of up to tile_rows (128 or 192) rows
+int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
+                    int64_t b_group_stride, int64_t pair_offset, int64_t M, int64_t N, int64_t K,
+                    const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles, int32_t epilogue, void* c,
+                    int64_t ldc, const float* row_scale, int64_t k_slices, void* ws, int64_t ws_bytes, int tile_rows,
+                    void* stream);
+
+constexpr int kTileRows = 128;  // grouped GEMM tile height, the smaller of the two (gemm.hip's grouped tiles)
 constexpr int kSortIpt = 16;    // routing items per thread per chunk in moe_sort_kernel
 constexpr int kMaxExperts = 256;
 
 // One block.  entries i = t*K + s (token t, slot s) of the routing.
 //   sorted position p of entry i: offsets[e] + (rank among entries of expert e)
 //   a_rows[p] = t, w_sorted[p] = top_w[i], slot_pos[i] = p (-1: invalid expert)
-//   tiles: (e, m0, m1) for every kTileRows rows of every expert, ntiles[0] = count.
+//   tiles: (e, m0, m1) for every tile_rows rows of every expert, ntiles[0] = count.
 __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restrict__ top_i,
                                                         const float* __restrict__ top_w, int n, int K, int E,
                                                         int32_t* __restrict__ a_rows, float* __restrict__ w_sorted,
                                                         int32_t* __restrict__ slot_pos, int32_t* __restrict__ tiles,
-                                                        int32_t* __restrict__ ntiles) {
+                                                        int32_t* __restrict__ ntiles, int tile_rows) {
   __shared__ int cnt[kMaxExperts], off[kMaxExperts], cur[kMaxExperts], toff[kMaxExperts];
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += blockDim.x) cnt[e] = 0;
@@ -70,7 +73,7 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
       cur[e] = 0;
       toff[e] = to;
       o += cnt[e];
-      to += (cnt[e] + kTileRows - 1) / kTileRows;
+      to += (cnt[e] + tile_rows - 1) / tile_rows;
     }
     ntiles[0] = to;
   }
@@ -100,12 +103,12 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
     }
   }
   for (int e = tid; e < E; e += blockDim.x) {
-    const int nt = (cnt[e] + kTileRows - 1) / kTileRows;
+    const int nt = (cnt[e] + tile_rows - 1) / tile_rows;
     for (int j = 0; j < nt; ++j) {
       int32_t* t = tiles + 3 * (toff[e] + j);
       t[0] = e;
-      t[1] = off[e] + j * kTileRows;
-      t[2] = min(off[e] + (j + 1) * kTileRows, off[e] + cnt[e]);
+      t[1] = off[e] + j * tile_rows;
+      t[2] = min(off[e] + (j + 1) * tile_rows, off[e] + cnt[e]);
     }
   }
 }
@@ -337,6 +340,16 @@ static float bf16_round_host(double v) {
   return f;
 }
 
+// Expert tile height: 192 rows while the experts average 96 to 176 rows (an
+// expert's rows then mostly spill past 128 but fit 192, and every further
+// tile of an expert streams its weights again), else 128.
+// G4MI_MOE_TILE_ROWS = 128 or 192 overrides.
+static int moe_prefill_tile_rows(int64_t pairs, int64_t E) {
+  const char* e = getenv("G4MI_MOE_TILE_ROWS");
+  if (e != nullptr && (atoi(e) == 128 || atoi(e) == 192)) return atoi(e);
+  return (pairs >= 96 * E && pairs < 176 * E) ? 192 : 128;
+}
+
 struct MoePrefillWs {
   int32_t *a_rows, *slot_pos, *tiles, *ntiles;
   float *w_sorted, *part;
@@ -379,18 +392,19 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
                "moe_prefill: workspace too small");
   hipStream_t st = as_stream(stream);
   const MoePrefillWs w = moe_prefill_ws(ws, n, K, E, F, H);
-  const int64_t max_tiles = (n * K + kTileRows - 1) / kTileRows + E;
+  const int tile_rows = moe_prefill_tile_rows(n * K, E);
+  const int64_t max_tiles = (n * K + tile_rows - 1) / tile_rows + E;
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, (int)n, (int)K, (int)E, w.a_rows,
-                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles);
+                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles, tile_rows);
   int rc = check_launch("moe_prefill sort");
   if (rc) return rc;
   // gate/up: gathered token rows x the expert's (gate, up) rows -> act [n*K, F]
-  rc = g4mi_gemm_bf16(xn, H, w.a_rows, gate_up, H, 2 * F * H, F * H, n * K, F, H, w.tiles, w.ntiles, max_tiles,
-                      2, w.act, F, w.w_sorted, 1, nullptr, 0, stream);
+  rc = gemm_bf16_tiles(xn, H, w.a_rows, gate_up, H, 2 * F * H, F * H, n * K, F, H, w.tiles, w.ntiles, max_tiles,
+                       2, w.act, F, w.w_sorted, 1, nullptr, 0, tile_rows, stream);
   if (rc) return rc;
   // down: act rows x the expert's down rows -> f32 partial [n*K, H]
-  rc = g4mi_gemm_bf16(w.act, F, nullptr, down, F, H * F, 0, n * K, H, F, w.tiles, w.ntiles, max_tiles, 1, w.part,
-                      H, nullptr, 1, nullptr, 0, stream);
+  rc = gemm_bf16_tiles(w.act, F, nullptr, down, F, H * F, 0, n * K, H, F, w.tiles, w.ntiles, max_tiles, 1, w.part,
+                       H, nullptr, 1, nullptr, 0, tile_rows, stream);
   if (rc) return rc;
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
                      w.slot_pos, (int)n, (int)K, (int)H, 0, out);
@@ -418,7 +432,7 @@ int g4mi_moe_decode_grouped(const uint16_t* xn, const float* top_w, const int32_
   // at most n <= 16 pairs per expert: one tile per selected expert
   const int tiles = (int)(n * K < E ? n * K : E);
   hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, (int)n, (int)K, (int)E, w.a_rows,
-                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles);
+                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles, kTileRows);
   const dim3 ggrid((unsigned)tiles, (unsigned)((F + 4 * kGrpPairs - 1) / (4 * kGrpPairs)));
   switch (H / 256) {
 #define G4MI_GU(I)                                                                                             \

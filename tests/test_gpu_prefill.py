@@ -246,7 +246,7 @@ def _device_moe(cfg, g, x):
     return out, top_w, top_i
 
 
-@pytest.mark.parametrize("which,n", [("tiny", 1), ("tiny", 37), ("tiny", 256), ("26b", 32)])
+@pytest.mark.parametrize("which,n", [("tiny", 1), ("tiny", 37), ("tiny", 256), ("tiny", 512), ("26b", 32)])
 def test_moe_prefill_matches_dense_oracle(which, n):
     cfg = tiny_parity_config() if which == "tiny" else _C2Cfg()
     lp = _moe_params(cfg, 20)
@@ -276,3 +276,31 @@ def test_moe_prefill_rows_independent_at_512_tokens():
                                 top_i[t : t + 1].contiguous(), g["experts.gate_up_proj"], g["experts.down_proj"])
         assert torch.equal(alone[0], out[t]), t
     assert bool(torch.isfinite(out.float()).all())
+
+
+@pytest.mark.parametrize("which,n", [("tiny", 512), ("26b", 2048)])
+def test_moe_prefill_192_row_tiles_equal_128(monkeypatch, which, n):
+    """From 96 (token, slot) pairs per expert on, the expert tiles are 192
+    rows (one tile per expert at the 2,048-token prefill, so each expert's
+    weights stream once); every output row accumulates over K in the same
+    order either way, so the two tilings agree bit for bit, and a row alone
+    equals the row in the batch."""
+    cfg = tiny_parity_config() if which == "tiny" else _C2Cfg()
+    g = {k: v.to(DEV) for k, v in _moe_params(cfg, 50).items()}
+    x = _rand((n, cfg.hidden_size), 51).to(DEV)
+    top_w, top_i = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                       cfg.top_k_experts, cfg.rms_norm_eps)
+    counts = torch.bincount(top_i.flatten().long(), minlength=cfg.num_experts)
+    print(f"{which} n={n}: rows per expert {int(counts.min())}..{int(counts.max())}")
+    outs = {}
+    for rows in ("128", "192"):
+        monkeypatch.setenv("G4MI_MOE_TILE_ROWS", rows)
+        outs[rows] = ops.moe_prefill(x, top_w, top_i, g["experts.gate_up_proj"], g["experts.down_proj"]).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(outs["128"].view(torch.int16), outs["192"].view(torch.int16))
+    monkeypatch.delenv("G4MI_MOE_TILE_ROWS")
+    for t in (0, n // 2, n - 1):
+        alone = ops.moe_prefill(x[t : t + 1].contiguous(), top_w[t : t + 1].contiguous(),
+                                top_i[t : t + 1].contiguous(), g["experts.gate_up_proj"], g["experts.down_proj"])
+        assert torch.equal(alone[0], outs["192"][t]), t
+    assert bool(torch.isfinite(outs["192"].float()).all())
