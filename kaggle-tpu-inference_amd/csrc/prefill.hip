@@ -52,40 +52,69 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   __syncthreads();
   const int total = n * K;
   // items in chunks of kSortIpt per thread: each chunk's loads are all in
-  // flight before its LDS atomics (one memory round trip per chunk, not per item)
+  // flight before its LDS atomics (one memory round trip per chunk, not per
+  // item); a single chunk (up to 16,384 items) stays in registers for the
+  // scatter below
   const int stride = (int)blockDim.x;
+  const bool one = total <= stride * kSortIpt;
+  int ev[kSortIpt];
+  float wv[kSortIpt];
   for (int i0 = 0; i0 < total; i0 += stride * kSortIpt) {
-    int ev[kSortIpt];
 #pragma unroll
     for (int u = 0; u < kSortIpt; ++u) {
       const int i = i0 + u * stride + tid;
       ev[u] = (i < total) ? top_i[i] : -1;
+      wv[u] = (i < total && one) ? top_w[i] : 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < kSortIpt; ++u)
       if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[ev[u]], 1);
   }
   __syncthreads();
-  if (tid == 0) {
-    int o = 0, to = 0;
-    for (int e = 0; e < E; ++e) {
-      off[e] = o;
-      cur[e] = 0;
-      toff[e] = to;
-      o += cnt[e];
-      to += (cnt[e] + tile_rows - 1) / tile_rows;
+  // expert offsets and tile offsets: an exclusive scan over the experts in
+  // one wave (lane l holds experts 4l .. 4l + 3, E <= 256)
+  if (tid < 64) {
+    int c[4], t[4], sc = 0, stl = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * tid + q;
+      c[q] = (e < E) ? cnt[e] : 0;
+      t[q] = (c[q] + tile_rows - 1) / tile_rows;
+      sc += c[q];
+      stl += t[q];
     }
-    ntiles[0] = to;
+    int ic = sc, it = stl;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(ic, d, 64), z = __shfl_up(it, d, 64);
+      if (tid >= d) {
+        ic += y;
+        it += z;
+      }
+    }
+    int o = ic - sc, to = it - stl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * tid + q;
+      if (e < E) {
+        off[e] = o;
+        toff[e] = to;
+        cur[e] = 0;
+      }
+      o += c[q];
+      to += t[q];
+    }
+    if (tid == 63) ntiles[0] = it;
   }
   __syncthreads();
   for (int i0 = 0; i0 < total; i0 += stride * kSortIpt) {
-    int ev[kSortIpt];
-    float wv[kSortIpt];
+    if (!one) {
 #pragma unroll
-    for (int u = 0; u < kSortIpt; ++u) {
-      const int i = i0 + u * stride + tid;
-      ev[u] = (i < total) ? top_i[i] : -1;
-      wv[u] = (i < total) ? top_w[i] : 0.0f;
+      for (int u = 0; u < kSortIpt; ++u) {
+        const int i = i0 + u * stride + tid;
+        ev[u] = (i < total) ? top_i[i] : -1;
+        wv[u] = (i < total) ? top_w[i] : 0.0f;
+      }
     }
 #pragma unroll
     for (int u = 0; u < kSortIpt; ++u) {
