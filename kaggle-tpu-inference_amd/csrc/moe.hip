@@ -453,40 +453,53 @@ __global__ __launch_bounds__(256) void router_scores_mfma_kernel(const uint16_t*
   u32x4 wq[PF];
 #pragma unroll
   for (int u = 0; u < PF; ++u) wq[u] = ld16(wrow + 4 * min(u, CH / 4 - 1));
-  for (int rr = 0; rr < kRouterMRows / 4; ++rr) {
-    const int r = wave * (kRouterMRows / 4) + rr;
-    const u32x4* xr = (const u32x4*)(x + (size_t)min(r0 + r, N - 1) * H);
+  // the wave's 4 token rows and both norm weights, all requested at once
+  // (one round trip, not three per row), then normalised from registers
+  constexpr int RW = kRouterMRows / 4;                 // rows per wave
+  constexpr int XPL = (kRouterMaxH / 8 + 63) / 64;     // 16-byte chunks per lane and row
+  u32x4 xv[RW][XPL], pwv[XPL], scv[XPL];
+#pragma unroll
+  for (int j = 0; j < XPL; ++j) {
+    const int cc = min(lane + 64 * j, CH - 1);
+    pwv[j] = ld16((pre_w != nullptr ? pw : sw) + cc);
+    scv[j] = ld16(sw + cc);
+#pragma unroll
+    for (int rr = 0; rr < RW; ++rr) {
+      const int r = wave * RW + rr;
+      xv[rr][j] = ld16((const u32x4*)(x + (size_t)min(r0 + r, N - 1) * H) + cc);
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < RW; ++rr) {
+    const int r = wave * RW + rr;
     float rp = 1.0f;
     if (pre_w != nullptr) {  // pre_feedforward_layernorm_2 (model.py:315)
       double s0 = 0.0;
-      for (int c8 = lane; c8 < CH; c8 += 64) s0 = sumsq8_f64(ld16(xr + c8), s0);
+#pragma unroll
+      for (int j = 0; j < XPL; ++j)
+        if (lane + 64 * j < CH) s0 = sumsq8_f64(xv[rr][j], s0);
       rp = rms_scale(group_sum_f64<64>(s0), H, eps);
+#pragma unroll
+      for (int j = 0; j < XPL; ++j) xv[rr][j] = scale8(xv[rr][j], rp, &pwv[j]);
     }
     double s1 = 0.0;
-    for (int c8 = lane; c8 < CH; c8 += 64) {
-      u32x4 v = ld16(xr + c8);
-      if (pre_w != nullptr) {
-        const u32x4 wc = ld16(pw + c8);
-        v = scale8(v, rp, &wc);
-      }
-      s1 = sumsq8_f64(v, s1);
-    }
-    const float r1 = rms_scale(group_sum_f64<64>(s1), H, eps);
-    for (int c8 = lane; c8 < CH; c8 += 64) {
-      u32x4 v = ld16(xr + c8);
-      if (pre_w != nullptr) {
-        const u32x4 wc = ld16(pw + c8);
-        v = scale8(v, rp, &wc);
-      }
-      const u32x4 sc = ld16(sw + c8);
-      float f[8], g[8];
-      unpack8(v, f);
-      unpack8(sc, g);
 #pragma unroll
-      for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r1) * g[q]) * inv_sqrt_h_bf);
-      u32x4 o;
-      o.x = pack2(f[0], f[1]); o.y = pack2(f[2], f[3]); o.z = pack2(f[4], f[5]); o.w = pack2(f[6], f[7]);
-      xs_rows[r * CH + c8] = o;
+    for (int j = 0; j < XPL; ++j)
+      if (lane + 64 * j < CH) s1 = sumsq8_f64(xv[rr][j], s1);
+    const float r1 = rms_scale(group_sum_f64<64>(s1), H, eps);
+#pragma unroll
+    for (int j = 0; j < XPL; ++j) {
+      const int c8 = lane + 64 * j;
+      if (c8 < CH) {
+        float f[8], g[8];
+        unpack8(xv[rr][j], f);
+        unpack8(scv[j], g);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) f[q] = rbf(rbf(rbf(f[q] * r1) * g[q]) * inv_sqrt_h_bf);
+        u32x4 o;
+        o.x = pack2(f[0], f[1]); o.y = pack2(f[2], f[3]); o.z = pack2(f[4], f[5]); o.w = pack2(f[6], f[7]);
+        xs_rows[r * CH + c8] = o;
+      }
     }
   }
   __syncthreads();
