@@ -7,11 +7,12 @@ each a replay of one captured HIP graph (engine.py:57-93; the layer loop of
 model.py:365-371).  Two prompts:
 
   * 54 tokens (the decode benchmark's prompt): 4 decode steps at positions
-    54-57 through the graph whose full layers are sized for 8,192 positions
-    (212 kernels per token);
-  * 8,190 tokens: 4 decode steps at positions 8,190-8,193, crossing from
-    that graph into the one sized for the whole cache at 8,192 (217 kernels
-    per token: the long-range attention kernels and their split reduction).
+    54-57 through the graph whose full layers are sized for 1,024 positions
+    (182 kernels per token: one attention launch on every layer);
+  * 8,190 tokens: 4 decode steps at positions 8,190-8,193, from the graph
+    sized for 8,192 positions (187 kernels per token) into the one sized for
+    the whole cache at 8,192 (192 kernels per token: the long-range
+    attention kernels and their split reduction).
 
 For each prompt the oracle takes the GPU's K/V rows of positions 0..P-2,
 then runs the prompt's last token and the GPU's tokens itself (torch-CPU,
