@@ -130,7 +130,11 @@ __host__ __device__ __forceinline__ bool tile_of(int bid, int mtiles, int ntiles
   return true;
 }
 
-template <int BM, int BN, int ST, int OCC, int EP>
+// K-step offset per group of grouped tiles (coprime with the K step counts
+// of the expert products, 44 and 11)
+constexpr int kKRot = 7;
+
+template <int BM, int BN, int ST, int OCC, int EP, bool GR>
 __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
   constexpr int WM = BM / 2, WN = BN / 2;    // wave tile
   constexpr int FM = WM / 16, FN = WN / 16;  // MFMA fragments per wave
@@ -153,7 +157,7 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
 
   // ---- this block's tile
   int group = 0, m0, m1, tx, ty;
-  if (g.tiles != nullptr) {
+  if constexpr (GR) {  // grouped tiles (g.tiles)
     if (!tile_of(blockIdx.x, g.ntiles[0], ncol_tiles, tx, ty, true)) return;
     const GemmTile t = g.tiles[tx];
     group = t.group;
@@ -172,6 +176,12 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
   const int ks0 = (ksteps_all * (int)blockIdx.z) / kslices;
   const int ks1 = (ksteps_all * ((int)blockIdx.z + 1)) / kslices;
   const int nks = ks1 - ks0;
+  // grouped tiles start their K walk at an offset set by the group (the
+  // tiles in flight then request different K slices of their weight rows),
+  // and request their weights with the non-temporal policy (each weight byte
+  // of a grouped product is read by one tile; the dense products' weights
+  // are shared by every row tile and stay cached)
+  const int krot = GR ? (group * kKRot) % ksteps_all : 0;
 
   // ---- DMA sources: instruction j of this wave fills tile rows
   // (wave*AI + j)*8 + lane/8, slot lane%8 (chunk (lane%8) ^ sw(row)).  Rows
@@ -225,7 +235,9 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
   auto issue1 = [&](int ks, auto sc, auto qc) __attribute__((always_inline)) {
     constexpr int q = decltype(qc)::value;
     uint8_t* s = sbase(sc);
-    const uint32_t kb = (uint32_t)ks * kBK * 2u;
+    int kse = ks;
+    if constexpr (GR) kse += krot - ((ks + krot >= ksteps_all) ? ksteps_all : 0);
+    const uint32_t kb = (uint32_t)kse * kBK * 2u;
     const char* gp;
     uint32_t l;
     if constexpr (q < AI) {
@@ -235,10 +247,16 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
       gp = bsrc[q - AI] + kb;
       l = (uint32_t)(uintptr_t)(s + BM * 128 + (wave * BI + q - AI) * 1024);
     }
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :
-                 : "v"(gp), "s"(__builtin_amdgcn_readfirstlane(l))
-                 : "memory", "m0");
+    if constexpr (q >= AI && GR)
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt"
+                   :
+                   : "v"(gp), "s"(__builtin_amdgcn_readfirstlane(l))
+                   : "memory", "m0");
+    else
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                   :
+                   : "v"(gp), "s"(__builtin_amdgcn_readfirstlane(l))
+                   : "memory", "m0");
   };
   struct Frag {
     u32x4 a[FM], b[FN];
@@ -541,7 +559,8 @@ static void launch(const GemmArgs& g, int64_t mtiles, hipStream_t st) {
   const int ncol = (EP == kEpGated) ? BN / 2 : BN;
   const int64_t nb = mtiles * ((g.N + ncol - 1) / ncol);
   dim3 grid((unsigned)(((nb + 7) / 8) * 8), 1, (unsigned)g.k_slices);
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, ST, OCC, EP>), grid, dim3(256), 0, st, g);
+  if (g.tiles != nullptr) hipLaunchKernelGGL((gemm_kernel<BM, BN, ST, OCC, EP, true>), grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((gemm_kernel<BM, BN, ST, OCC, EP, false>), grid, dim3(256), 0, st, g);
 }
 
 int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const uint16_t* b, int64_t ldb,
