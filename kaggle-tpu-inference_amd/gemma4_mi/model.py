@@ -7,6 +7,7 @@ signatures; the math runs in libg4mi's gfx950 kernels.
 from __future__ import annotations
 
 import math
+import os
 
 import torch
 
@@ -526,6 +527,12 @@ class PrefillRunner:
             self.top_w = z(cap, cfg.top_k_experts, dt=torch.float32)
             self.top_i = z(cap, cfg.top_k_experts, dt=torch.int32)
         self.pos = torch.arange(cap, dtype=torch.int32, device=dev)
+        # a second stream (default priority) for the dense MLP beside the MoE
+        # block (see run); G4MI_PREFILL_STREAMS=0 keeps one stream
+        use_side = moe and os.environ.get("G4MI_PREFILL_STREAMS", "1") != "0"
+        self.side = torch.cuda.Stream(device=dev) if use_side else None
+        self.ev_fork = torch.cuda.Event() if use_side else None
+        self.ev_join = torch.cuda.Event() if use_side else None
         self.rope = rope if rope is not None else {
             SLIDING: rope_table(cfg.head_dim, cfg.rope_theta_sliding, 1.0, self.max_len, dev),
             FULL: rope_table(cfg.global_head_dim, cfg.rope_theta_full, cfg.rope_partial_rotary_factor_full,
@@ -575,14 +582,32 @@ class PrefillRunner:
                                lp.get("pre_feedforward_layernorm_2"), eps, x1, xm, xe)
             gate, up = lp["mlp.gate_proj"], lp["mlp.up_proj"]
             act = self.act[:n]
-            ops.prefill_gemm(xm, gate, act, epilogue=ops.EP_GATED,
-                             pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0])
-            ops.prefill_gemm(act, lp["mlp.down_proj"], mlp_out)
+
+            def dense_mlp(ws_key="gemm"):
+                ops.prefill_gemm(xm, gate, act, epilogue=ops.EP_GATED,
+                                 pair_offset=(up.data_ptr() - gate.data_ptr()) // 2, n=gate.shape[0], ws_key=ws_key)
+                ops.prefill_gemm(act, lp["mlp.down_proj"], mlp_out, ws_key=ws_key)
+
+            if moe and self.side is not None:
+                # the dense MLP and the MoE block read the same normed rows and
+                # meet only in the layer tail: the dense MLP (MFMA-bound) runs
+                # on a second stream beside the router and the expert products
+                # (bound by their weight stream)
+                main = torch.cuda.current_stream()
+                self.ev_fork.record(main)
+                self.side.wait_event(self.ev_fork)
+                with torch.cuda.stream(self.side):
+                    dense_mlp("gemm_side")
+                    self.ev_join.record(self.side)
+            else:
+                dense_mlp()
             if moe:
                 tw, ti = self.top_w[:n], self.top_i[:n]
                 ops.moe_router_topk(xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],
                                     cfg.top_k_experts, eps, out=(tw, ti))
                 ops.moe_prefill(xe, tw, ti, lp["experts.gate_up_proj"], lp["experts.down_proj"], out=moe_out)
+                if self.side is not None:
+                    torch.cuda.current_stream().wait_event(self.ev_join)
             if i + 1 < L:
                 ops.rows_tail(x1, mlp_out, moe_out, lp.get("post_feedforward_layernorm_1"),
                               lp.get("post_feedforward_layernorm_2"), lp["post_feedforward_layernorm"],

@@ -460,14 +460,15 @@ EP_BF16, EP_F32, EP_GATED = 0, 1, 2
 
 
 def gemm(a, b, out=None, a_rows=None, epilogue=EP_BF16, pair_offset=0, n=None, row_scale=None, k_slices=1,
-         lda=None, ldc=None, tiles=None, ntiles=None, m=None):
+         lda=None, ldc=None, tiles=None, ntiles=None, m=None, ws_key="gemm"):
     """C = A[a_rows] . B^T on MFMA (bf16 in, f32 accumulate).
 
     a [*, K] bf16; b [N, K] bf16, or [G, ..., N, K] groups selected per
     64-row tile by `tiles` (int32 [T, 3] of (group, m0, m1), live count in
     `ntiles`, int32 [1]).  epilogue EP_BF16, EP_F32, or EP_GATED with the up
     rows at b + pair_offset elements and row_scale [M] f32 (n = gate rows).
-    out [M, N] (row stride ldc)."""
+    out [M, N] (row stride ldc).  ws_key names the split-K workspace (calls
+    that may run at the same time on different streams need their own)."""
     K = a.shape[-1]
     M = m if m is not None else (a_rows.numel() if a_rows is not None else a.shape[0])
     N = n if n is not None else b.shape[-2]
@@ -478,7 +479,7 @@ def gemm(a, b, out=None, a_rows=None, epilogue=EP_BF16, pair_offset=0, n=None, r
     ws = None
     nbytes = int(_lib.lib().g4mi_gemm_workspace_bytes(M, N, k_slices))
     if nbytes:
-        ws = WORKSPACE.get(a.device, "gemm", nbytes)
+        ws = WORKSPACE.get(a.device, ws_key, nbytes)
     group_stride = b.stride(0) if (tiles is not None and b.dim() >= 3) else 0
     _lib.call("g4mi_gemm_bf16", _ptr(a), a.stride(0) if lda is None else lda, _ptr(a_rows), _ptr(b), b.stride(-2),
               group_stride, int(pair_offset), M, N, K, _ptr(tiles), _ptr(ntiles),
@@ -580,7 +581,7 @@ def rows_tail(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, n
               stream_handle(x1.device))
 
 
-def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256):
+def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256, ws_key="gemm"):
     """gemm() for the batched prefill: activations a [M, K] times the weight
     rows w [N, K] on the MFMA kernels (M <= 16: the skinny kernel; more rows:
     the tile kernel, split over K when there are fewer tiles than `blocks`);
@@ -594,7 +595,7 @@ def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256)
         tiles = ((M + tm - 1) // tm) * ((N + 127) // 128)
         if tiles < blocks:
             k_slices = max(1, min((blocks + tiles - 1) // tiles, K // 128, 16))
-    return gemm(a, w, out=out, epilogue=epilogue, pair_offset=pair_offset, n=N, k_slices=k_slices)
+    return gemm(a, w, out=out, epilogue=epilogue, pair_offset=pair_offset, n=N, k_slices=k_slices, ws_key=ws_key)
 
 
 def q_norm_rope(q, q_norm, rope_cos, rope_sin, p0, eps):
