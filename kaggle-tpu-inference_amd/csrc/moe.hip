@@ -505,7 +505,9 @@ __global__ __launch_bounds__(256) void router_scores_mfma_kernel(const uint16_t*
   __syncthreads();
   if (e0 >= E) return;  // no barrier below
   const u32x4* xrow = xs_rows + (lane & 15) * CH + (lane >> 4);
-  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+  // two accumulator chains (even and odd k slots of each MFMA group), so
+  // consecutive MFMAs do not wait for each other's result; summed at the end
+  f64x4 acc[2] = {{0.0, 0.0, 0.0, 0.0}, {0.0, 0.0, 0.0, 0.0}};
   const int nch = CH / 4;  // 32-wide k chunks
   for (int c0 = 0; c0 < nch; c0 += PF) {
 #pragma unroll
@@ -520,7 +522,7 @@ __global__ __launch_bounds__(256) void router_scores_mfma_kernel(const uint16_t*
         for (int s = 0; s < 8; ++s) {
           const double a = (double)((s & 1) ? bf_hi(xw[s >> 1]) : bf_lo(xw[s >> 1]));
           const double b = (double)((s & 1) ? bf_hi(ww[s >> 1]) : bf_lo(ww[s >> 1]));
-          acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc, 0, 0, 0);
+          acc[s & 1] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[s & 1], 0, 0, 0);
         }
       }
     }
@@ -529,7 +531,7 @@ __global__ __launch_bounds__(256) void router_scores_mfma_kernel(const uint16_t*
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int n = r0 + 4 * r + (lane >> 4);
-    if (n < N && e < E) scores[(size_t)n * E + e] = rbf(f32_of(acc[r]));
+    if (n < N && e < E) scores[(size_t)n * E + e] = rbf(f32_of(acc[0][r] + acc[1][r]));
   }
 }
 
