@@ -123,8 +123,8 @@ __global__ __launch_bounds__(256) void layer_in_kernel(InArgs a) {
   if constexpr (MODE == kInTail) tail_compute(x, T, a.tail.moe != nullptr, H, a.eps, red);
   if constexpr (MODE != kInNormed) {
     // the residual store is issued after the last reduction, so no barrier
-    // waits for it
-    const float r = vrms(x, H, a.eps, red);
+    // waits for it (the norm's round in a region of its own)
+    const float r = vrms<256, true>(x, H, a.eps, red + 12);
     if (blockIdx.x == 0 && a.x_out != nullptr) vstore(x, (u32x4*)a.x_out, NCH);
     vscale_w(x, r, win);
   }
@@ -274,10 +274,11 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
   u32x4 w[kFfnInTasks][IT];
   load_row<32, IT>(dense ? dense_row(min(t0 + wave, tlast)) : a.r_proj + (size_t)min(e, a.E - 1) * H, l, w[0]);
   // x1 = bf16(x + rms(o, post_attention_ln)); xm = rms(x1, pre_ff); xe = rms(x1, pre_ff_2)
-  vscale_w(o, vrms(o, H, a.eps, red), wpa);
+  // the three norms' reduction rounds in regions of their own (red[0, 12))
+  vscale_w(o, vrms<256, true>(o, H, a.eps, red), wpa);
   vadd(x, o);
   if (bid == 0) vstore(x, (u32x4*)a.x1_out, NCH);
-  const float r1 = vrms(x, H, a.eps, red);
+  const float r1 = vrms<256, true>(x, H, a.eps, red + 4);
   if (dense) {
     vscale_w(x, r1, wf);
     vstore(x, xs, NCH);
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(256) void ffn_in_kernel(FfnInArgs a) {
     vscale_w(xe, r1, wf);
     if (rb == 0) vstore(xe, (u32x4*)a.xe_out, NCH);
     // router input x2 = bf16(bf16(rms(xe) * scale) * bf16(H^-0.5)) (model.py:225-226)
-    const float r2 = vrms(xe, H, a.eps, red);
+    const float r2 = vrms<256, true>(xe, H, a.eps, red + 8);
 #pragma unroll
     for (int j = 0; j < Vec::NC; ++j) {
       const int c = tid + 256 * j;
@@ -466,7 +467,7 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
   // the next layer's input norm (model.py:298) once, so the next kernel
   // starts from the normalised vector instead of three dependent reductions.
   __shared__ int flag;
-  __shared__ double red[2 * NT / 64];
+  __shared__ double red[4 * NT / 64];
   if (!arrive_last_grid(a.counter, &flag)) return;
   const int nch = a.H / 8;
   TailRegs<NT> T;
@@ -482,7 +483,7 @@ __global__ __launch_bounds__(kOutThreads) void ffn_out_kernel(FfnOutArgs a) {
   vload(wn, a.w_next, nch);
   T.ls = a.tail.ls[0];
   tail_compute(x, T, a.e_down != nullptr, a.H, a.eps, red);
-  const float r = vrms(x, a.H, a.eps, red);
+  const float r = vrms<NT, true>(x, a.H, a.eps, red + 3 * NT / 64);
   vstore(x, (u32x4*)a.x_out, nch);
   vscale_w(x, r, wn);
   vstore(x, (u32x4*)a.xn_out, nch);
@@ -534,7 +535,7 @@ __global__ __launch_bounds__(256) void lmhead_kernel(LmArgs a) {
   load_row<32, IT>(a.embed + (size_t)min(r, a.V - 1) * H, l, w);
   if constexpr (!NORMED) {
     tail_compute(x, T, a.tail.moe != nullptr, H, a.eps, red);
-    vscale_w(x, vrms(x, H, a.eps, red), wn0);
+    vscale_w(x, vrms<256, true>(x, H, a.eps, red + 12), wn0);
   }
   vstore(x, xs, NCH);
   __syncthreads();

@@ -339,7 +339,7 @@ __global__ __launch_bounds__(256) void rows_post_attn_kernel(const uint16_t* __r
 __global__ __launch_bounds__(256) void rows_tail_kernel(TailArgs ta, const uint16_t* __restrict__ w_next, int H,
                                                         float eps, uint16_t* __restrict__ x_out,
                                                         uint16_t* __restrict__ xn_out) {
-  __shared__ double red[8];
+  __shared__ double red[16];
   const int t = blockIdx.x, nch = H / 8;
   const size_t ro = (size_t)t * H;
   TailArgs tr = ta;
@@ -351,7 +351,7 @@ __global__ __launch_bounds__(256) void rows_tail_kernel(TailArgs ta, const uint1
   tail_load(T, tr, nch);
   vload(wn, w_next, nch);
   tail_compute(x, T, tr.moe != nullptr, H, eps, red);
-  const float r = vrms(x, H, eps, red);
+  const float r = vrms<256, true>(x, H, eps, red + 12);
   vstore(x, (u32x4*)(x_out + ro), nch);
   vscale_w(x, r, wn);
   vstore(x, (u32x4*)(xn_out + ro), nch);

@@ -99,12 +99,14 @@ __device__ __forceinline__ void vstore(const VecT<NT>& v, u32x4* dst, int nch) {
     if (c < nch) dst[c] = v.c[j];
   }
 }
-// `red` holds 2*NT/64 doubles (block_sum2_f64 uses both halves)
-template <int NT>
+// `red` holds NT/64 doubles.  FRESH: no thread of the block reads `red`
+// any more (a region not used before in the kernel), so the barrier that
+// orders this round's stores after an earlier round's reads is left out.
+template <int NT, bool FRESH = false>
 __device__ __forceinline__ double block_sum_nt(double v, double* red) {
   constexpr int NW = NT / 64;
   v = group_sum_f64<kWave>(v);
-  __syncthreads();
+  if constexpr (!FRESH) __syncthreads();
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
   __syncthreads();
   double t = red[0];
@@ -112,9 +114,9 @@ __device__ __forceinline__ double block_sum_nt(double v, double* red) {
   for (int i = 1; i < NW; ++i) t += red[i];
   return t;
 }
-template <int NT>
+template <int NT, bool FRESH = false>
 __device__ __forceinline__ float vrms(const VecT<NT>& v, int H, float eps, double* red) {
-  return rms_scale(block_sum_nt<NT>(vsumsq(v), red), H, eps);
+  return rms_scale(block_sum_nt<NT, FRESH>(vsumsq(v), red), H, eps);
 }
 
 // v = bf16(v * r * w) with the weight already in registers
@@ -123,14 +125,15 @@ __device__ __forceinline__ void vscale_w(VecT<NT>& v, float r, const VecT<NT>& w
 #pragma unroll
   for (int j = 0; j < VecT<NT>::NC; ++j) v.c[j] = scale8(v.c[j], r, &w.c[j]);
 }
-// Two block sums in one reduction round.
-template <int NT>
+// Two block sums in one reduction round (`red`: 2*NT/64 doubles; FRESH as
+// in block_sum_nt).
+template <int NT, bool FRESH = false>
 __device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red) {
   constexpr int NW = NT / 64;
   a = group_sum_f64<kWave>(a);
   b = group_sum_f64<kWave>(b);
   const int w = threadIdx.x >> 6;
-  __syncthreads();
+  if constexpr (!FRESH) __syncthreads();
   if ((threadIdx.x & 63) == 0) {
     red[w] = a;
     red[NW + w] = b;
@@ -148,8 +151,9 @@ __device__ __forceinline__ void block_sum2_f64(double& a, double& b, double* red
 
 // Tail of the previous layer: x = bf16(bf16(x1 + rms(hs, post_ff)) * ls),
 // hs = bf16(rms(mlp, post_ff_1) + rms(moe, post_ff_2)), or hs = mlp without MoE.
-// All operands are loaded up front (one memory round trip), then three
-// dependent reduction rounds follow.  `red` holds 2*NT/64 doubles.
+// All operands are loaded up front (one memory round trip), then two
+// dependent reduction rounds follow.  `red`: 3*NT/64 doubles the block has
+// not used before (callers keep red[3*NT/64, 4*NT/64) for their next norm).
 struct TailArgs {
   const uint16_t *x1, *mlp, *moe, *w_pf1, *w_pf2, *w_pf, *ls;
 };
@@ -173,14 +177,17 @@ __device__ __forceinline__ void tail_load(TailRegs<NT>& T, const TailArgs& t, in
 }
 template <int NT>
 __device__ __forceinline__ void tail_compute(VecT<NT>& x, TailRegs<NT>& T, bool moe, int H, float eps, double* red) {
+  // each reduction round in a region of its own (red[0, 3*NT/64), fresh):
+  // one barrier per round
+  constexpr int NW = NT / 64;
   if (moe) {
     double s1 = vsumsq(T.a), s2 = vsumsq(T.b);
-    block_sum2_f64<NT>(s1, s2, red);
+    block_sum2_f64<NT, true>(s1, s2, red);
     vscale_w(T.a, rms_scale(s1, H, eps), T.w1);
     vscale_w(T.b, rms_scale(s2, H, eps), T.w2);
     vadd(T.a, T.b);
   }
-  vscale_w(T.a, vrms(T.a, H, eps, red), T.w3);
+  vscale_w(T.a, vrms<NT, true>(T.a, H, eps, red + 2 * NW), T.w3);
   x = T.x1;
   vadd(x, T.a);
   vmul(x, bf2f(T.ls));
