@@ -334,8 +334,10 @@ int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K
  * [n, K] int32, gate_up [E, 2, F, H], down [E, H, F] -> out [n, H] bf16 = bf16
  * of one f32 sum over the selected experts.  Unselected experts contribute
  * exact zeros in the reference (masked weights), so only the selected
- * (token, expert) pairs are computed, as grouped MFMA GEMMs.  n <= 65535,
- * E <= 256, K <= 32, H and F multiples of 64. */
+ * (token, expert) pairs are computed, as grouped MFMA GEMMs.  With out =
+ * NULL the combine is left out and each (token, slot) pair's f32 output stays
+ * in ws for g4mi_rows_tail_experts.  n <= 65535, E <= 256, K <= 32, H and F
+ * multiples of 64. */
 int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_t F, int64_t H);
 int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
                      const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
@@ -374,6 +376,17 @@ int g4mi_rows_tail(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* 
                    const uint16_t* post_ff1_ln, const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln,
                    const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps, uint16_t* x_out,
                    uint16_t* xn_out, void* stream);
+/* g4mi_rows_tail with moe_out = the combine of the per-expert outputs that
+ * g4mi_moe_prefill(out = NULL) left in its workspace moe_ws (the same n, K,
+ * E, F, H): moe[t] = bf16(f32 sum over the token's K slots in order,
+ * model.py:250), then the tail (model.py:312-322) and the next norm, in one
+ * launch.  Identical to g4mi_moe_prefill with out followed by g4mi_rows_tail.
+ * H = 64*i <= 4096. */
+int g4mi_rows_tail_experts(const uint16_t* x1, const uint16_t* mlp_out, int64_t n, int64_t K, int64_t E, int64_t F,
+                           const uint16_t* post_ff1_ln, const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln,
+                           const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps,
+                           uint16_t* x_out, uint16_t* xn_out, const void* moe_ws, int64_t moe_ws_bytes,
+                           void* stream);
 
 /* Prefill attention (model.py:195-215 at T > 1).  q_norm_rope: q = rope(
  * rms_norm(q, q_norm)) in place for T rows x NH heads at positions p0 + t

@@ -357,6 +357,72 @@ __global__ __launch_bounds__(256) void rows_tail_kernel(TailArgs ta, const uint1
   vstore(x, (u32x4*)(xn_out + ro), nch);
 }
 
+// rows_tail_kernel with the MoE output combined here: moe[t, h] =
+// bf16(sum over s < K, in order, of part[slot_pos[t*K + s], h]) (f32, as
+// moe_combine_kernel), then the tail.  Every slot's part chunks of this
+// thread are requested with the other operands, before the first add.
+constexpr int kTailSlots = 8;  // slots summed per pass
+__global__ __launch_bounds__(256) void rows_tail_combine_kernel(TailArgs ta, const float* __restrict__ part,
+                                                                const int32_t* __restrict__ slot_pos, int K,
+                                                                const uint16_t* __restrict__ w_next, int H, float eps,
+                                                                uint16_t* __restrict__ x_out,
+                                                                uint16_t* __restrict__ xn_out) {
+  __shared__ double red[16];
+  const int t = blockIdx.x, nch = H / 8;
+  const size_t ro = (size_t)t * H;
+  TailRegs<256> T;
+  Vec x, wn;
+  vload(T.a, ta.mlp + ro, nch);
+  vload(T.x1, ta.x1 + ro, nch);
+  vload(T.w3, ta.w_pf, nch);
+  vload(T.w1, ta.w_pf1, nch);
+  vload(T.w2, ta.w_pf2, nch);
+  T.ls = ta.ls[0];
+  vload(wn, w_next, nch);
+  float s[Vec::NC][8];
+#pragma unroll
+  for (int j = 0; j < Vec::NC; ++j)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[j][i] = 0.0f;
+  for (int q0 = 0; q0 < K; q0 += kTailSlots) {
+    int pv[kTailSlots];
+    float4 v[kTailSlots][Vec::NC][2];
+#pragma unroll
+    for (int u = 0; u < kTailSlots; ++u) {
+      pv[u] = (q0 + u < K) ? slot_pos[(size_t)t * K + q0 + u] : -1;
+#pragma unroll
+      for (int j = 0; j < Vec::NC; ++j) {
+        const int c = min((int)threadIdx.x + 256 * j, nch - 1);
+        const float4* src = (const float4*)(part + (size_t)max(pv[u], 0) * H + 8 * c);
+        v[u][j][0] = src[0];
+        v[u][j][1] = src[1];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kTailSlots; ++u) {
+      if (pv[u] < 0) continue;
+#pragma unroll
+      for (int j = 0; j < Vec::NC; ++j) {
+        s[j][0] += v[u][j][0].x; s[j][1] += v[u][j][0].y; s[j][2] += v[u][j][0].z; s[j][3] += v[u][j][0].w;
+        s[j][4] += v[u][j][1].x; s[j][5] += v[u][j][1].y; s[j][6] += v[u][j][1].z; s[j][7] += v[u][j][1].w;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < Vec::NC; ++j) {
+    const int c = (int)threadIdx.x + 256 * j;
+    u32x4 o;
+    o.x = pack2(s[j][0], s[j][1]); o.y = pack2(s[j][2], s[j][3]);
+    o.z = pack2(s[j][4], s[j][5]); o.w = pack2(s[j][6], s[j][7]);
+    T.b.c[j] = (c < nch) ? o : u32x4{0u, 0u, 0u, 0u};
+  }
+  tail_compute(x, T, true, H, eps, red);
+  const float r = vrms<256, true>(x, H, eps, red + 12);
+  vstore(x, (u32x4*)(x_out + ro), nch);
+  vscale_w(x, r, wn);
+  vstore(x, (u32x4*)(xn_out + ro), nch);
+}
+
 static int64_t al256(int64_t x) { return ((x + 255) / 256) * 256; }
 
 static float bf16_round_host(double v) {
@@ -413,7 +479,7 @@ int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_
 int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
                      const uint16_t* down, int64_t n, int64_t H, int64_t F, int64_t E, int64_t K, uint16_t* out,
                      void* ws, int64_t ws_bytes, void* stream) {
-  G4MI_REQUIRE(xn && top_w && top_i && gate_up && down && out && ws, G4MI_EINVAL, "moe_prefill: missing argument");
+  G4MI_REQUIRE(xn && top_w && top_i && gate_up && down && ws, G4MI_EINVAL, "moe_prefill: missing argument");
   G4MI_REQUIRE(n >= 1 && n <= 65535 && K >= 1 && K <= 32 && E >= 1 && E <= kMaxExperts, G4MI_EINVAL,
                "moe_prefill: bad n/K/E");
   G4MI_REQUIRE(H % 64 == 0 && F % 64 == 0, G4MI_EUNSUPPORTED, "moe_prefill: H and F must be multiples of 64");
@@ -435,6 +501,7 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
   rc = gemm_bf16_tiles(w.act, F, nullptr, down, F, H * F, 0, n * K, H, F, w.tiles, w.ntiles, max_tiles, 1, w.part,
                        H, nullptr, 1, nullptr, 0, tile_rows, stream);
   if (rc) return rc;
+  if (out == nullptr) return 0;  // the per-slot outputs stay in ws (g4mi_rows_tail_experts combines them)
   hipLaunchKernelGGL(moe_combine_kernel, dim3((unsigned)((H / 4 + 255) / 256), (unsigned)n), dim3(256), 0, st, w.part,
                      w.slot_pos, (int)n, (int)K, (int)H, 0, out);
   return check_launch("moe_prefill combine");
@@ -526,6 +593,27 @@ int g4mi_rows_tail(const uint16_t* x1, const uint16_t* mlp_out, const uint16_t* 
   hipLaunchKernelGGL(rows_tail_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), ta, next_ln, (int)H, eps,
                      x_out, xn_out);
   return check_launch("rows_tail");
+}
+
+int g4mi_rows_tail_experts(const uint16_t* x1, const uint16_t* mlp_out, int64_t n, int64_t K, int64_t E, int64_t F,
+                           const uint16_t* post_ff1_ln, const uint16_t* post_ff2_ln, const uint16_t* post_ff_ln,
+                           const uint16_t* layer_scalar, const uint16_t* next_ln, int64_t H, float eps,
+                           uint16_t* x_out, uint16_t* xn_out, const void* moe_ws, int64_t moe_ws_bytes,
+                           void* stream) {
+  G4MI_REQUIRE(x1 && mlp_out && post_ff1_ln && post_ff2_ln && post_ff_ln && layer_scalar && next_ln && x_out &&
+                   xn_out && moe_ws,
+               G4MI_EINVAL, "rows_tail_experts: missing argument");
+  G4MI_REQUIRE(n >= 1 && n <= 65535 && K >= 1 && K <= 32 && E >= 1 && E <= kMaxExperts, G4MI_EINVAL,
+               "rows_tail_experts: bad n/K/E");
+  G4MI_REQUIRE(H % 64 == 0 && H <= 4096 && F % 64 == 0, G4MI_EUNSUPPORTED,
+               "rows_tail_experts: H=%lld F=%lld (multiples of 64, H <= 4096)", (long long)H, (long long)F);
+  G4MI_REQUIRE(moe_ws_bytes >= g4mi_moe_prefill_workspace_bytes(n, K, E, F, H), G4MI_EWORKSPACE,
+               "rows_tail_experts: workspace smaller than the moe_prefill one it reads");
+  const MoePrefillWs w = moe_prefill_ws(const_cast<void*>(moe_ws), n, K, E, F, H);
+  const TailArgs ta{x1, mlp_out, nullptr, post_ff1_ln, post_ff2_ln, post_ff_ln, layer_scalar};
+  hipLaunchKernelGGL(rows_tail_combine_kernel, dim3((unsigned)n), dim3(256), 0, as_stream(stream), ta, w.part,
+                     w.slot_pos, (int)K, next_ln, (int)H, eps, x_out, xn_out);
+  return check_launch("rows_tail_experts");
 }
 
 }  // extern "C"

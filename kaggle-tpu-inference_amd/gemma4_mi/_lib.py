@@ -95,6 +95,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "g4mi_rows_post_attn": (_int, [_p, _p, _i64, _p, _p, _p, _i64, _f32, _p, _p, _p, _p]),
     "g4mi_rows_tail": (_int, [_p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _f32, _p, _p, _p]),
+    "g4mi_rows_tail_experts": (
+        _int,
+        [_p, _p, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _i64, _f32, _p, _p, _p, _i64, _p],
+    ),
     "g4mi_sample": (_int, [_p, _i64, _i64, _p, _i32, _p, _p, _p, _i64, _p, _i64, _p]),
     "g4mi_kv_append": (
         _int,

@@ -530,6 +530,9 @@ class PrefillRunner:
         # a second stream (default priority) for the dense MLP beside the MoE
         # block (see run); G4MI_PREFILL_STREAMS=0 keeps one stream
         use_side = moe and os.environ.get("G4MI_PREFILL_STREAMS", "1") != "0"
+        # the MoE combine inside the layer-tail kernel (G4MI_PREFILL_FUSED_TAIL=0:
+        # the combine kernel, then the tail)
+        self.fused_tail = os.environ.get("G4MI_PREFILL_FUSED_TAIL", "1") != "0"
         self.side = torch.cuda.Stream(device=dev) if use_side else None
         self.ev_fork = torch.cuda.Event() if use_side else None
         self.ev_join = torch.cuda.Event() if use_side else None
@@ -601,14 +604,24 @@ class PrefillRunner:
                     self.ev_join.record(self.side)
             else:
                 dense_mlp()
+            fused_tail = moe and i + 1 < L and self.fused_tail
             if moe:
                 tw, ti = self.top_w[:n], self.top_i[:n]
                 ops.moe_router_topk(xe, lp["router.scale"], lp["router.proj"], lp["router.per_expert_scale"],
                                     cfg.top_k_experts, eps, out=(tw, ti))
-                ops.moe_prefill(xe, tw, ti, lp["experts.gate_up_proj"], lp["experts.down_proj"], out=moe_out)
+                # with a tail to follow, the combine of the experts' outputs
+                # runs inside the tail kernel
+                moe_ws = ops.moe_prefill(xe, tw, ti, lp["experts.gate_up_proj"], lp["experts.down_proj"],
+                                         out=moe_out, combine=not fused_tail)
                 if self.side is not None:
                     torch.cuda.current_stream().wait_event(self.ev_join)
-            if i + 1 < L:
+            if fused_tail:
+                E, F = cfg.num_experts, cfg.moe_intermediate_size
+                ops.rows_tail_experts(x1, mlp_out, moe_ws, cfg.top_k_experts, E, F,
+                                      lp["post_feedforward_layernorm_1"], lp["post_feedforward_layernorm_2"],
+                                      lp["post_feedforward_layernorm"], lp["layer_scalar"],
+                                      self.layers[i + 1]["input_layernorm"], eps, x, xn)
+            elif i + 1 < L:
                 ops.rows_tail(x1, mlp_out, moe_out, lp.get("post_feedforward_layernorm_1"),
                               lp.get("post_feedforward_layernorm_2"), lp["post_feedforward_layernorm"],
                               lp["layer_scalar"], self.layers[i + 1]["input_layernorm"], eps, x, xn)

@@ -534,9 +534,10 @@ def moe_decode_grouped(xn, top_w, top_i, gate_up, down, combine="bf16_running", 
     return out
 
 
-def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
+def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None, combine=True):
     """model.py:241-250 for xn [n, H]: out [n, H] bf16 (selected experts only,
-    grouped MFMA GEMMs)."""
+    grouped MFMA GEMMs).  combine=False leaves the per-slot f32 outputs in the
+    workspace for rows_tail_experts and returns the workspace."""
     n, H = xn.shape
     E, _, F, _ = gate_up.shape
     K = top_i.shape[1]
@@ -545,14 +546,14 @@ def moe_prefill(xn, top_w, top_i, gate_up, down, out=None, ws=None):
     _need(top_i, torch.int32, "top_i", (n, K))
     _need(gate_up, BF16, "gate_up", (E, 2, F, H))
     _need(down, BF16, "down", (E, H, F))
-    if out is None:
+    if out is None and combine:
         out = torch.empty((n, H), dtype=BF16, device=xn.device)
     nbytes = int(_lib.lib().g4mi_moe_prefill_workspace_bytes(n, K, E, F, H))
     if ws is None:
         ws = WORKSPACE.get(xn.device, "moe_prefill", nbytes)
     _lib.call("g4mi_moe_prefill", _ptr(xn), _ptr(top_w), _ptr(top_i), _ptr(gate_up), _ptr(down), n, H, F, E, K,
-              _ptr(out), _ptr(ws), ws.numel(), stream_handle(xn.device))
-    return out
+              _ptr(out if combine else None), _ptr(ws), ws.numel(), stream_handle(xn.device))
+    return out if combine else ws
 
 
 # ------------------------------------------------------------------ prefill rows
@@ -579,6 +580,17 @@ def rows_tail(x1, mlp_out, moe_out, post_ff1, post_ff2, post_ff, layer_scalar, n
     _lib.call("g4mi_rows_tail", _ptr(x1), _ptr(mlp_out), _ptr(moe_out), n, _ptr(post_ff1), _ptr(post_ff2),
               _ptr(post_ff), _ptr(layer_scalar), _ptr(next_ln), H, float(eps), _ptr(x_out), _ptr(xn_out),
               stream_handle(x1.device))
+
+
+def rows_tail_experts(x1, mlp_out, moe_ws, K, E, F, post_ff1, post_ff2, post_ff, layer_scalar, next_ln, eps, x_out,
+                      xn_out):
+    """rows_tail with the MoE output combined from the per-slot outputs that
+    moe_prefill(combine=False) left in moe_ws (model.py:250, 312-322), in one
+    launch; identical to moe_prefill + rows_tail."""
+    n, H = x1.shape
+    _lib.call("g4mi_rows_tail_experts", _ptr(x1), _ptr(mlp_out), n, K, E, F, _ptr(post_ff1), _ptr(post_ff2),
+              _ptr(post_ff), _ptr(layer_scalar), _ptr(next_ln), H, float(eps), _ptr(x_out), _ptr(xn_out), _ptr(moe_ws),
+              moe_ws.numel(), stream_handle(x1.device))
 
 
 def prefill_gemm(a, w, out, epilogue=EP_BF16, pair_offset=0, n=None, blocks=256, ws_key="gemm"):

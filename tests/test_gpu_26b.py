@@ -314,18 +314,21 @@ def test_batched_prefill_256_matches_oracle(m26):
 @pytest.mark.parametrize("n", [300, 2048])
 def test_prefill_second_stream_is_bit_identical(m26, monkeypatch, n):
     """The batched prefill with the dense MLP on a second stream beside the
-    MoE block equals the one-stream prefill bit for bit: the last rows' tail
-    inputs and every layer's K/V cache rows (the two branches read the same
-    normed rows and meet only in the layer tail)."""
+    MoE block, and with the MoE combine inside the layer-tail kernel, equals
+    the one-stream prefill with the combine kernel bit for bit: the last
+    rows' tail inputs and every layer's K/V cache rows (the two branches
+    read the same normed rows and meet only in the layer tail; the fused
+    tail sums the slots in the combine kernel's order)."""
     cfg, params, *_ = m26
     prompt = torch.tensor(np.random.default_rng(9).integers(0, cfg.vocab_size, size=n), dtype=torch.int32,
                           device=DEV)
     got = []
-    for flag in ("1", "0"):
+    for flag, fused in (("1", "1"), ("0", "0"), ("1", "0")):
         monkeypatch.setenv("G4MI_PREFILL_STREAMS", flag)
+        monkeypatch.setenv("G4MI_PREFILL_FUSED_TAIL", fused)
         cache = gm.init_cache(cfg, None, 1, 2048, device=DEV)
         pr = gm.PrefillRunner(cfg, params, cache, n, device=DEV)
-        assert (pr.side is not None) == (flag == "1")
+        assert (pr.side is not None) == (flag == "1") and pr.fused_tail == (fused == "1")
         pr.run(prompt, n)
         torch.cuda.synchronize()
         rows = [t.clone() for t in (pr.x1[:n], pr.mlp_out[:n], pr.moe_out[:n])]
@@ -333,8 +336,9 @@ def test_prefill_second_stream_is_bit_identical(m26, monkeypatch, n):
         got.append(rows + kv)
         del pr, cache
         torch.cuda.empty_cache()
-    for a, b in zip(*got):
-        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    for other in got[1:]:
+        for a, b in zip(got[0], other):
+            assert torch.equal(a.view(torch.int16), b.view(torch.int16))
 
 
 def test_prefill_prefix_rows_do_not_depend_on_later_tokens(m26):

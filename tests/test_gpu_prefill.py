@@ -304,3 +304,29 @@ def test_moe_prefill_192_row_tiles_equal_128(monkeypatch, which, n):
                                 top_i[t : t + 1].contiguous(), g["experts.gate_up_proj"], g["experts.down_proj"])
         assert torch.equal(alone[0], outs["192"][t]), t
     assert bool(torch.isfinite(outs["192"].float()).all())
+
+
+@pytest.mark.parametrize("which,n", [("tiny", 37), ("tiny", 512), ("26b", 300)])
+def test_rows_tail_experts_equals_combine_then_tail(which, n):
+    """The layer tail with the MoE combine inside it (moe_prefill without its
+    combine, then rows_tail_experts) equals moe_prefill's combined output
+    followed by rows_tail, bit for bit (x and the next layer's normed x)."""
+    cfg = tiny_parity_config() if which == "tiny" else _C2Cfg()
+    H, K, E = cfg.hidden_size, cfg.top_k_experts, cfg.num_experts
+    g = {k: v.to(DEV) for k, v in _moe_params(cfg, 60).items()}
+    xe = _rand((n, H), 61).to(DEV)
+    x1, mlp = _rand((n, H), 62).to(DEV), _rand((n, H), 63, 0.5).to(DEV)
+    w1, w2, w3, wn = (_rand((H,), 64 + j).to(DEV) for j in range(4))
+    ls = _rand((1,), 70).to(DEV)
+    top_w, top_i = ops.moe_router_topk(xe, g["router.scale"], g["router.proj"], g["router.per_expert_scale"], K,
+                                       cfg.rms_norm_eps)
+    F = g["experts.down_proj"].shape[2]
+    moe = ops.moe_prefill(xe, top_w, top_i, g["experts.gate_up_proj"], g["experts.down_proj"])
+    xa, xna = torch.empty_like(x1), torch.empty_like(x1)
+    ops.rows_tail(x1, mlp, moe, w1, w2, w3, ls, wn, cfg.rms_norm_eps, xa, xna)
+    ws = ops.moe_prefill(xe, top_w, top_i, g["experts.gate_up_proj"], g["experts.down_proj"], combine=False)
+    xb, xnb = torch.empty_like(x1), torch.empty_like(x1)
+    ops.rows_tail_experts(x1, mlp, ws, K, E, F, w1, w2, w3, ls, wn, cfg.rms_norm_eps, xb, xnb)
+    torch.cuda.synchronize()
+    assert torch.equal(xa.view(torch.int16), xb.view(torch.int16))
+    assert torch.equal(xna.view(torch.int16), xnb.view(torch.int16))
