@@ -48,7 +48,36 @@ struct PfAttnArgs {
   uint16_t* ctx;            // [T, NH, D]
   int T, NH, KV, page, num_pages, max_pages, p0, window;
   float softcap;
+  int nqb;   // query blocks per KV head
+  int xmap;  // block order: 0 plain, 1 KV divides 8, 2 KV a multiple of 8
 };
+
+// Block order.  The launch is a 1-D grid whose blocks the dispatcher hands to
+// the 8 XCDs in turn (block b to the XCD of b % 8), and each XCD has its own
+// L2.  The query blocks of one KV head read the same K/V rows, so they are
+// kept on the XCDs of that head: with KV dividing 8, XCD x serves head
+// x % KV and every (8 / KV)-th query block of it (long and short blocks
+// alike, so the XCDs finish together); with KV a multiple of 8, XCD x serves
+// heads x, x + 8, ...; other head counts take the plain order (block b: head
+// b / nqb).  Within a head the query blocks go longest first.  Returns false
+// for the padding blocks of the first order.
+__device__ __forceinline__ bool pf_block(const PfAttnArgs& a, int& kv, int& qb) {
+  const int b = (int)blockIdx.x, x = b & 7, slot = b >> 3;
+  int j;
+  if (a.xmap == 1) {
+    kv = x % a.KV;
+    j = x / a.KV + (8 / a.KV) * slot;
+  } else if (a.xmap == 2) {
+    const int per = a.KV / 8;
+    kv = x + 8 * (slot % per);
+    j = slot / per;
+  } else {
+    kv = b / a.nqb;
+    j = b % a.nqb;
+  }
+  qb = a.nqb - 1 - j;
+  return j < a.nqb;
+}
 
 // ---------------------------------------------------------------- q norm + RoPE
 // q = rope(rms_norm(q_raw, q_norm)) in place for T rows of NH heads at
@@ -90,12 +119,28 @@ __global__ __launch_bounds__(256) void q_norm_rope_kernel(uint16_t* __restrict__
 }
 
 // ---------------------------------------------------------------- attention
-// max / sum over the 16 lanes of a DPP row (the 16 key columns of a tile row)
+// max / sum over the 16 lanes of a DPP row (the 16 key columns of a tile row).
+// The max is one v_max_f32 with a DPP operand per round (fmaxf on a DPP move
+// would add a move and two canonicalising maxes; the scores hold no NaN); the
+// s_nop gives the two wait states a DPP read of a just-written VGPR needs.
+template <int CTRL>
+__device__ __forceinline__ float dpp_max_f(float v) {
+  float r;
+  if constexpr (CTRL == kDppXor1)
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+  else if constexpr (CTRL == kDppXor2)
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+  else if constexpr (CTRL == kDppHalfMirror)
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_half_mirror row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+  else
+    asm("s_nop 1\n\tv_max_f32_dpp %0, %1, %1 row_mirror row_mask:0xf bank_mask:0xf" : "=v"(r) : "v"(v));
+  return r;
+}
 __device__ __forceinline__ float row16_max(float v) {
-  v = fmaxf(v, dpp_f<kDppXor1>(v));
-  v = fmaxf(v, dpp_f<kDppXor2>(v));
-  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
-  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  v = dpp_max_f<kDppXor1>(v);
+  v = dpp_max_f<kDppXor2>(v);
+  v = dpp_max_f<kDppHalfMirror>(v);
+  v = dpp_max_f<kDppMirror>(v);
   return v;
 }
 __device__ __forceinline__ float row16_sum(float v) {
@@ -106,7 +151,15 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-template <int D, int G>
+// p = bf16(e / l) from the reciprocal rl = rcp(l): e * rl lies within 3.5 f32
+// ulps of the rounded quotient (rcp within 1 ulp, the product's rounding), so
+// it rounds to the same bf16 unless it sits within 8 ulps of a bf16 rounding
+// midpoint (low 16 bits 0x7ff8..0x8008); those take the IEEE division.
+__device__ __forceinline__ bool near_bf16_midpoint(float x) {
+  return ((__float_as_uint(x) - 0x7ff8u) & 0xffffu) <= 16u;
+}
+
+template <int D, int G, bool CAP>
 __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttnArgs a) {
   constexpr int NW = pf_waves<D>();
   constexpr int NTH = 64 * NW;              // threads
@@ -124,9 +177,8 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
   __shared__ __align__(16) uint16_t pt[ROWS * LDP];
   __shared__ int ptl[kPfPtl];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int kv = blockIdx.y;
-  const int nqb = (a.T + QP - 1) / QP;
-  const int qb = nqb - 1 - (int)blockIdx.x;  // longest rows first
+  int kv, qb;
+  if (!pf_block(a, kv, qb)) return;
   const int t0 = qb * QP;
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
@@ -154,6 +206,13 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
   const int k_lo = (a.window > 0) ? max(0, pos_first + 1 - a.window) : 0;
   const int kb0 = k_lo / KB, kb1 = pos_last / KB;
   const float cap = a.softcap;
+  // key block kb is interior when every row of the block attends all its keys
+  // (no mask, no -inf score); the others (the diagonal, the window's start)
+  // take the masked steps
+  const int lo_max = (a.window > 0) ? max(0, pos_last + 1 - a.window) : 0;
+  auto interior = [&](int kb) { return kb * KB >= lo_max && kb * KB + KB - 1 <= pos_first; };
+  using Edge = std::true_type;
+  using Inner = std::false_type;
 
   // the block's page-table entries, staged once (a barrier follows before use)
   const int first_pg = (kb0 * KB) / a.page;
@@ -211,7 +270,7 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
     }
   };
   // scores of this wave's 16 rows x KB keys: s[n][i] = row 4(l/16)+i, key k0 + 16n + l%16
-  auto scores = [&](int kb, float (*s)[4]) {
+  auto scores = [&](int kb, float (*s)[4], auto edge) {
     const int k0 = kb * KB;
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -226,9 +285,13 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float sv = rbf(acc[i]);
-        if (cap > 0.0f) sv = tanhf(sv / cap) * cap;
-        const int lo = (a.window > 0) ? max(0, rpos[i] + 1 - a.window) : 0;
-        s[n][i] = (j >= lo && j <= rpos[i]) ? sv : -INFINITY;
+        if constexpr (CAP) sv = tanhf(sv / cap) * cap;
+        if constexpr (decltype(edge)::value) {
+          const int lo = (a.window > 0) ? max(0, rpos[i] + 1 - a.window) : 0;
+          s[n][i] = (j >= lo && j <= rpos[i]) ? sv : -INFINITY;
+        } else {
+          s[n][i] = sv;
+        }
       }
     }
   };
@@ -249,13 +312,13 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
     m[i] = -INFINITY;
     l[i] = 0.0f;
   }
-  auto step1 = [&](int q, Tile& T) {
+  auto step1 = [&](int q, Tile& T, auto edge) {
     lds_barrier();
     put(T, false);
     target(q + 1, T);
     lds_barrier();
     float s[NT][4];
-    scores(kb0 + q, s);
+    scores(kb0 + q, s, edge);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float bm = s[0][i];
@@ -264,9 +327,14 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       bm = row16_max(bm);
       const float mn = fmaxf(m[i], bm);
       float e = 0.0f;
-      if (mn != -INFINITY) {
+      if constexpr (decltype(edge)::value) {
+        if (mn != -INFINITY) {
 #pragma unroll
-        for (int n = 0; n < NT; ++n) e += (s[n][i] == -INFINITY) ? 0.0f : expf(s[n][i] - mn);
+          for (int n = 0; n < NT; ++n) e += (s[n][i] == -INFINITY) ? 0.0f : expf(s[n][i] - mn);
+        }
+      } else {
+#pragma unroll
+        for (int n = 0; n < NT; ++n) e += expf(s[n][i] - mn);
       }
       e = row16_sum(e);
       l[i] = (m[i] == -INFINITY) ? e : l[i] * expf(m[i] - mn) + e;
@@ -276,24 +344,39 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
   Tile tile;
   lds_barrier();  // ptl
   target(0, tile);
-  for (int q = 0; q < n; ++q) step1(q, tile);
+  {
+    int q = 0;
+    for (; q < n && !interior(kb0 + q); ++q) step1(q, tile, Edge{});
+    for (; q < n && interior(kb0 + q); ++q) step1(q, tile, Inner{});
+    for (; q < n; ++q) step1(q, tile, Edge{});
+  }
 
   f32x4 o[DT];
 #pragma unroll
   for (int dt = 0; dt < DT; ++dt) o[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   uint16_t* pw = pt + 16 * wave * LDP;  // this wave's 16 rows of P
-  auto step2 = [&](int q, Tile& T) {
+  float rl[4];                          // 1 / l (0 for a row without keys)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) rl[i] = (l[i] > 0.0f) ? __builtin_amdgcn_rcpf(l[i]) : 0.0f;
+  auto step2 = [&](int q, Tile& T, auto edge) {
     lds_barrier();
     put(T, true);
     target(n + q + 1, T);
     lds_barrier();
     float s[NT][4];
-    scores(kb0 + q, s);
+    scores(kb0 + q, s, edge);
+    // p = bf16(exp(s - m) / l), 0 for a masked key or a row without keys
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float p = (s[nn][i] == -INFINITY || !(l[i] > 0.0f)) ? 0.0f : rbf(expf(s[nn][i] - m[i]) / l[i]);
+        float e;
+        if constexpr (decltype(edge)::value)
+          e = (s[nn][i] == -INFINITY) ? 0.0f : expf(s[nn][i] - m[i]);
+        else
+          e = expf(s[nn][i] - m[i]);
+        float p = e * rl[i];
+        if (near_bf16_midpoint(p)) p = e / l[i];
         pw[(4 * (lane >> 4) + i) * LDP + 16 * nn + fr] = f2bf(p);
       }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -310,7 +393,12 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       }
     }
   };
-  for (int q = 0; q < n; ++q) step2(q, tile);
+  {
+    int q = 0;
+    for (; q < n && !interior(kb0 + q); ++q) step2(q, tile, Edge{});
+    for (; q < n && interior(kb0 + q); ++q) step2(q, tile, Inner{});
+    for (; q < n; ++q) step2(q, tile, Edge{});
+  }
 
   // ---- ctx = bf16(O): row 4(l/16)+i of the wave, d = 16*dt + l%16
 #pragma unroll
@@ -370,11 +458,28 @@ int g4mi_prefill_attention(const uint16_t* q, const uint16_t* k_pages, const uin
   a.T = (int)T; a.NH = (int)NH; a.KV = (int)KV; a.page = (int)page_size; a.num_pages = (int)num_pages;
   a.max_pages = (int)max_pages; a.p0 = (int)p0; a.window = (int)window; a.softcap = softcap;
   hipStream_t st = as_stream(stream);
-#define G4MI_PF(DD, GG)                                                                                   \
-  if (D == DD && G == GG) {                                                                               \
-    constexpr int QP = 16 * pf_waves<DD>() / GG;                                                          \
-    hipLaunchKernelGGL((attn_prefill_kernel<DD, GG>), dim3((unsigned)((T + QP - 1) / QP), (unsigned)KV),  \
-                       dim3(64 * pf_waves<DD>()), 0, st, a);                                              \
+  // 1-D grid in the order of pf_block
+  auto grid_of = [&](int64_t qp) -> int64_t {
+    const int64_t nqb = (T + qp - 1) / qp;
+    a.nqb = (int)nqb;
+    if (8 % KV == 0) {
+      a.xmap = 1;
+      const int64_t per = 8 / KV;
+      return KV * ((nqb + per - 1) / per * per);
+    }
+    a.xmap = (KV % 8 == 0) ? 2 : 0;
+    return KV * nqb;
+  };
+#define G4MI_PF(DD, GG)                                                                                      \
+  if (D == DD && G == GG) {                                                                                  \
+    const int64_t nb = grid_of(16 * pf_waves<DD>() / GG);                                                    \
+    G4MI_REQUIRE(nb <= 2147483647, G4MI_EINVAL, "prefill_attention: %lld blocks", (long long)nb);            \
+    if (softcap > 0.0f)                                                                                      \
+      hipLaunchKernelGGL((attn_prefill_kernel<DD, GG, true>), dim3((unsigned)nb), dim3(64 * pf_waves<DD>()), \
+                         0, st, a);                                                                          \
+    else                                                                                                     \
+      hipLaunchKernelGGL((attn_prefill_kernel<DD, GG, false>), dim3((unsigned)nb), dim3(64 * pf_waves<DD>()),\
+                         0, st, a);                                                                          \
   }
   G4MI_PF(64, 1) G4MI_PF(64, 2) G4MI_PF(64, 4) G4MI_PF(64, 8)
   G4MI_PF(128, 1) G4MI_PF(128, 2) G4MI_PF(128, 4) G4MI_PF(128, 8)
