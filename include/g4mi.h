@@ -46,6 +46,13 @@ const char* g4mi_last_error_string(void);
  * layout of the cross-lane reductions every kernel uses. */
 int g4mi_selftest_lane_reductions(const float* in, float* out, double* out_d, int32_t waves, void* stream);
 
+/* Diagnostics (no counterpart in the reference): adds to *mismatches (device
+ * memory, zeroed by the caller) the number of floats x = -(bits lo + k),
+ * k < count, where the softmax's exp for x <= 0 differs from expf (below
+ * -103.97, where expf gives 0, a result of at most 2^-149 counts as equal).
+ * lo + count <= 0x7f800000 (finite floats). */
+int g4mi_selftest_exp_nonpositive(int64_t lo, int64_t count, uint64_t* mismatches, void* stream);
+
 /* Diagnostics (no counterpart in the reference; runs on the host, no GPU
  * needed): the MFMA GEMM's block -> tile map.  For a grid sized for max_tiles
  * row tiles x ncol_tiles column tiles with mtiles row tiles live (grouped

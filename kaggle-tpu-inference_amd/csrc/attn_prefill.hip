@@ -330,14 +330,20 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       if constexpr (decltype(edge)::value) {
         if (mn != -INFINITY) {
 #pragma unroll
-          for (int n = 0; n < NT; ++n) e += (s[n][i] == -INFINITY) ? 0.0f : expf(s[n][i] - mn);
+          for (int n = 0; n < NT; ++n) e += (s[n][i] == -INFINITY) ? 0.0f : exp_nonpos(s[n][i] - mn);
         }
       } else {
 #pragma unroll
-        for (int n = 0; n < NT; ++n) e += expf(s[n][i] - mn);
+        for (int n = 0; n < NT; ++n) e += exp_nonpos(s[n][i] - mn);
       }
       e = row16_sum(e);
-      l[i] = (m[i] == -INFINITY) ? e : l[i] * expf(m[i] - mn) + e;
+      // rescale the sum when the max moved (exp(0) = 1 leaves it as it is)
+      if (m[i] == -INFINITY)
+        l[i] = e;
+      else if (m[i] != mn)
+        l[i] = l[i] * exp_nonpos(m[i] - mn) + e;
+      else
+        l[i] += e;
       m[i] = mn;
     }
   };
@@ -372,9 +378,9 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       for (int i = 0; i < 4; ++i) {
         float e;
         if constexpr (decltype(edge)::value)
-          e = (s[nn][i] == -INFINITY) ? 0.0f : expf(s[nn][i] - m[i]);
+          e = (s[nn][i] == -INFINITY) ? 0.0f : exp_nonpos(s[nn][i] - m[i]);
         else
-          e = expf(s[nn][i] - m[i]);
+          e = exp_nonpos(s[nn][i] - m[i]);
         float p = e * rl[i];
         if (near_bf16_midpoint(p)) p = e / l[i];
         pw[(4 * (lane >> 4) + i) * LDP + 16 * nn + fr] = f2bf(p);

@@ -25,13 +25,29 @@ __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w <<
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf2f(uint16_t u) { return __uint_as_float((uint32_t)u << 16); }
 
-// f32 -> bf16, round to nearest even (NaN stays NaN).
 // f32 -> bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32; NaN stays
 // a quiet NaN).  One instruction converts a pair.
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint16_t f2bf(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 // Round an f32 to the nearest bf16 and return it as f32.
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// exp(x) for x <= 0 with expf's rounding on [-103.97, 0]: x * log2(e) as the
+// unevaluated sum hi + lo (hi = RN(x * L2E), lo = fma(x, L2E, -hi) +
+// x * L2E_LO, where L2E + L2E_LO = log2(e) to 48 bits), n = rne(hi), then
+// 2^(hi - n + lo) on the hardware exp2, scaled by 2^n.  expf's range checks
+// are left out: x <= 0 cannot overflow, and below -103.97 this returns at
+// most 2^-149 where expf returns 0 (the softmax callers round probabilities
+// to bf16, whose smallest value is 2^-133, and add exps to sums that hold
+// exp(0) = 1).  -inf gives NaN: callers select 0 for masked scores.
+__device__ __forceinline__ float exp_nonpos(float x) {
+#pragma clang fp contract(off)  // hi - n must not become fma(x, L2E, -n)
+  constexpr float kL2E = 0x1.715476p+0f, kL2ELo = 0x1.4ae0bep-26f;
+  const float hi = x * kL2E;
+  const float lo = __builtin_fmaf(x, kL2ELo, __builtin_fmaf(x, kL2E, -hi));
+  const float n = __builtin_rintf(hi);
+  return __builtin_amdgcn_ldexpf(__builtin_amdgcn_exp2f((hi - n) + lo), (int)n);
+}
 // f64 -> f32, kept opaque: the reference rounds f64 results to f32 first, and
 // without the barrier the compiler fuses f64 -> f32 -> bf16 into a single
 // f64 -> bf16 rounding, which differs in rare halfway cases.

@@ -24,7 +24,31 @@ __global__ void selftest_reduce_kernel(const float* __restrict__ in, float* __re
   }
 }
 
+// exp_nonpos(x) against expf(x) for x = -(the float with bits lo + k),
+// k < count: counts the x whose results differ, where below -103.97 (expf's
+// zero) a result of at most 2^-149 counts as equal.
+__global__ __launch_bounds__(256) void selftest_exp_kernel(uint32_t lo, uint32_t count,
+                                                           unsigned long long* __restrict__ mismatches) {
+  unsigned long long bad = 0;
+  for (uint32_t k = blockIdx.x * 256u + threadIdx.x; k < count; k += gridDim.x * 256u) {
+    const float x = -__uint_as_float(lo + k);
+    const float a = exp_nonpos(x), b = expf(x);
+    bad += !(__float_as_uint(a) == __float_as_uint(b) || (b == 0.0f && a <= 0x1p-149f));
+  }
+  if (bad != 0) atomicAdd(mismatches, bad);
+}
+
 }  // namespace g4mi
+
+extern "C" int g4mi_selftest_exp_nonpositive(int64_t lo, int64_t count, uint64_t* mismatches, void* stream) {
+  G4MI_REQUIRE(mismatches, G4MI_EINVAL, "selftest_exp_nonpositive: null pointer");
+  G4MI_REQUIRE(lo >= 0 && count >= 1 && lo + count <= 0x7f800000LL, G4MI_EINVAL,
+               "selftest_exp_nonpositive: bits [%lld, %lld) are not finite floats", (long long)lo,
+               (long long)(lo + count));
+  hipLaunchKernelGGL(g4mi::selftest_exp_kernel, dim3(4096), dim3(256), 0, g4mi::as_stream(stream), (uint32_t)lo,
+                     (uint32_t)count, (unsigned long long*)mismatches);
+  return g4mi::check_launch("selftest_exp_nonpositive");
+}
 
 extern "C" int g4mi_selftest_lane_reductions(const float* in, float* out, double* out_d, int32_t waves,
                                              void* stream) {

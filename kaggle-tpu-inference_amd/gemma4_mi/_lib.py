@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "g4mi_last_error_string": (ctypes.c_char_p, []),
     "g4mi_selftest_lane_reductions": (_int, [_p, _p, _p, _i32, _p]),
     "g4mi_selftest_tile_order": (_int, [_i32, _i32, _i32, _i32, _p, _i64]),
+    "g4mi_selftest_exp_nonpositive": (_int, [_i64, _i64, _p, _p]),
     "g4mi_fill_normal_bf16": (_int, [_p, _i64, _u64, _f64, _p]),
     "g4mi_philox4x32_10": (_int, [_p, _u64, _p, _i64, _p]),
     "g4mi_moe_router_scores": (_int, [_p, _p, _p, _p, _i64, _i64, _i64, _f32, _p, _p]),

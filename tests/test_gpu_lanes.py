@@ -34,3 +34,13 @@ def test_group_sums_match_host():
             # every lane of a group holds the bitwise-same total
             g = got[w, j].reshape(-1, width)
             assert np.all(g == g[:, :1]), f"f32 width {width} not uniform across the group"
+
+
+def test_softmax_exp_matches_expf_on_every_nonpositive_float():
+    """The prefill attention's exp for x <= 0 (exp_nonpos) rounds as expf does
+    for every float in [-104, 0]: all 1,120,927,745 of them."""
+    mism = torch.zeros(1, dtype=torch.int64, device="cuda:0")
+    count = 0x42D00000 + 1  # bits of -0.0 .. -104.0
+    _lib.call("g4mi_selftest_exp_nonpositive", 0, count, ops._ptr(mism), ops.stream_handle())
+    torch.cuda.synchronize()
+    assert int(mism.item()) == 0
