@@ -172,8 +172,12 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
   constexpr int LDK = D + 8;                // K row stride in LDS (elements)
   constexpr int LDV = KB + 8;               // V^T row stride
   constexpr int LDP = KB + 8;               // P row stride
-  __shared__ __align__(16) uint16_t kt[KB * LDK];
-  __shared__ __align__(16) uint16_t vt[D * LDV];
+  // From head_dim 256 the K/V tiles are double-buffered (the next step's rows
+  // go to the other buffer while this one is read: one barrier per step; 157
+  // KB of LDS at 256, 151 KB at 512, where one block per CU runs anyway).
+  constexpr int NBUF = (D >= 256) ? 2 : 1;
+  __shared__ __align__(16) uint16_t kt[NBUF][KB * LDK];
+  __shared__ __align__(16) uint16_t vt[NBUF][D * LDV];
   __shared__ __align__(16) uint16_t pt[ROWS * LDP];
   __shared__ int ptl[kPfPtl];
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -245,13 +249,15 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       }
     }
   };
-  auto put = [&](const Tile& T, bool with_v) {
+  auto put = [&](const Tile& T, bool with_v, int buf) {
+    uint16_t* kw = kt[buf];
+    uint16_t* vw = vt[buf];
     const u32x4 z = {0u, 0u, 0u, 0u};
     // K: lanes walk a key row (conflict-free 16-byte stores)
 #pragma unroll
     for (int i = 0; i < CPT; ++i) {
       const int c = tid + NTH * i, j = c / (D / 8), d0 = (c % (D / 8)) * 8;
-      *(u32x4*)(kt + j * LDK + d0) = T.ok ? T.k[i] : z;
+      *(u32x4*)(kw + j * LDK + d0) = T.ok ? T.k[i] : z;
     }
     // V transposed: lanes walk the keys of one 8-value column group, so the
     // 2-byte LDS stores of a wave land in consecutive halfwords
@@ -263,21 +269,22 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
         const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          vt[(d0 + 2 * e) * LDV + j] = (uint16_t)(w[e] & 0xffffu);
-          vt[(d0 + 2 * e + 1) * LDV + j] = (uint16_t)(w[e] >> 16);
+          vw[(d0 + 2 * e) * LDV + j] = (uint16_t)(w[e] & 0xffffu);
+          vw[(d0 + 2 * e + 1) * LDV + j] = (uint16_t)(w[e] >> 16);
         }
       }
     }
   };
   // scores of this wave's 16 rows x KB keys: s[n][i] = row 4(l/16)+i, key k0 + 16n + l%16
-  auto scores = [&](int kb, float (*s)[4], auto edge) {
+  auto scores = [&](int kb, float (*s)[4], auto edge, int buf) {
     const int k0 = kb * KB;
+    const uint16_t* kr = kt[buf];
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
-        const u32x4 b = *(const u32x4*)(kt + (16 * n + fr) * LDK + 32 * st + fk);
+        const u32x4 b = *(const u32x4*)(kr + (16 * n + fr) * LDK + 32 * st + fk);
         acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, qf[st]),
                                                       __builtin_bit_cast(bf16x8, b), acc, 0, 0, 0);
       }
@@ -312,13 +319,29 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
     m[i] = -INFINITY;
     l[i] = 0.0f;
   }
+  // Step g (pass 1: g = q, pass 2: g = n + q) reads buffer g % NBUF.  With
+  // two buffers, step g stores step g + 1's rows (requested one step earlier)
+  // into the other buffer, requests step g + 2's, and ends at the barrier
+  // that makes them visible (and frees buffer g % 2 for step g + 2); with one,
+  // the step stores its own rows between two barriers.
+  auto stage = [&](int g, Tile& T) {
+    if constexpr (NBUF == 2) {
+      if (g + 1 < 2 * n) put(T, g + 1 >= n, (g + 1) & 1);
+      target(g + 2, T);
+    } else {
+      lds_barrier();
+      put(T, g >= n, 0);
+      target(g + 1, T);
+      lds_barrier();
+    }
+  };
+  auto end_step = [&]() {
+    if constexpr (NBUF == 2) lds_barrier();
+  };
   auto step1 = [&](int q, Tile& T, auto edge) {
-    lds_barrier();
-    put(T, false);
-    target(q + 1, T);
-    lds_barrier();
+    stage(q, T);
     float s[NT][4];
-    scores(kb0 + q, s, edge);
+    scores(kb0 + q, s, edge, q % NBUF);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float bm = s[0][i];
@@ -346,10 +369,16 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
         l[i] += e;
       m[i] = mn;
     }
+    end_step();
   };
   Tile tile;
   lds_barrier();  // ptl
   target(0, tile);
+  if constexpr (NBUF == 2) {
+    put(tile, false, 0);  // step 0 is a pass-1 step (n >= 1)
+    target(1, tile);
+    lds_barrier();
+  }
   {
     int q = 0;
     for (; q < n && !interior(kb0 + q); ++q) step1(q, tile, Edge{});
@@ -365,12 +394,10 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
 #pragma unroll
   for (int i = 0; i < 4; ++i) rl[i] = (l[i] > 0.0f) ? __builtin_amdgcn_rcpf(l[i]) : 0.0f;
   auto step2 = [&](int q, Tile& T, auto edge) {
-    lds_barrier();
-    put(T, true);
-    target(n + q + 1, T);
-    lds_barrier();
+    const int g = n + q, buf = g % NBUF;
+    stage(g, T);
     float s[NT][4];
-    scores(kb0 + q, s, edge);
+    scores(kb0 + q, s, edge, buf);
     // p = bf16(exp(s - m) / l), 0 for a masked key or a row without keys
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn)
@@ -393,11 +420,12 @@ __global__ __launch_bounds__(64 * pf_waves<D>()) void attn_prefill_kernel(PfAttn
       const u32x4 pa = *(const u32x4*)(pw + fr * LDP + 32 * st + fk);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const u32x4 vb = *(const u32x4*)(vt + (16 * dt + fr) * LDV + 32 * st + fk);
+        const u32x4 vb = *(const u32x4*)(vt[buf] + (16 * dt + fr) * LDV + 32 * st + fk);
         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, pa),
                                                         __builtin_bit_cast(bf16x8, vb), o[dt], 0, 0, 0);
       }
     }
+    end_step();
   };
   {
     int q = 0;
