@@ -1194,9 +1194,19 @@ __device__ __forceinline__ void attn_local_pv(const AttnDims& a, const Range& R,
   const int nst = (len + PPB - 1) / PPB;
   constexpr int PG = kLocalPage;
   const PtRow<DPT> pt_row = pt_row_of<DPT>(a, page_table, 0);
+  // the attended range spans at most kLocalLen / PG + 1 pages; with a page
+  // table their entries are staged in LDS first (one round trip; a table
+  // load per step, under the step's branch, waited for each before its V row)
+  constexpr int NPG = kLocalLen / PG + 1;
+  __shared__ int ptv[NPG];
+  const int pfirst = R.lo / PG;
   // the new V row's raw values, then the V slice at every attended position
   float vx[PL], dummy[PL];
   if (append && wave < NW) load_slice<PL>((v_raw != nullptr ? v_raw : k_raw) + (size_t)kv * D + lane * PL, vx);
+  if constexpr (!DPT) {
+    if (tid < NPG) ptv[tid] = pt_row[min(pfirst + tid, a.max_pages - 1)];
+    __syncthreads();
+  }
   // V steps in chunks of CH (a block-uniform branch per chunk, none inside:
   // a chunk's LDS reads are then issued together); the rows of steps past
   // the range are not requested and read as zero
@@ -1205,6 +1215,13 @@ __device__ __forceinline__ void attn_local_pv(const AttnDims& a, const Range& R,
   u32x4 vv[NST];
   bool okv[NST];
   if (wave < NW) {
+    int pgv[NST];  // every step's page, before the first V row is requested
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int p = R.lo + min(st * PPB + wave * PPW + slot, len - 1);
+      if constexpr (DPT) pgv[st] = pt_row[p / PG];
+      else pgv[st] = ptv[p / PG - pfirst];
+    }
 #pragma unroll
     for (int st = 0; st < NST; ++st) {
       const int j = st * PPB + wave * PPW + slot;
@@ -1212,7 +1229,7 @@ __device__ __forceinline__ void attn_local_pv(const AttnDims& a, const Range& R,
       vv[st] = u32x4{0u, 0u, 0u, 0u};
       if (st < nst) {  // block-uniform: no loads for the steps past the range
         const int p = R.lo + min(j, len - 1);
-        const int pg = pt_row[p / PG];
+        const int pg = pgv[st];
         const bool valid = pg >= 0 && pg < a.num_pages;
         const long long off = ((((long long)(valid ? pg : 0) * a.KV + kv) * PG) + (p % PG)) * (long long)D;
         vv[st] = ld16((const u32x4*)(v_pages + off + d0));
