@@ -142,6 +142,135 @@ __global__ __launch_bounds__(1024) void moe_sort_kernel(const int32_t* __restric
   }
 }
 
+// The same sort for many entries, over several blocks in two launches (one
+// block serialises its LDS atomics: 16,384 entries on 128 counters).  Block b
+// of either launch owns entries [b * per, (b + 1) * per), per = kSortBlk *
+// ipt.
+//   moe_count_kernel: the block's per-expert counts -> hist[b][e];
+//   moe_place_kernel: every block reads all counts, scans them (expert
+//     offsets, this block's start within each expert, the tile offsets;
+//     block 0 writes the tile list) and places its own entries, each at its
+//     expert's offset + this block's start + its rank among the block's
+//     entries of that expert.
+// Rows of an expert may come in any order (each output row of the grouped
+// GEMMs depends on its own row only, and the combine reads them through
+// slot_pos), as in moe_sort_kernel, whose ranks come from LDS atomics too.
+constexpr int kSortBlk = 1024;        // threads per block
+constexpr int kSortMaxBlocks = 64;    // hist holds kSortMaxBlocks * kMaxExperts counts
+constexpr int kSortIptMax = 16;       // entries per thread at most
+
+__global__ __launch_bounds__(kSortBlk) void moe_count_kernel(const int32_t* __restrict__ top_i, int total, int ipt,
+                                                             int E, int32_t* __restrict__ hist) {
+  __shared__ int cnt[kMaxExperts];
+  const int tid = threadIdx.x, per = kSortBlk * ipt, i0 = (int)blockIdx.x * per;
+  for (int e = tid; e < E; e += kSortBlk) cnt[e] = 0;
+  __syncthreads();
+  for (int u = 0; u < ipt; ++u) {
+    const int i = i0 + u * kSortBlk + tid;
+    const int e = (i < total) ? top_i[i] : -1;
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += kSortBlk) hist[(size_t)blockIdx.x * E + e] = cnt[e];
+}
+
+__global__ __launch_bounds__(kSortBlk) void moe_place_kernel(const int32_t* __restrict__ top_i,
+                                                             const float* __restrict__ top_w, int total, int ipt,
+                                                             int K, int E, const int32_t* __restrict__ hist,
+                                                             int32_t* __restrict__ a_rows,
+                                                             float* __restrict__ w_sorted,
+                                                             int32_t* __restrict__ slot_pos,
+                                                             int32_t* __restrict__ tiles,
+                                                             int32_t* __restrict__ ntiles, int tile_rows) {
+  __shared__ int cnt[kMaxExperts], off[kMaxExperts], cur[kMaxExperts], toff[kMaxExperts];
+  __shared__ int hl[kSortMaxBlocks * kMaxExperts];
+  const int tid = threadIdx.x, nb = (int)gridDim.x, b = (int)blockIdx.x;
+  const int per = kSortBlk * ipt, i0 = b * per;
+  // this block's entries and every block's counts, all requested at once
+  int ev[kSortIptMax];
+  float wv[kSortIptMax];
+#pragma unroll
+  for (int u = 0; u < kSortIptMax; ++u) {
+    const int i = i0 + u * kSortBlk + tid;
+    ev[u] = (u < ipt && i < total) ? top_i[i] : -1;
+    wv[u] = (u < ipt && i < total) ? top_w[i] : 0.0f;
+  }
+  for (int j = tid; j < nb * E; j += kSortBlk) hl[j] = hist[j];
+  __syncthreads();
+  // per expert: the total count, and the entries of the blocks before this one
+  for (int e = tid; e < E; e += kSortBlk) {
+    int t = 0, before = 0;
+    for (int q = 0; q < nb; ++q) {
+      const int c = hl[q * E + e];
+      before += (q < b) ? c : 0;
+      t += c;
+    }
+    cnt[e] = t;
+    cur[e] = before;
+  }
+  __syncthreads();
+  // expert offsets and tile offsets: an exclusive scan over the experts in
+  // one wave (lane l holds experts 4l .. 4l + 3, E <= 256)
+  if (tid < 64) {
+    int c[4], t[4], sc = 0, stl = 0;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * tid + q;
+      c[q] = (e < E) ? cnt[e] : 0;
+      t[q] = (c[q] + tile_rows - 1) / tile_rows;
+      sc += c[q];
+      stl += t[q];
+    }
+    int ic = sc, it = stl;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int y = __shfl_up(ic, d, 64), z = __shfl_up(it, d, 64);
+      if (tid >= d) {
+        ic += y;
+        it += z;
+      }
+    }
+    int o = ic - sc, to = it - stl;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * tid + q;
+      if (e < E) {
+        off[e] = o;
+        toff[e] = to;
+      }
+      o += c[q];
+      to += t[q];
+    }
+    if (tid == 63 && b == 0) ntiles[0] = it;
+  }
+  __syncthreads();
+  if (b == 0) {
+    for (int e = tid; e < E; e += kSortBlk) {
+      const int nt = (cnt[e] + tile_rows - 1) / tile_rows;
+      for (int j = 0; j < nt; ++j) {
+        int32_t* t = tiles + 3 * (toff[e] + j);
+        t[0] = e;
+        t[1] = off[e] + j * tile_rows;
+        t[2] = min(off[e] + (j + 1) * tile_rows, off[e] + cnt[e]);
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kSortIptMax; ++u) {
+    const int i = i0 + u * kSortBlk + tid;
+    if (u >= ipt || i >= total) continue;
+    const int e = ev[u];
+    if (e >= 0 && e < E) {
+      const int p = off[e] + atomicAdd(&cur[e], 1);
+      a_rows[p] = i / K;
+      w_sorted[p] = wv[u];
+      slot_pos[i] = p;
+    } else {
+      slot_pos[i] = -1;
+    }
+  }
+}
+
 // out[t, h] = bf16(sum over s < K, in order, of part[slot_pos[t*K + s], h]) (f32),
 // or with `running` the decode combine: a bf16 running sum of bf16(part) in
 // slot order (model.py:289-293)
@@ -446,7 +575,7 @@ static int moe_prefill_tile_rows(int64_t pairs, int64_t E) {
 }
 
 struct MoePrefillWs {
-  int32_t *a_rows, *slot_pos, *tiles, *ntiles;
+  int32_t *a_rows, *slot_pos, *tiles, *ntiles, *hist;
   float *w_sorted, *part;
   uint16_t* act;
 };
@@ -460,9 +589,28 @@ static MoePrefillWs moe_prefill_ws(void* ws, int64_t n, int64_t K, int64_t E, in
   w.tiles = (int32_t*)p; p += al256(max_tiles * 12);
   w.ntiles = (int32_t*)p; p += 256;
   w.w_sorted = (float*)p; p += al256(nk * 4);
+  w.hist = (int32_t*)p; p += al256((int64_t)kSortMaxBlocks * kMaxExperts * 4);
   w.act = (uint16_t*)p; p += al256(nk * F * 2);
   w.part = (float*)p;
   return w;
+}
+
+// Groups the (token, slot) entries by expert and lists the expert tiles: one
+// block up to kSortIpt entries per thread, else the two-launch form.
+static void launch_moe_sort(const int32_t* top_i, const float* top_w, int n, int K, int E, const MoePrefillWs& w,
+                            int tile_rows, hipStream_t st) {
+  const int total = n * K;
+  const int ipt = (total + kSortBlk * kSortMaxBlocks - 1) / (kSortBlk * kSortMaxBlocks);
+  const char* one = getenv("G4MI_MOE_SORT_ONE_BLOCK");
+  if (total <= 4 * kSortBlk || ipt > kSortIptMax || (one != nullptr && atoi(one) != 0)) {
+    hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, n, K, E, w.a_rows, w.w_sorted,
+                       w.slot_pos, w.tiles, w.ntiles, tile_rows);
+    return;
+  }
+  const int nb = (total + kSortBlk * ipt - 1) / (kSortBlk * ipt);  // <= kSortMaxBlocks
+  hipLaunchKernelGGL(moe_count_kernel, dim3((unsigned)nb), dim3(kSortBlk), 0, st, top_i, total, ipt, E, w.hist);
+  hipLaunchKernelGGL(moe_place_kernel, dim3((unsigned)nb), dim3(kSortBlk), 0, st, top_i, top_w, total, ipt, K, E,
+                     w.hist, w.a_rows, w.w_sorted, w.slot_pos, w.tiles, w.ntiles, tile_rows);
 }
 
 }  // namespace g4mi
@@ -473,7 +621,8 @@ extern "C" {
 
 int64_t g4mi_moe_prefill_workspace_bytes(int64_t n, int64_t K, int64_t E, int64_t F, int64_t H) {
   const int64_t nk = n * K, max_tiles = (nk + kTileRows - 1) / kTileRows + E;
-  return 3 * al256(nk * 4) + al256(max_tiles * 12) + 256 + al256(nk * F * 2) + al256(nk * H * 4);
+  return 3 * al256(nk * 4) + al256(max_tiles * 12) + 256 + al256((int64_t)kSortMaxBlocks * kMaxExperts * 4) +
+         al256(nk * F * 2) + al256(nk * H * 4);
 }
 
 int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_i, const uint16_t* gate_up,
@@ -489,8 +638,7 @@ int g4mi_moe_prefill(const uint16_t* xn, const float* top_w, const int32_t* top_
   const MoePrefillWs w = moe_prefill_ws(ws, n, K, E, F, H);
   const int tile_rows = moe_prefill_tile_rows(n * K, E);
   const int64_t max_tiles = (n * K + tile_rows - 1) / tile_rows + E;
-  hipLaunchKernelGGL(moe_sort_kernel, dim3(1), dim3(1024), 0, st, top_i, top_w, (int)n, (int)K, (int)E, w.a_rows,
-                     w.w_sorted, w.slot_pos, w.tiles, w.ntiles, tile_rows);
+  launch_moe_sort(top_i, top_w, (int)n, (int)K, (int)E, w, tile_rows, st);
   int rc = check_launch("moe_prefill sort");
   if (rc) return rc;
   // gate/up: gathered token rows x the expert's (gate, up) rows -> act [n*K, F]

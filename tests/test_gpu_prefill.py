@@ -306,6 +306,28 @@ def test_moe_prefill_192_row_tiles_equal_128(monkeypatch, which, n):
     assert bool(torch.isfinite(outs["192"].float()).all())
 
 
+@pytest.mark.parametrize("n", [513, 2048, 20000])
+def test_moe_sort_blocks_equal_one_block(monkeypatch, n):
+    """The expert grouping over several blocks (more than 4,096 (token, slot)
+    entries; 20,000 tokens of the tiny model's 4 slots take 2 entries per
+    thread) gives what the one-block sort gives, bit for bit, also with expert
+    indices outside the table (they contribute nothing)."""
+    cfg = tiny_parity_config()
+    g = {k: v.to(DEV) for k, v in _moe_params(cfg, 60).items()}
+    x = _rand((n, cfg.hidden_size), 61).to(DEV)
+    top_w, top_i = ops.moe_router_topk(x, g["router.scale"], g["router.proj"], g["router.per_expert_scale"],
+                                       cfg.top_k_experts, cfg.rms_norm_eps)
+    top_i[::7, 1] = -1
+    top_i[::11, 2] = cfg.num_experts + 3
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("G4MI_MOE_SORT_ONE_BLOCK", flag)
+        outs[flag] = ops.moe_prefill(x, top_w, top_i, g["experts.gate_up_proj"], g["experts.down_proj"]).clone()
+    torch.cuda.synchronize()
+    assert torch.equal(outs["0"].view(torch.int16), outs["1"].view(torch.int16))
+    assert bool(torch.isfinite(outs["0"].float()).all())
+
+
 @pytest.mark.parametrize("which,n", [("tiny", 37), ("tiny", 512), ("26b", 300)])
 def test_rows_tail_experts_equals_combine_then_tail(which, n):
     """The layer tail with the MoE combine inside it (moe_prefill without its
