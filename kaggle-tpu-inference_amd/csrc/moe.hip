@@ -405,6 +405,109 @@ __global__ __launch_bounds__(64 * kDownWaves) void moe_down_kernel(
   if (lane == 0 && h < H) out[(size_t)n * H + h] = f2bf(run);
 }
 
+// Several tokens (2 <= N <= 8, K <= 8), routing given: one wave per output
+// row h for all N tokens, so the row h of an expert that several tokens chose
+// is read once (moe_down_kernel reads it once per token, the repeats coming
+// from the MALL).  Each wave lists the distinct valid experts of the N * K
+// (token, slot) pairs in order of first occurrence, with the mask of pairs
+// that chose each; in pass r lane group g reads the row of distinct expert
+// 8r + g (the next pass's rows are requested before this pass's products)
+// and dots it with the activations of each of its pairs exactly as
+// moe_down_kernel's lane group for that pair does (the same chunks per lane
+// in the same order, the same 8-lane sum), into the wave's part of that pair;
+// lane n then combines token n's parts in slot order.  A pair whose expert is
+// outside [0, E) keeps part 0, as there.  Bit-identical to moe_down_kernel.
+constexpr int kDownShMaxN = 8, kDownShMaxK = 8;
+constexpr int kDownShPairs = kDownShMaxN * kDownShMaxK;
+
+template <int IT>
+__global__ __launch_bounds__(64 * kDownWaves) void moe_down_shared_kernel(
+    const uint16_t* __restrict__ act, const uint16_t* __restrict__ down, const int32_t* __restrict__ top_i, int N,
+    int H, int E, int K, int bf16_running, uint16_t* __restrict__ out) {
+  constexpr int F = IT * 64;
+  constexpr int NT = 64 * kDownWaves;
+  constexpr int APT = (kDownShPairs * (F / 8) + NT - 1) / NT;  // activation chunks per thread, at most
+  __shared__ u32x4 act_lds[kDownShPairs * (F / 8)];
+  __shared__ int dexp[kDownWaves][kDownShPairs];                  // distinct expert d of each wave
+  __shared__ unsigned long long dmask[kDownWaves][kDownShPairs];  // the pairs that chose it
+  __shared__ float parts[kDownWaves][kDownShPairs];
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 3, l8 = lane & 7, wave = wave_id();
+  const int h = blockIdx.x * kDownWaves + wave;
+  const int hc = min(h, H - 1);
+  const int NK = N * K, mch = NK * (F / 8);
+  // every pair's expert (one per lane), then this thread's activation chunks
+  const int pe_raw = top_i[min(lane, NK - 1)];
+  u32x4 av[APT];
+#pragma unroll
+  for (int j = 0; j < APT; ++j) av[j] = ld16((const u32x4*)act + min(tid + NT * j, mch - 1));
+  const int pe = (lane < NK && pe_raw >= 0 && pe_raw < E) ? pe_raw : -1;
+  parts[wave][lane] = 0.0f;
+  // distinct experts in order of first occurrence; lane group g keeps the
+  // expert of its first pass in a register
+  unsigned long long rem = __ballot(pe >= 0);
+  int nd = 0, e0 = 0;
+  while (rem != 0ull) {
+    const int q0 = (int)__builtin_ctzll(rem);
+    const int v = __builtin_amdgcn_readlane(pe, q0);
+    const unsigned long long m = __ballot(pe == v);
+    if (lane == 0) {
+      dexp[wave][nd] = v;
+      dmask[wave][nd] = m;
+    }
+    if (nd == g) e0 = v;
+    rem &= ~m;
+    ++nd;
+  }
+  const int npass = (nd + 7) / 8;
+  auto load_rows = [&](int e, u32x4 (&w)[IT]) __attribute__((always_inline)) {
+    const u32x4* row = (const u32x4*)(down + ((size_t)e * H + hc) * F);
+#pragma unroll
+    for (int i = 0; i < IT; ++i) w[i] = ld_stream(row + l8 + 8 * i);
+  };
+  u32x4 wa[IT], wb[IT];
+  load_rows(e0, wa);
+#pragma unroll
+  for (int j = 0; j < APT; ++j)
+    if (tid + NT * j < mch) act_lds[tid + NT * j] = av[j];
+  lds_barrier();
+  // pass r: rows in `cur`; the next pass's rows requested into `nxt` first
+  auto pass = [&](int r, u32x4 (&cur)[IT], u32x4 (&nxt)[IT]) __attribute__((always_inline)) {
+    if (r + 1 < npass) {
+      const int dn = min(8 * (r + 1) + g, nd - 1);
+      load_rows(dexp[wave][dn], nxt);
+    }
+    const int d = 8 * r + g;
+    unsigned long long pm = (d < nd) ? dmask[wave][d] : 0ull;
+    while (pm != 0ull) {  // uniform per lane group
+      const int q = (int)__builtin_ctzll(pm);
+      pm &= pm - 1ull;
+      const u32x4* am = act_lds + q * (F / 8);
+      float part = 0.0f;
+#pragma unroll
+      for (int i = 0; i < IT; ++i) part = dot8(cur[i], am[l8 + 8 * i], part);
+      part = group_sum<8>(part);
+      if (l8 == 0) parts[wave][q] = part;
+    }
+  };
+  for (int r = 0; r < npass; r += 2) {
+    pass(r, wa, wb);
+    if (r + 1 < npass) pass(r + 1, wb, wa);
+  }
+  if (lane < N && h < H) {
+    float run = 0.0f;
+    for (int s = 0; s < K; ++s) {
+      const float pq = parts[wave][lane * K + s];
+      if (bf16_running) {
+        const float b = rbf(pq);
+        run = (s == 0) ? b : rbf(run + b);
+      } else {
+        run = (s == 0) ? pq : run + pq;
+      }
+    }
+    out[(size_t)lane * H + h] = f2bf(run);
+  }
+}
+
 // ------------------------------------------------------------------ launchers
 static float bf16_inv_sqrt(int64_t H) {
   // bf16(H^-0.5): the constant the reference multiplies in bf16 (model.py:226)
@@ -586,8 +689,33 @@ static void launch_gateup(int it, const uint16_t* x, const uint16_t* gu, const f
   }
 }
 
+// The shared-row down at 8 tokens of at most 8 slots each: 26B shapes,
+// uniform routing (50.9 of 64 experts distinct), 37.9 against 40.1 us for the
+// token rows; at 2 and 4 tokens (15.8 and 28.5 distinct) the token rows,
+// whose repeats come from the MALL, are faster (12.0 / 20.9 against
+// 13.5 / 22.6 us), and at 6 as well.  G4MI_MOE_DOWN_SHARED=0 keeps the token
+// rows at 8, =1 forces the shared rows from 2 tokens.
+static bool down_shared(int N, int K) {
+  if (N < 2 || N > kDownShMaxN || K > kDownShMaxK) return false;
+  const char* e = getenv("G4MI_MOE_DOWN_SHARED");
+  if (e != nullptr) return atoi(e) != 0;
+  return N == kDownShMaxN;
+}
+
 static void launch_down(int it, const uint16_t* act, const uint16_t* dn, const int32_t* ti, int N, int H, int E,
                         int K, int running, uint16_t* out, hipStream_t st) {
+  if (down_shared(N, K)) {
+    const dim3 sgrid((unsigned)((H + kDownWaves - 1) / kDownWaves));
+    switch (it) {
+#define G4MI_CASE(I)                                                                                          \
+  case I:                                                                                                     \
+    hipLaunchKernelGGL(moe_down_shared_kernel<I>, sgrid, dim3(64 * kDownWaves), 0, st, act, dn, ti, N, H, E, K, \
+                       running, out);                                                                         \
+    return;
+      G4MI_IT_CASES(G4MI_CASE)
+#undef G4MI_CASE
+    }
+  }
   dim3 grid((unsigned)((H + kDownWaves - 1) / kDownWaves), (unsigned)N);
   const size_t lds = (size_t)K * it * 64 * 2;  // K * F bf16 activations
   switch (it) {

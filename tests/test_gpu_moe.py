@@ -162,6 +162,33 @@ def test_gateup_shared_experts_read_once_bit_identical(c2, n, pool):
     assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (n, pool)
 
 
+@pytest.mark.parametrize("n,pool", [(2, 8), (3, 128), (4, 12), (8, 8), (8, 20), (8, 128)])
+def test_down_shared_rows_bit_identical(c2, n, pool, monkeypatch):
+    """From 2 to 8 tokens the down kernel reads an expert's row h once for all
+    the tokens that chose it (one wave per row h for every token); its output
+    must equal the one-token-row-per-block kernel (G4MI_MOE_DOWN_SHARED=0) bit
+    for bit, for both combines, also with expert indices outside the table."""
+    cfg, g, _ = c2
+    k = cfg.top_k_experts
+    x = _gen((n, cfg.hidden_size), 5, f"xd.n{n}.{pool}", 1.0)
+    rng = np.random.default_rng(2000 + 10 * n + pool)
+    ti = torch.tensor(np.stack([rng.permutation(pool)[:k] for _ in range(n)]), dtype=torch.int32, device=DEV)
+    tw = torch.tensor(rng.uniform(0.01, 0.3, size=(n, k)), dtype=torch.float32, device=DEV)
+    act = ops.moe_gateup(x, g["experts.gate_up_proj"], tw, ti)
+    dn = g["experts.down_proj"]
+    ti_bad = ti.clone()
+    ti_bad[0, 2] = -1
+    ti_bad[n - 1, 6] = cfg.num_experts + 3
+    for routing in (ti, ti_bad):
+        for combine in ("bf16_running", "f32"):
+            monkeypatch.setenv("G4MI_MOE_DOWN_SHARED", "0")
+            ref = ops.moe_down(act, dn, routing, combine)
+            monkeypatch.setenv("G4MI_MOE_DOWN_SHARED", "1")
+            got = ops.moe_down(act, dn, routing, combine)
+            torch.cuda.synchronize()
+            assert torch.equal(got.view(torch.int16), ref.view(torch.int16)), (n, pool, combine)
+
+
 @pytest.mark.parametrize("n", [1, 4])
 def test_expert_indices_outside_the_table_contribute_nothing(c2, n):
     """A routed expert index outside [0, E) (-1, E + 7) is skipped: the
