@@ -68,6 +68,17 @@ struct GemmArgs {
 
 constexpr int kBK = 64;  // K per pipeline stage
 
+// Waves per block of the 16-column skinny products (gemm_skinny_kernel with
+// NTL = 1): 8 by default, so that each wave's eighth of K (up to 12 or 16
+// steps of A and B) is one request that fits its registers; with 4 waves a
+// quarter of the 2,816-wide gated product (22 steps of A, gate and up) needs
+// more than 256 VGPRs and the compiler splits the request.  At 8 rows the
+// batched decode step 6.40 -> 6.34 ms.  G4MI_SKINNY_WAVES=4 keeps 4 waves.
+static bool skinny_8_waves() {
+  const char* e = getenv("G4MI_SKINNY_WAVES");
+  return e == nullptr || atoi(e) != 4;
+}
+
 // ---- tile GEMM (M > 16 rows)
 // A block computes a BM x BN tile (BM, BN in {64, 128, ...}) with 4 waves
 // (2 x 2), each a (BM/2) x (BN/2) patch of 16 x 16 MFMA accumulators.  K
@@ -431,13 +442,14 @@ __global__ __launch_bounds__(256, OCC) void gemm_kernel(GemmArgs g) {
 
 // ---- skinny GEMM (M <= 16 rows: batched decode, short prompts)
 // A block owns 16*NTL output columns (B rows; with the gated epilogue the
-// gate and the up rows) for all M <= 16 A rows; its 4 waves split K into
-// quarters.  Per k-step a wave loads one A fragment and multiplies it into
-// NTL 16x16 MFMA chains (A rows beyond M are clamped duplicates and are not
-// stored).  The wave partials meet in LDS and are summed in wave order, so
-// there is no split-K reduce kernel.  Each wave requests CHK k-steps of A and
-// B -- its whole K quarter when that fits, so one round trip -- before the
-// first multiply.  NTL = 4 amortises the A fragments over 64 columns when N
+// gate and the up rows) for all M <= 16 A rows; its NWV waves (8 for the
+// 16-column products, 4 for the 64-column ones) split K into NWV ranges.
+// Per k-step a wave loads one A fragment and multiplies it into NTL 16x16
+// MFMA chains (A rows beyond M are clamped duplicates and are not stored).
+// The wave partials meet in LDS and are summed in wave order, so there is no
+// split-K reduce kernel.  Each wave requests CHK k-steps of A and B -- its
+// whole K range when that fits, so one round trip -- before the first
+// multiply.  NTL = 4 amortises the A fragments over 64 columns when N
 // is large (the lm_head); NTL = 1 keeps ceil(N/16) blocks for the layer
 // projections.  With column segments (NTL = 1) a block's 16 columns lie in
 // one segment, whose B rows and C it uses.
@@ -632,8 +644,12 @@ int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const
       // a wave's whole K quarter in one request when it is at most 24 (or 32) steps
       const dim3 grid((unsigned)((N + 15) / 16));
       const bool wide = (K / 32 + 3) / 4 > 24;
+      const bool w8 = skinny_8_waves();
+      const bool wide8 = (K / 32 + 7) / 8 > 12;
 #define G4MI_SKINNY(E)                                                                          \
-  if (wide) hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 32>), grid, dim3(256), 0, st, g);      \
+  if (w8 && wide8) hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 16, 8>), grid, dim3(512), 0, st, g); \
+  else if (w8) hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 12, 8>), grid, dim3(512), 0, st, g); \
+  else if (wide) hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 32>), grid, dim3(256), 0, st, g);      \
   else hipLaunchKernelGGL((gemm_skinny_kernel<E, 1, 24>), grid, dim3(256), 0, st, g);
       if (epilogue == kEpGated) { G4MI_SKINNY(kEpGated) }
       else if (epilogue == kEpF32) { G4MI_SKINNY(kEpF32) }
@@ -707,8 +723,14 @@ int g4mi_gemm_bf16_segments(const uint16_t* a, int64_t lda, int64_t M, int64_t K
   g.b = g.seg_b[0]; g.c = g.seg_c[0]; g.N = (int)end; g.ldc = n[0];
   const dim3 grid((unsigned)(end / 16));
   hipStream_t st = as_stream(stream);
-  if ((K / 32 + 3) / 4 > 24) hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 32>), grid, dim3(256), 0, st, g);
-  else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 24>), grid, dim3(256), 0, st, g);
+  if (skinny_8_waves()) {
+    if ((K / 32 + 7) / 8 > 12) hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 16, 8>), grid, dim3(512), 0, st, g);
+    else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 12, 8>), grid, dim3(512), 0, st, g);
+  } else if ((K / 32 + 3) / 4 > 24) {
+    hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 32>), grid, dim3(256), 0, st, g);
+  } else {
+    hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 1, 24>), grid, dim3(256), 0, st, g);
+  }
   return check_launch("gemm_bf16_segments");
 }
 
