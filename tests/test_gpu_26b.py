@@ -426,9 +426,11 @@ def test_batch_decode_at_8k_contexts(m26):
     prefilled to 8,150-8,190 tokens (staggered, each through the batched
     prefill into pages handed out by one PagePool), then 4 batched greedy
     steps (model.py:402-408 masks per position; engine.py:71-83).  At B = 8
-    and these lengths every layer runs the long-range attention path (8-wave
-    scores and P.V kernels and the split reduction launch; asserted from the
-    split counts).  Each row's logits at every step against the batch-1
+    and these lengths the full layers run the long-range attention path
+    (8-wave scores and P.V kernels and the split reduction launch) and the
+    sliding layers 64-position splits (4-wave kernels, the last block of a
+    head reducing the splits in order); asserted from the split counts.
+    Each row's logits at every step against the batch-1
     decode runner fed the same tokens, and rows 0 and 7 at the last step
     against the oracle run on that row's K/V cache rows copied to the host."""
     cfg, params, cpu, po = m26
@@ -437,9 +439,11 @@ def test_batch_decode_at_8k_contexts(m26):
     prompts = [np.random.default_rng(60 + b).integers(0, cfg.vocab_size, size=n).tolist()
                for b, n in enumerate(lens)]
     eng = BatchEngine(cfg, params, batch=B, max_len=max_len, device=DEV)
-    # both layer kinds take the 8-wave path: span > 64 positions per split
-    for lt, span in ((SLIDING, min(cfg.sliding_window, max_len)), (FULL, max_len)):
-        assert span > 64 * eng.runner.splits[lt], (lt, eng.runner.splits[lt])
+    # full layers: the 8-wave path (more than 64 positions per split);
+    # sliding layers: 64-position splits
+    assert max_len > 64 * eng.runner.splits[FULL], eng.runner.splits[FULL]
+    window = min(cfg.sliding_window, max_len)
+    assert eng.runner.splits[SLIDING] == (window + 63) // 64, eng.runner.splits[SLIDING]
     firsts = [eng.add(b, p) for b, p in enumerate(prompts)]
     # the pool mapped each sequence's pages out of one shared pool, in add order
     owned = [set(o) for o in eng.pool.owned]
