@@ -641,7 +641,8 @@ int gemm_bf16_tiles(const uint16_t* a, int64_t lda, const int32_t* a_rows, const
       if (epilogue == kEpF32) hipLaunchKernelGGL((gemm_skinny_kernel<kEpF32, 4, 8>), grid, dim3(256), 0, st, g);
       else hipLaunchKernelGGL((gemm_skinny_kernel<kEpBf16, 4, 8>), grid, dim3(256), 0, st, g);
     } else {
-      // a wave's whole K quarter in one request when it is at most 24 (or 32) steps
+      // a wave's whole K range in one request: with 8 waves an eighth of at
+      // most 12 (or 16) steps, with 4 a quarter of at most 24 (or 32)
       const dim3 grid((unsigned)((N + 15) / 16));
       const bool wide = (K / 32 + 3) / 4 > 24;
       const bool w8 = skinny_8_waves();
